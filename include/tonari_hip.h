@@ -1,0 +1,114 @@
+/*
+ * tonari_hip.h - C ABI of the MI355X (gfx950) neighbor-list library
+ * (libtonari_hip.so).
+ *
+ * This ABI replaces the reference's pybind11 CUDA provider entry point
+ *   _torch_cuda.neighbor_list(positions, batch_ptr, cell, pbc, cutoff,
+ *                             half_list, include_self, algorithm, sorted)
+ *       -> [P (E,2) int64, S (E,3) int32]
+ * (songfeitong/tonari csrc/torch/bindings_cuda.cpp:59-228, registered at
+ * :233-238; internal launchers declared in csrc/torch/neighbors_cuda.h:9-38,
+ * called from src/tonari/_torch_frontend.py:138-145).
+ *
+ * The single pybind call is split in two so that the caller owns every device
+ * allocation (the library never calls hipMalloc):
+ *   1. tnr_workspace_size()  - bytes of device scratch for this request
+ *   2. tnr_count()           - geometry, binning and the counting pass; the only
+ *                              host synchronisation: returns E
+ *   3. tnr_emit()            - writes the requested quantities (i, j, P, S, d,
+ *                              D) into caller buffers sized for E pairs
+ * The frontend calls them in this order with the same request, workspace and
+ * stream.  Quantity assembly that the reference does in Torch
+ * (src/tonari/_torch_frontend.py:78-105) is fused into tnr_emit.
+ *
+ * All pointers are device pointers unless stated otherwise.  Every launch and
+ * copy goes on `stream`, on the current HIP device.  The library keeps no
+ * mutable global state: concurrent calls with distinct workspaces are safe.
+ *
+ * Return codes: TNR_OK, TNR_INPUT_ERROR (reference InputError -> Python
+ * ValueError), TNR_SEARCH_ERROR (reference SearchError / TORCH_CHECK ->
+ * Python RuntimeError), TNR_DEVICE_ERROR (HIP failure -> RuntimeError).  A
+ * NUL-terminated message is written to `err` (capacity `err_len`).
+ */
+#ifndef TONARI_HIP_H
+#define TONARI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TNR_ABI_VERSION 1
+
+#define TNR_OK 0
+#define TNR_INPUT_ERROR 1
+#define TNR_SEARCH_ERROR 2
+#define TNR_DEVICE_ERROR 3
+
+#define TNR_FLOAT32 0
+#define TNR_FLOAT64 1
+
+/* Algorithm enum of the reference (csrc/core/algorithm.h:10-29). */
+#define TNR_AUTO 0
+#define TNR_BRUTE_FORCE 1
+#define TNR_CELL_LIST 2
+
+/* One neighbor-list request: the arguments of bindings_cuda.cpp:59-68. */
+typedef struct tnr_request {
+    int32_t dtype;            /* TNR_FLOAT32 or TNR_FLOAT64 */
+    int32_t algorithm;        /* TNR_AUTO / TNR_BRUTE_FORCE / TNR_CELL_LIST */
+    int64_t n_atoms;          /* N_total */
+    int64_t n_structures;     /* B (batch_ptr has B + 1 entries) */
+    const void* positions;    /* T[N][3], contiguous */
+    const int64_t* batch_ptr; /* int64[B + 1] */
+    const void* cell;         /* T[B][3][3], rows are cell vectors */
+    const uint8_t* pbc;       /* uint8 (bool) [B][3] */
+    double cutoff;            /* strict, finite, positive */
+    int32_t half_list;        /* 0 / 1 */
+    int32_t include_self;     /* 0 / 1 */
+    int32_t sorted;           /* 0 / 1 (output is always source-major) */
+    int32_t reserved;
+} tnr_request;
+
+/* Output buffers for tnr_emit; any pointer may be NULL (not requested). */
+typedef struct tnr_outputs {
+    int64_t n_pairs;    /* E returned by tnr_count */
+    int64_t* pairs;     /* P: int64[E][2] (source, target) */
+    int32_t* shifts;    /* S: int32[E][3] */
+    void* distances;    /* d: T[E] */
+    void* vectors;      /* D: T[E][3] = pos[j] - pos[i] + S @ cell[b] */
+    int64_t* sources;   /* i: int64[E] */
+    int64_t* targets;   /* j: int64[E] */
+} tnr_outputs;
+
+/* ABI version compiled into the library (TNR_ABI_VERSION). */
+int tnr_abi_version(void);
+
+/* Offload target the library was compiled for ("gfx950"). */
+const char* tnr_device_arch(void);
+
+/* Device scratch bytes for `req`; depends only on dtype, N and B. */
+size_t tnr_workspace_size(const tnr_request* req);
+
+/*
+ * Validates the request on the device, builds per-structure geometry and the
+ * cell-list bins, counts pairs per source and scans the counts.  Copies the
+ * status and pair count into `host_result` (pinned host memory, at least 4
+ * int64) and synchronises `stream`; *n_pairs receives E.
+ */
+int tnr_count(const tnr_request* req, void* workspace, size_t workspace_bytes,
+              int64_t* host_result, void* stream, int64_t* n_pairs, char* err,
+              size_t err_len);
+
+/* Writes every non-NULL output of `out` for the request last counted in
+ * `workspace`; the pair order is source-major (sorted by source index). */
+int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
+             const tnr_outputs* out, void* stream, char* err, size_t err_len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TONARI_HIP_H */

@@ -1,0 +1,83 @@
+"""Shared helpers for the test suite (parity checks against the CPU oracle)."""
+
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+
+
+def keys_of(pairs, shifts) -> np.ndarray:
+    """Canonically sorted (i, j, Sx, Sy, Sz) rows; asserts there are no duplicates."""
+    p = pairs.detach().cpu().numpy() if hasattr(pairs, "detach") else np.asarray(pairs)
+    s = shifts.detach().cpu().numpy() if hasattr(shifts, "detach") else np.asarray(shifts)
+    assert p.dtype == np.int64 and s.dtype == np.int32
+    assert p.ndim == 2 and p.shape[1] == 2 and s.shape == (len(p), 3)
+    keys = oracle.canonical_keys(p, s)
+    if len(keys) > 1:
+        dup = np.all(keys[1:] == keys[:-1], axis=1)
+        assert not dup.any(), "neighbor list contains duplicate pair identities"
+    return keys
+
+
+def key_set(pairs, shifts) -> set[tuple[int, ...]]:
+    return {tuple(int(x) for x in row) for row in keys_of(pairs, shifts)}
+
+
+def assert_same_keys(actual: np.ndarray, expected: np.ndarray) -> None:
+    if actual.shape == expected.shape and np.array_equal(actual, expected):
+        return
+    a = {tuple(r) for r in actual.tolist()}
+    e = {tuple(r) for r in expected.tolist()}
+    missing = sorted(e - a)[:10]
+    extra = sorted(a - e)[:10]
+    raise AssertionError(
+        f"pair sets differ: {len(actual)} vs {len(expected)} pairs; "
+        f"missing {missing} extra {extra}"
+    )
+
+
+def assert_sorted_by_source(pairs) -> None:
+    src = pairs[:, 0]
+    src = src.detach().cpu().numpy() if hasattr(src, "detach") else np.asarray(src)
+    assert np.all(src[1:] >= src[:-1])
+
+
+def oracle_call(cfg: dict, *, algorithm: str | None = None, threads: int = 8, kind: str = "port"):
+    return oracle.neighbor_pairs(
+        cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"],
+        half_list=cfg.get("half_list", False), include_self=cfg.get("include_self", False),
+        algorithm=algorithm or cfg.get("algorithm", "auto"), threads=threads, kind=kind,
+    )
+
+
+def geometry_tolerance(dtype) -> float:
+    """d/D agreement bound from the specification: 1e-5 relative (fp32), 1e-12 (fp64)."""
+    return 1e-5 if np.dtype(dtype) == np.float32 else 1e-12
+
+
+def assert_geometry_close(pairs, shifts, d, D, cfg) -> None:
+    """Check d and D of each pair against the reference formula D = x[j]-x[i]+S@cell[b].
+
+    Tolerance: |D - D_ref| <= rtol * (|D_ref| + cutoff) componentwise and the same
+    for d, with rtol 1e-5 for float32 and 1e-12 for float64; the reference
+    formula is evaluated in float64 from the same inputs.
+    """
+    pos = cfg["positions"].astype(np.float64)
+    cell = cfg["cell"].astype(np.float64)
+    bp = cfg["batch_ptr"]
+    p = pairs.detach().cpu().numpy() if hasattr(pairs, "detach") else pairs
+    s = shifts.detach().cpu().numpy() if hasattr(shifts, "detach") else shifts
+    b = np.searchsorted(bp[1:], p[:, 0], side="right")
+    ref = pos[p[:, 1]] - pos[p[:, 0]] + np.einsum("ei,eij->ej", s.astype(np.float64), cell[b])
+    rtol = geometry_tolerance(cfg["positions"].dtype)
+    scale = np.abs(ref) + cfg["cutoff"]
+    if D is not None:
+        Dn = D.detach().cpu().numpy().astype(np.float64)
+        bad = np.abs(Dn - ref) > rtol * scale
+        assert not bad.any(), f"D differs at {np.argwhere(bad)[:5].tolist()}"
+    if d is not None:
+        dn = d.detach().cpu().numpy().astype(np.float64)
+        dref = np.sqrt(np.sum(ref * ref, axis=1))
+        bad = np.abs(dn - dref) > rtol * (dref + cfg["cutoff"])
+        assert not bad.any(), f"d differs at {np.argwhere(bad)[:5].tolist()}"

@@ -1,0 +1,105 @@
+"""Loader for the HIP provider ``libtonari_hip.so`` (C ABI, ctypes).
+
+Replaces the reference's provider loader (``src/tonari/_extensions.py:26-66``):
+the same lazy, cached load with ``ImportError`` on a missing or incompatible
+build, checked against ``torch.version.hip`` instead of ``torch.version.cuda``.
+The C ABI is declared in ``include/tonari_hip.h``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
+ABI_VERSION = 1
+
+TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR = 0, 1, 2, 3
+ALGORITHMS = {"auto": 0, "brute_force": 1, "cell_list": 2}
+EXPORTS = (
+    "tnr_abi_version",
+    "tnr_device_arch",
+    "tnr_workspace_size",
+    "tnr_count",
+    "tnr_emit",
+)
+
+
+class Request(ctypes.Structure):
+    """``tnr_request`` of include/tonari_hip.h."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("algorithm", ctypes.c_int32),
+        ("n_atoms", ctypes.c_int64),
+        ("n_structures", ctypes.c_int64),
+        ("positions", ctypes.c_void_p),
+        ("batch_ptr", ctypes.c_void_p),
+        ("cell", ctypes.c_void_p),
+        ("pbc", ctypes.c_void_p),
+        ("cutoff", ctypes.c_double),
+        ("half_list", ctypes.c_int32),
+        ("include_self", ctypes.c_int32),
+        ("sorted", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class Outputs(ctypes.Structure):
+    """``tnr_outputs`` of include/tonari_hip.h."""
+
+    _fields_ = [
+        ("n_pairs", ctypes.c_int64),
+        ("pairs", ctypes.c_void_p),
+        ("shifts", ctypes.c_void_p),
+        ("distances", ctypes.c_void_p),
+        ("vectors", ctypes.c_void_p),
+        ("sources", ctypes.c_void_p),
+        ("targets", ctypes.c_void_p),
+    ]
+
+
+def open_library(path: str = LIBRARY) -> ctypes.CDLL:
+    """Open the shared library and declare every exported signature."""
+    if not os.path.exists(path):
+        raise ImportError(
+            f"the HIP provider was not built ({path} is missing); "
+            "run `python -m tonari_amd.build`"
+        )
+    lib = ctypes.CDLL(path)
+    lib.tnr_abi_version.restype = ctypes.c_int
+    lib.tnr_abi_version.argtypes = []
+    lib.tnr_device_arch.restype = ctypes.c_char_p
+    lib.tnr_device_arch.argtypes = []
+    lib.tnr_workspace_size.restype = ctypes.c_size_t
+    lib.tnr_workspace_size.argtypes = [ctypes.POINTER(Request)]
+    lib.tnr_count.restype = ctypes.c_int
+    lib.tnr_count.argtypes = [
+        ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_emit.restype = ctypes.c_int
+    lib.tnr_emit.argtypes = [
+        ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(Outputs),
+        ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    version = lib.tnr_abi_version()
+    if version != ABI_VERSION:
+        raise ImportError(
+            f"libtonari_hip.so has ABI version {version}, expected {ABI_VERSION}; rebuild it"
+        )
+    return lib
+
+
+@lru_cache
+def load_torch_hip() -> ctypes.CDLL:
+    """Load the provider for PyTorch tensors on ROCm (HIP) devices."""
+    import torch
+
+    if not getattr(torch.version, "hip", None):
+        raise ImportError(
+            "tonari_amd requires a ROCm build of PyTorch (torch.version.hip is unset)"
+        )
+    return open_library()

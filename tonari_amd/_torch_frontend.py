@@ -1,0 +1,248 @@
+"""PyTorch frontend of ``neighbor_list``.
+
+Restates the reference frontend (``src/tonari/_torch_frontend.py``): the same
+single-structure normalisation (``:25-48``), validation and messages
+(``:51-75``), detached contiguous arguments (``:128-137``) and quantity order
+(``:78-105``).  The native call goes to the HIP C ABI instead of the pybind11
+CUDA provider (``:138-145``); i/j/P/S/d/D are written by the emit kernel
+instead of being assembled with Torch gathers.
+
+When ``d`` or ``D`` is requested and ``positions`` or ``cell`` requires
+gradients, d/D are built from P and S with the reference's differentiable
+Torch expression so autograd works as in the reference.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from math import isfinite
+
+import torch
+from torch import Tensor
+
+from ._extensions import (
+    ALGORITHMS,
+    TNR_INPUT_ERROR,
+    TNR_OK,
+    Outputs,
+    Request,
+    load_torch_hip,
+)
+
+
+def _require_torch_tensors(*, cell: object, pbc: object, batch_ptr: object | None) -> None:
+    for name, tensor in (("cell", cell), ("pbc", pbc), ("batch_ptr", batch_ptr)):
+        if tensor is not None and not isinstance(tensor, Tensor):
+            raise TypeError(
+                "positions, cell, pbc, and batch_ptr must all be PyTorch tensors; "
+                f"{name} has type {type(tensor).__name__}"
+            )
+
+
+def normalize_torch_inputs(
+    positions: Tensor, cell: Tensor, pbc: Tensor, batch_ptr: Tensor | None
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    if positions.ndim != 2 or positions.shape[1] != 3:
+        raise ValueError("positions must have shape (N_total, 3)")
+    if batch_ptr is None:
+        if cell.ndim != 2 or cell.shape != (3, 3):
+            raise ValueError("single-structure cell must have shape (3, 3)")
+        if pbc.ndim != 1 or pbc.shape != (3,):
+            raise ValueError("single-structure pbc must have shape (3,)")
+        batch_ptr = torch.tensor([0, len(positions)], dtype=torch.int64, device=positions.device)
+        cell = cell.unsqueeze(0)
+        pbc = pbc.unsqueeze(0)
+    else:
+        if cell.ndim != 3:
+            raise ValueError("batched cell must have shape (B, 3, 3)")
+        if pbc.ndim != 2:
+            raise ValueError("batched pbc must have shape (B, 3)")
+    return positions, cell, pbc, batch_ptr
+
+
+def validate_torch_inputs(
+    positions: Tensor, cell: Tensor, pbc: Tensor, cutoff: float, batch_ptr: Tensor
+) -> None:
+    if positions.device.type not in ("cpu", "cuda"):
+        raise ValueError("positions must be a CPU or CUDA tensor")
+    if positions.dtype not in (torch.float32, torch.float64):
+        raise ValueError("positions must have dtype float32 or float64")
+    if batch_ptr.ndim != 1 or batch_ptr.numel() == 0 or batch_ptr.dtype != torch.int64:
+        raise ValueError("batch_ptr must be int64 with shape (B + 1,)")
+    if cell.shape != (batch_ptr.numel() - 1, 3, 3):
+        raise ValueError("cell must have shape (B, 3, 3)")
+    if cell.dtype != positions.dtype:
+        raise ValueError("cell and positions must have the same dtype")
+    if pbc.shape != (batch_ptr.numel() - 1, 3) or pbc.dtype != torch.bool:
+        raise ValueError("pbc must be bool with shape (B, 3)")
+    if any(tensor.device != positions.device for tensor in (cell, pbc, batch_ptr)):
+        raise ValueError("positions, cell, pbc, and batch_ptr must be on the same device")
+    if not isfinite(cutoff) or cutoff <= 0:
+        raise ValueError("cutoff must be finite and positive")
+
+
+def _differentiable_geometry(
+    quantities: str, positions: Tensor, cell: Tensor, batch_ptr: Tensor, pairs: Tensor,
+    shifts: Tensor,
+) -> dict[str, Tensor]:
+    """The reference's Torch expression for D and d (``_torch_frontend.py:92-104``)."""
+    source = pairs[:, 0].contiguous()
+    target = pairs[:, 1].contiguous()
+    pair_batch = torch.bucketize(source, batch_ptr[1:], right=True)
+    vectors = positions[target] - positions[source] + torch.einsum(
+        "ei,eij->ej", shifts.to(positions.dtype), cell[pair_batch]
+    )
+    values = {"D": vectors}
+    if "d" in quantities:
+        values["d"] = torch.linalg.vector_norm(vectors, dim=1)
+    return values
+
+
+def _raise(code: int, message: str) -> None:
+    if code == TNR_INPUT_ERROR:
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def neighbor_list_hip(
+    quantities: str,
+    positions: Tensor,
+    batch_ptr: Tensor,
+    cell: Tensor,
+    pbc: Tensor,
+    cutoff: float,
+    *,
+    half_list: bool,
+    include_self: bool,
+    algorithm: str,
+    sorted: bool,
+    grad_positions: Tensor | None = None,
+    grad_cell: Tensor | None = None,
+) -> tuple[Tensor, ...]:
+    """Run count + emit on the tensors' HIP device; returns one tensor per quantity."""
+    try:
+        lib = load_torch_hip()
+    except ImportError as error:
+        raise RuntimeError(f"the CUDA provider is unavailable: {error}") from error
+    device = positions.device
+    if positions.shape[0] >= 2**31:
+        raise ValueError("the current implementation supports fewer than 2^31 atoms")
+    need_grad = (
+        any(q in quantities for q in "dD")
+        and torch.is_grad_enabled()
+        and (
+            (grad_positions is not None and grad_positions.requires_grad)
+            or (grad_cell is not None and grad_cell.requires_grad)
+        )
+    )
+    req = Request(
+        dtype=0 if positions.dtype == torch.float32 else 1,
+        algorithm=ALGORITHMS[algorithm],
+        n_atoms=positions.shape[0],
+        n_structures=batch_ptr.numel() - 1,
+        positions=positions.data_ptr(),
+        batch_ptr=batch_ptr.data_ptr(),
+        cell=cell.data_ptr(),
+        pbc=pbc.data_ptr(),
+        cutoff=cutoff,
+        half_list=int(half_list),
+        include_self=int(include_self),
+        sorted=int(sorted),
+        reserved=0,
+    )
+    err = ctypes.create_string_buffer(512)
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        host = torch.empty(4, dtype=torch.int64, pin_memory=True)
+        n_pairs = ctypes.c_int64(0)
+        code = lib.tnr_count(
+            ctypes.byref(req), workspace.data_ptr(), ws_bytes, host.data_ptr(), stream,
+            ctypes.byref(n_pairs), err, len(err),
+        )
+        if code != TNR_OK:
+            _raise(code, err.value.decode())
+        count = int(n_pairs.value)
+        dtype = positions.dtype
+        want = set(quantities)
+        if need_grad:
+            want |= {"P", "S"}
+            want -= {"d", "D"}
+        out: dict[str, Tensor] = {}
+        if "P" in want:
+            out["P"] = torch.empty((count, 2), dtype=torch.int64, device=device)
+        if "S" in want:
+            out["S"] = torch.empty((count, 3), dtype=torch.int32, device=device)
+        if "i" in want:
+            out["i"] = torch.empty((count,), dtype=torch.int64, device=device)
+        if "j" in want:
+            out["j"] = torch.empty((count,), dtype=torch.int64, device=device)
+        if "d" in want:
+            out["d"] = torch.empty((count,), dtype=dtype, device=device)
+        if "D" in want:
+            out["D"] = torch.empty((count, 3), dtype=dtype, device=device)
+        if count > 0 and out:
+            ptrs = Outputs(
+                n_pairs=count,
+                pairs=out["P"].data_ptr() if "P" in out else None,
+                shifts=out["S"].data_ptr() if "S" in out else None,
+                distances=out["d"].data_ptr() if "d" in out else None,
+                vectors=out["D"].data_ptr() if "D" in out else None,
+                sources=out["i"].data_ptr() if "i" in out else None,
+                targets=out["j"].data_ptr() if "j" in out else None,
+            )
+            code = lib.tnr_emit(
+                ctypes.byref(req), workspace.data_ptr(), ws_bytes, ctypes.byref(ptrs), stream,
+                err, len(err),
+            )
+            if code != TNR_OK:
+                _raise(code, err.value.decode())
+        if need_grad:
+            out.update(
+                _differentiable_geometry(
+                    quantities, grad_positions, grad_cell, batch_ptr, out["P"], out["S"]
+                )
+            )
+    return tuple(out[q] for q in quantities)
+
+
+def neighbor_list_torch(
+    quantities: str,
+    positions: Tensor,
+    cell: Tensor,
+    pbc: Tensor,
+    cutoff: float,
+    batch_ptr: Tensor | None,
+    *,
+    algorithm: str,
+    cpu_threads: int | None,
+    sorted: bool,
+    half_list: bool,
+    include_self: bool,
+) -> tuple[Tensor, ...]:
+    _require_torch_tensors(cell=cell, pbc=pbc, batch_ptr=batch_ptr)
+    positions, cell, pbc, batch_ptr = normalize_torch_inputs(positions, cell, pbc, batch_ptr)
+    cutoff = float(cutoff)
+    validate_torch_inputs(positions, cell, pbc, cutoff, batch_ptr)
+    if not positions.is_cuda:
+        raise RuntimeError(
+            "the Torch CPU provider is unavailable: tonari_amd runs the neighbor search "
+            "on ROCm (HIP) devices; move the tensors to a GPU"
+        )
+    if cpu_threads is not None:
+        raise ValueError("cpu_threads only applies to CPU inputs")
+    return neighbor_list_hip(
+        quantities,
+        positions.detach().contiguous(),
+        batch_ptr.contiguous(),
+        cell.detach().contiguous(),
+        pbc.contiguous(),
+        cutoff,
+        half_list=half_list,
+        include_self=include_self,
+        algorithm=algorithm,
+        sorted=sorted,
+        grad_positions=positions,
+        grad_cell=cell,
+    )

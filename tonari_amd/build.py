@@ -1,0 +1,66 @@
+"""Compile libtonari_hip.so for gfx950 with hipcc (in-tree, no JIT cache).
+
+Flags that matter for parity and safety:
+  -ffp-contract=off                      no implicit FMA contraction; the
+                                         broad phase asks for fma explicitly
+  -fno-gpu-flush-denormals-to-zero       IEEE denormals, like the CPU path
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                         no packed FP32 instructions
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+SOURCES = [os.path.join(HERE, "csrc", "tonari_hip.hip")]
+HEADERS = [os.path.join(HERE, "csrc", "nl_device.h"), os.path.join(ROOT, "include", "tonari_hip.h")]
+OUTPUT = os.path.join(HERE, "_lib", "libtonari_hip.so")
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the ROCm toolchain is required to build tonari_amd")
+    return path
+
+
+def command(output: str = OUTPUT, extra: list[str] | None = None) -> list[str]:
+    return [
+        hipcc(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-ffp-contract=off",
+        "-fno-gpu-flush-denormals-to-zero",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-I", os.path.join(ROOT, "include"),
+        *(extra or []),
+        *SOURCES,
+        "-o", output,
+    ]
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(os.path.dirname(OUTPUT), exist_ok=True)
+    tmp = OUTPUT + ".tmp"
+    cmd = command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        sys.stderr.write(result.stdout + result.stderr)
+        raise RuntimeError("hipcc failed to build libtonari_hip.so")
+    os.replace(tmp, OUTPUT)
+    return OUTPUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

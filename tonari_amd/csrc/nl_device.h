@@ -1,0 +1,187 @@
+// Device-side building blocks shared by the neighbor-list kernels: wave64
+// primitives, pair-identity policy, per-structure records and the workspace
+// layout.  Target: gfx950 (CDNA4), wave64 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace tnr {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kPieceCap = 192;            // stencil pieces per source bin
+constexpr int kStencilReach = 2;          // bins per cutoff along each grid axis
+constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
+constexpr int64_t kAutoBruteCandidates = 4096;     // N_b * images at or below: brute force
+
+// Status bits.  Input errors map to ValueError, search errors to RuntimeError.
+enum StatusBit : unsigned long long {
+    ST_BP_START = 1ull << 0,
+    ST_BP_END = 1ull << 1,
+    ST_BP_ORDER = 1ull << 2,
+    ST_CELL_NONFINITE = 1ull << 3,
+    ST_CELL_RANK = 1ull << 4,
+    ST_DUAL_RANGE = 1ull << 5,
+    ST_REPEAT_RANGE = 1ull << 6,
+    ST_IMAGE_CAP = 1ull << 7,
+    ST_BATCH_IMAGE_CAP = 1ull << 8,
+    ST_POS_NONFINITE = 1ull << 9,
+    ST_WRAP_RANGE = 1ull << 10,
+    ST_SHIFT_RANGE = 1ull << 11,
+    ST_CELL_UNSAFE = 1ull << 12,
+    ST_CAPACITY = 1ull << 13,
+};
+// Bits that make every later kernel skip its work (inputs are unusable).
+constexpr unsigned long long kAbortBits =
+    ST_BP_START | ST_BP_END | ST_BP_ORDER | ST_CELL_NONFINITE | ST_CELL_RANK | ST_DUAL_RANGE |
+    ST_REPEAT_RANGE | ST_IMAGE_CAP | ST_POS_NONFINITE | ST_WRAP_RANGE | ST_CAPACITY;
+
+// Slots of the status block (int64 each).
+enum StatusSlot : int {
+    SS_FLAGS = 0,
+    SS_PAIRS = 1,
+    SS_TOTAL_IMAGES = 2,
+    SS_TOTAL_BINS = 3,
+    SS_SLOTS = 64,
+};
+
+enum Algo : int { ALGO_NONE = 0, ALGO_BRUTE = 1, ALGO_CELL = 2 };
+
+// One record per structure.  Filled by k_setup (geometry), k_atoms
+// (reductions) and k_plan (algorithm and bin grid).
+struct alignas(16) StructRec {
+    int64_t atom0;
+    int64_t natoms;
+    int64_t nimages;
+    int64_t bin0;
+    int64_t nbins;
+    double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
+    double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
+    double lo[3];        // grid origin (inactive axes)
+    double inv_w[3];     // bins per grid unit
+    double pad;          // broad-phase margin (length units)
+    double inner2;       // broad d2 below this: inside for sure
+    double outer2;       // broad d2 at or above this: outside for sure
+    double cut2;         // (T)(cutoff * cutoff) as double
+    unsigned long long umin[3], umax[3];   // ordered keys of grid-coordinate bounds
+    unsigned long long cmin[3], cmax[3];   // ordered keys of Cartesian wrapped bounds
+    unsigned long long maxp[3];            // bits of max |p_c| (non-negative doubles)
+    uint32_t maxw[3];    // max |wrap_a| (2^31 fits)
+    int32_t reps[3];     // image repeats R_a
+    int32_t nb[3];       // bins per axis
+    int32_t reach[3];    // stencil reach K_a in bins
+    int32_t zseg;        // maximum z segments per stencil row
+    int32_t active;      // bit a set: axis a periodic
+    int32_t algo;
+    int32_t any_wrap;
+};
+
+// Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte
+// aligned base.  Depends only on N, B and the scalar size.
+struct Layout {
+    size_t status, structs, struct_bins, struct_bin_off, atom_struct, atom_wrap, atom_q,
+        atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials, total;
+    int64_t cap_bins, n_partials;
+};
+
+constexpr int64_t kScanItems = 8;
+constexpr int64_t kScanChunk = kBlock * kScanItems;
+
+inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
+
+inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
+    Layout L{};
+    L.cap_bins = 2 * n + 64 * b + 64;
+    const int64_t longest = (L.cap_bins > n ? L.cap_bins : n) + 1;
+    L.n_partials = (longest + kScanChunk - 1) / kScanChunk + 1;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = align_up(o + bytes);
+        return at;
+    };
+    L.status = take(sizeof(int64_t) * SS_SLOTS);
+    L.structs = take(sizeof(StructRec) * (size_t)(b > 0 ? b : 1));
+    L.struct_bins = take(sizeof(int64_t) * (size_t)(b + 1));
+    L.struct_bin_off = take(sizeof(int64_t) * (size_t)(b + 2));
+    L.atom_struct = take(sizeof(int32_t) * (size_t)(n + 1));
+    L.atom_wrap = take(sizeof(int32_t) * 4 * (size_t)(n + 1));
+    L.atom_q = take(tsize * 4 * (size_t)(n + 1));
+    L.atom_bin = take(sizeof(int32_t) * (size_t)(n + 1));
+    L.atom_rank = take(sizeof(int32_t) * (size_t)(n + 1));
+    L.bin_count = take(sizeof(int32_t) * (size_t)(L.cap_bins + 1));
+    L.bin_start = take(sizeof(int32_t) * (size_t)(L.cap_bins + 2));
+    L.binned = take(tsize * 4 * (size_t)(n + 1));
+    L.counts = take(sizeof(int64_t) * (size_t)(n + 1));
+    L.offsets = take(sizeof(int64_t) * (size_t)(n + 2));
+    L.partials = take(sizeof(int64_t) * (size_t)(L.n_partials + 1));
+    L.total = o;
+    return L;
+}
+
+// ------------------------------------------------------------ wave helpers
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ unsigned long long ballot(bool p) { return __ballot(p); }
+
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ int lanes_below(unsigned long long mask) {
+    return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(mask >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((unsigned)mask, 0u));
+}
+
+__device__ __forceinline__ int read_lane(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float read_lane(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double read_lane(double v, int l) {
+    const long long bits = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(bits & 0xffffffffll), l);
+    const int hi = __builtin_amdgcn_readlane((int)(bits >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ __forceinline__ long long read_lane(long long v, int l) {
+    const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffffll), l);
+    const int hi = __builtin_amdgcn_readlane((int)(v >> 32), l);
+    return ((long long)hi << 32) | (unsigned int)lo;
+}
+
+// Ordered 64-bit key of a double: key order == numeric order.
+__device__ __forceinline__ unsigned long long order_key(double x) {
+    const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+    return (b >> 63) ? ~b : (b | (1ull << 63));
+}
+__host__ __device__ inline double key_value(unsigned long long k) {
+    const unsigned long long b = (k >> 63) ? (k & ~(1ull << 63)) : ~k;
+    double x;
+    __builtin_memcpy(&x, &b, sizeof(x));
+    return x;
+}
+
+// ------------------------------------------------------------ pair policy
+// Reference: csrc/core/pair_policy.h:42-79.  A zero-shift self pair is kept
+// only with include_self; a half list keeps the lexicographically smaller of
+// (s, t, S) and (t, s, -S).  When s == t the output shift equals the image
+// shift, so the identity tests below take the image shift.
+
+__device__ __forceinline__ bool lex_negative(int kx, int ky, int kz) {
+    return kx < 0 || (kx == 0 && (ky < 0 || (ky == 0 && kz < 0)));
+}
+
+template <int MODE>
+__device__ __forceinline__ bool keep_identity(int s, int t, int kx, int ky, int kz) {
+    const bool self0 = s == t && kx == 0 && ky == 0 && kz == 0;
+    if (self0) return (MODE & 1) != 0;
+    if constexpr ((MODE & 2) != 0) {
+        if (s != t) return s < t;
+        return lex_negative(kx, ky, kz);
+    }
+    return true;
+}
+
+}  // namespace tnr
