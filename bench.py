@@ -1,0 +1,315 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X neighbor-list hot path (one JSON line on stdout).
+
+Headline workload (the north-star target): C4, a
+100,000-atom periodic float32 box of 100 A edge, cutoff 6 A, cell_list,
+quantities 'PD'.  One step is one public ``neighbor_list`` call with the
+inputs already resident in HBM (count pass, one host read of E, emit pass).
+``value`` is whole-job throughput in M pairs/s.
+
+Also reported:
+  roofline      the dominant kernel (the cell-list emit kernel) timed with
+                HIP events on the stream it runs on; achieved = algorithmic
+                bytes per launch (N*3*4 + E*(16+12)) / average duration,
+                against the 8 TB/s MI355X HBM peak
+  kernel_sum    count pipeline + emit timed the same way (no host gaps)
+  cpu_baseline  the reference CPU core (oracle/_ref, when built) or the
+                oracle restatement, on the full C4 workload with every
+                host core, median of 7 calls
+  secondary     C2 (batched crystals, the metric's second workload), C3 and
+                C5 measured the same way as the headline (no CPU leg)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+METRIC = "pairs/sec (M edges/s) + achieved HBM GB/s, 100k-atom box and batched crystals"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def to_device(cfg, dev):
+    import torch
+
+    return {
+        "positions": torch.as_tensor(cfg["positions"]).to(dev),
+        "cell": torch.as_tensor(cfg["cell"]).to(dev),
+        "pbc": torch.as_tensor(cfg["pbc"]).to(dev),
+        "batch_ptr": torch.as_tensor(cfg["batch_ptr"]).to(dev),
+    }
+
+
+def public_call(cfg, t):
+    from tonari_amd import neighbor_list
+
+    return neighbor_list(
+        cfg["quantities"], t["positions"], t["cell"], t["pbc"], cfg["cutoff"], t["batch_ptr"],
+        algorithm=cfg["algorithm"], sorted=cfg["sorted"], half_list=cfg["half_list"],
+        include_self=cfg["include_self"],
+    )
+
+
+def time_public(cfg, t, steps: int, warmup: int):
+    """Wall time of `steps` public calls bracketed by device synchronisation."""
+    import torch
+
+    out = None
+    for _ in range(warmup):
+        out = public_call(cfg, t)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = public_call(cfg, t)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    n_pairs = int(out[0].shape[0]) if out else 0
+    del out
+    return elapsed / steps, n_pairs
+
+
+def time_phases(cfg, t, reps: int):
+    """HIP-event durations of the count pipeline and of the emit kernel.
+
+    Drives the C ABI exactly as the frontend does, on torch's current stream,
+    recording events around tnr_count_async and around tnr_emit.  For a
+    cell-list workload tnr_emit launches one kernel (the cell-list emit), so
+    the second interval is that kernel's duration.
+    """
+    import torch
+
+    from tonari_amd._extensions import ALGORITHMS, Outputs, Request, load_torch_hip
+
+    lib = load_torch_hip()
+    pos = t["positions"]
+    dev = pos.device
+    req = Request(
+        dtype=0 if pos.dtype == torch.float32 else 1, algorithm=ALGORITHMS[cfg["algorithm"]],
+        n_atoms=pos.shape[0], n_structures=t["batch_ptr"].numel() - 1,
+        positions=pos.data_ptr(), batch_ptr=t["batch_ptr"].data_ptr(),
+        cell=t["cell"].data_ptr(), pbc=t["pbc"].data_ptr(), cutoff=cfg["cutoff"],
+        half_list=int(cfg["half_list"]), include_self=int(cfg["include_self"]),
+        sorted=int(cfg["sorted"]), stencil_reach=0,
+    )
+    ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    host = torch.empty(4, dtype=torch.int64, pin_memory=True)
+    err = ctypes.create_string_buffer(512)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    count_ms, emit_ms = [], []
+    quantities = cfg["quantities"]
+    n = ctypes.c_int64(0)
+    outs = {}
+    for rep in range(reps + 1):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        rc = lib.tnr_count_async(ctypes.byref(req), ws.data_ptr(), ws_bytes, host.data_ptr(),
+                                 stream, err, len(err))
+        ev[1].record()
+        torch.cuda.synchronize()
+        if rc != 0 or lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err)) != 0:
+            raise RuntimeError(err.value.decode())
+        E = int(n.value)
+        if not outs:
+            dt = pos.dtype
+            shapes = {"P": ((E, 2), torch.int64), "S": ((E, 3), torch.int32),
+                      "i": ((E,), torch.int64), "j": ((E,), torch.int64),
+                      "d": ((E,), dt), "D": ((E, 3), dt)}
+            outs = {q: torch.empty(shapes[q][0], dtype=shapes[q][1], device=dev)
+                    for q in set(quantities)}
+        ptr = lambda q: outs[q].data_ptr() if q in outs else None  # noqa: E731
+        o = Outputs(n_pairs=E, plan=int(host[3]), pairs=ptr("P"), shifts=ptr("S"),
+                    distances=ptr("d"), vectors=ptr("D"), sources=ptr("i"), targets=ptr("j"))
+        ev[2].record()
+        rc = lib.tnr_emit(ctypes.byref(req), ws.data_ptr(), ws_bytes, ctypes.byref(o), stream,
+                          err, len(err))
+        ev[3].record()
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError(err.value.decode())
+        if rep > 0:  # the first repetition warms caches and code objects
+            count_ms.append(ev[0].elapsed_time(ev[1]))
+            emit_ms.append(ev[2].elapsed_time(ev[3]))
+    plan = int(host[3])
+    del outs, ws
+    return statistics.mean(count_ms), statistics.mean(emit_ms), E, plan
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        data = json.load(fh)
+    return data.get("hbm_bytes_per_launch")
+
+
+def cpu_baseline(cfg, mode: str):
+    """The reference CPU core (or the restatement) on the same workload, all host cores."""
+    import oracle
+
+    kind = "reference" if mode in ("auto", "reference") and oracle.available("reference") else "port"
+    if mode == "reference" and kind != "reference":
+        log("oracle/_ref is not built; using the restatement")
+    cores = len(os.sched_getaffinity(0))
+    call = lambda: oracle.neighbor_pairs(  # noqa: E731
+        cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"],
+        half_list=cfg["half_list"], include_self=cfg["include_self"],
+        algorithm=cfg["algorithm"], threads=cores, kind=kind)
+    t0 = time.perf_counter()
+    pairs, _ = call()
+    n_pairs = len(pairs)
+    del pairs
+    samples = []
+    while len(samples) < 7 and (time.perf_counter() - t0) < 30.0:
+        s = time.perf_counter()
+        out = call()
+        samples.append(time.perf_counter() - s)
+        del out
+    med = statistics.median(samples)
+    return {
+        "value": round(n_pairs / med / 1e6, 3),
+        "unit": "M pairs/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": f"full C4 workload ({len(cfg['positions'])} atoms, {n_pairs} pairs, P+S "
+                  f"native output), median of {len(samples)} calls after one warm-up call",
+        "ms_per_call": round(med * 1e3, 3),
+    }
+
+
+def measure(name, cfg, steps, warmup, reps, dev):
+    from tonari_amd import workloads as W
+
+    t = to_device(cfg, dev)
+    ms_step, n_pairs = time_public(cfg, t, steps, warmup)
+    count_ms, emit_ms, E, plan = time_phases(cfg, t, reps)
+    assert E == n_pairs
+    itemsize = cfg["positions"].dtype.itemsize
+    b_alg = W.algorithmic_bytes(len(cfg["positions"]), n_pairs, cfg["quantities"], itemsize)
+    kernel_sum = count_ms + emit_ms
+    res = {
+        "n_atoms": len(cfg["positions"]),
+        "n_pairs": n_pairs,
+        "ms_per_step": round(ms_step * 1e3, 4),
+        "M_pairs_per_s": round(n_pairs / ms_step / 1e6, 3),
+        "M_atoms_per_s": round(len(cfg["positions"]) / ms_step / 1e6, 3),
+        "algorithmic_bytes": b_alg,
+        "count_us": round(count_ms * 1e3, 2),
+        "emit_us": round(emit_ms * 1e3, 2),
+        "kernel_sum_us": round(kernel_sum * 1e3, 2),
+        "GBps_kernel_sum": round(b_alg / (kernel_sum * 1e-3) / 1e9, 1),
+        "frac_kernel_sum": round(b_alg / (kernel_sum * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "GBps_end_to_end": round(b_alg / ms_step / 1e9, 1),
+        "plan": plan,
+    }
+    del t
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--reps", type=int, default=20, help="event-timed repetitions")
+    ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "reference", "port", "off"])
+    ap.add_argument("--secondary", default="C2,C3,C5", help="comma list, or 'none'")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path: run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    from tonari_amd import workloads as W
+
+    if not os.path.exists(os.path.join(ROOT, "tonari_amd", "_lib", "libtonari_hip.so")):
+        from tonari_amd import build
+
+        build.build()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    cfg = W.c4()
+    log("C4: timing")
+    head = measure("C4", cfg, args.steps, args.warmup, args.reps, dev)
+    log(f"C4: {head}")
+    secondary = {}
+    if args.secondary != "none":
+        for name in [s for s in args.secondary.split(",") if s]:
+            log(f"{name}: timing")
+            scfg = W.CONFIGS[name]()
+            steps = max(3, args.steps // 3) if name == "C5" else args.steps
+            secondary[name] = measure(name, scfg, steps, 2, max(3, args.reps // 4), dev)
+            log(f"{name}: {secondary[name]}")
+    base = None
+    if args.cpu_baseline != "off":
+        log("cpu baseline")
+        base = cpu_baseline(cfg, args.cpu_baseline)
+        log(f"cpu baseline: {base}")
+
+    emit_s = head["emit_us"] * 1e-6
+    achieved = head["algorithmic_bytes"] / emit_s / 1e9
+    line = {
+        "metric": METRIC,
+        "value": head["M_pairs_per_s"],
+        "unit": "M pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy PCG64, BASELINE.json configs)",
+        "config": {
+            "workload": "C4: 100000 atoms uniform in a 100 A periodic cube (density 0.1/A^3), "
+                        "float32, cutoff 6 A, cell_list, quantities 'PD', full list",
+            "n_atoms": head["n_atoms"],
+            "n_pairs": head["n_pairs"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "k_cell<float, full, emit>",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": load_traffic("c4_emit"),
+            "algorithmic_bytes_per_launch": head["algorithmic_bytes"],
+            "avg_launch_us": head["emit_us"],
+        },
+        "cpu_baseline": base,
+        "M_atoms_per_s": head["M_atoms_per_s"],
+        "kernel_sum_us": head["kernel_sum_us"],
+        "count_us": head["count_us"],
+        "frac_kernel_sum": head["frac_kernel_sum"],
+        "GBps_end_to_end": head["GBps_end_to_end"],
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -69,12 +69,13 @@ typedef struct tnr_request {
     int32_t half_list;        /* 0 / 1 */
     int32_t include_self;     /* 0 / 1 */
     int32_t sorted;           /* 0 / 1 (output is always source-major) */
-    int32_t reserved;
+    int32_t stencil_reach;    /* cell-list bins per cutoff along each axis, 1-4; 0 = default (2) */
 } tnr_request;
 
 /* Output buffers for tnr_emit; any pointer may be NULL (not requested). */
 typedef struct tnr_outputs {
     int64_t n_pairs;    /* E returned by tnr_count */
+    int64_t plan;       /* host_result[3] of tnr_count (kernel families in use); 0 = all */
     int64_t* pairs;     /* P: int64[E][2] (source, target) */
     int32_t* shifts;    /* S: int32[E][3] */
     void* distances;    /* d: T[E] */
@@ -95,12 +96,23 @@ size_t tnr_workspace_size(const tnr_request* req);
 /*
  * Validates the request on the device, builds per-structure geometry and the
  * cell-list bins, counts pairs per source and scans the counts.  Copies the
- * status and pair count into `host_result` (pinned host memory, at least 4
- * int64) and synchronises `stream`; *n_pairs receives E.
+ * status words into `host_result` (pinned host memory, at least 4 int64:
+ * status flags, E, total periodic images, plan mask) and synchronises
+ * `stream`; *n_pairs receives E.  Equivalent to tnr_count_async followed by
+ * hipStreamSynchronize(stream) and tnr_count_finish.
  */
 int tnr_count(const tnr_request* req, void* workspace, size_t workspace_bytes,
               int64_t* host_result, void* stream, int64_t* n_pairs, char* err,
               size_t err_len);
+
+/* The counting pass without the synchronisation: everything is enqueued on
+ * `stream`; `host_result` is valid once the stream has reached this point. */
+int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_bytes,
+                    int64_t* host_result, void* stream, char* err, size_t err_len);
+
+/* Decodes `host_result` written by a completed tnr_count_async: maps the
+ * status flags to the reference's error types and messages, sets *n_pairs. */
+int tnr_count_finish(const int64_t* host_result, int64_t* n_pairs, char* err, size_t err_len);
 
 /* Writes every non-NULL output of `out` for the request last counted in
  * `workspace`; the pair order is source-major (sorted by source index). */

@@ -23,6 +23,8 @@ EXPORTS = (
     "tnr_device_arch",
     "tnr_workspace_size",
     "tnr_count",
+    "tnr_count_async",
+    "tnr_count_finish",
     "tnr_emit",
 )
 
@@ -43,7 +45,7 @@ class Request(ctypes.Structure):
         ("half_list", ctypes.c_int32),
         ("include_self", ctypes.c_int32),
         ("sorted", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("stencil_reach", ctypes.c_int32),
     ]
 
 
@@ -52,6 +54,7 @@ class Outputs(ctypes.Structure):
 
     _fields_ = [
         ("n_pairs", ctypes.c_int64),
+        ("plan", ctypes.c_int64),
         ("pairs", ctypes.c_void_p),
         ("shifts", ctypes.c_void_p),
         ("distances", ctypes.c_void_p),
@@ -78,6 +81,15 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     lib.tnr_count.restype = ctypes.c_int
     lib.tnr_count.argtypes = [
         ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_count_async.restype = ctypes.c_int
+    lib.tnr_count_async.argtypes = [
+        ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_count_finish.restype = ctypes.c_int
+    lib.tnr_count_finish.argtypes = [
         ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, ctypes.c_size_t,
     ]
     lib.tnr_emit.restype = ctypes.c_int

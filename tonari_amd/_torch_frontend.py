@@ -148,7 +148,7 @@ def neighbor_list_hip(
         half_list=int(half_list),
         include_self=int(include_self),
         sorted=int(sorted),
-        reserved=0,
+        stencil_reach=0,
     )
     err = ctypes.create_string_buffer(512)
     with torch.cuda.device(device):
@@ -185,6 +185,7 @@ def neighbor_list_hip(
         if count > 0 and out:
             ptrs = Outputs(
                 n_pairs=count,
+                plan=int(host[3]),
                 pairs=out["P"].data_ptr() if "P" in out else None,
                 shifts=out["S"].data_ptr() if "S" in out else None,
                 distances=out["d"].data_ptr() if "d" in out else None,

@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "../../include/tonari_hip.h"
+
 #include <cstddef>
 #include <cstdint>
 
@@ -45,14 +47,16 @@ enum StatusSlot : int {
     SS_FLAGS = 0,
     SS_PAIRS = 1,
     SS_TOTAL_IMAGES = 2,
-    SS_TOTAL_BINS = 3,
+    SS_PLAN = 3,          // bit 0: some brute-force structure, bit 1: some cell-list one
+    SS_TOTAL_BINS = 4,
     SS_SLOTS = 64,
 };
 
 enum Algo : int { ALGO_NONE = 0, ALGO_BRUTE = 1, ALGO_CELL = 2 };
 
 // One record per structure.  Filled by k_setup (geometry), k_atoms
-// (reductions) and k_plan (algorithm and bin grid).
+// (reductions of atoms in blocks that span several structures) and k_plan
+// (margins, algorithm and bin grid).
 struct alignas(16) StructRec {
     int64_t atom0;
     int64_t natoms;
@@ -69,8 +73,8 @@ struct alignas(16) StructRec {
     double cut2;         // (T)(cutoff * cutoff) as double
     unsigned long long umin[3], umax[3];   // ordered keys of grid-coordinate bounds
     unsigned long long cmin[3], cmax[3];   // ordered keys of Cartesian wrapped bounds
-    unsigned long long maxp[3];            // bits of max |p_c| (non-negative doubles)
-    uint32_t maxw[3];    // max |wrap_a| (2^31 fits)
+    unsigned long long maxp;               // bits of max_c |p_c| (non-negative double)
+    uint32_t maxw;       // max_a |wrap_a| (2^31 fits)
     int32_t reps[3];     // image repeats R_a
     int32_t nb[3];       // bins per axis
     int32_t reach[3];    // stencil reach K_a in bins
@@ -78,14 +82,26 @@ struct alignas(16) StructRec {
     int32_t active;      // bit a set: axis a periodic
     int32_t algo;
     int32_t any_wrap;
+    int32_t diagonal;    // every off-diagonal cell entry is zero
 };
+
+// Per-block reduction record written by k_atoms for blocks whose atoms all
+// lie in one structure (k_plan combines them without atomics).
+struct alignas(16) BlockPartial {
+    unsigned long long umin[3], umax[3], cmin[3], cmax[3];
+    unsigned long long maxp;
+    unsigned long long maxw;
+};
+
+constexpr int kMaxChunks = 8;   // candidate chunks of 64 held in registers
 
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
     size_t status, structs, struct_bins, struct_bin_off, atom_struct, atom_wrap, atom_q,
-        atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials, total;
-    int64_t cap_bins, n_partials;
+        atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials,
+        block_partials, masks, total;
+    int64_t cap_bins, n_partials, n_atom_blocks;
 };
 
 constexpr int64_t kScanItems = 8;
@@ -119,6 +135,9 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.counts = take(sizeof(int64_t) * (size_t)(n + 1));
     L.offsets = take(sizeof(int64_t) * (size_t)(n + 2));
     L.partials = take(sizeof(int64_t) * (size_t)(L.n_partials + 1));
+    L.n_atom_blocks = (n + kBlock - 1) / kBlock;
+    L.block_partials = take(sizeof(BlockPartial) * (size_t)(L.n_atom_blocks + 1));
+    L.masks = take(sizeof(unsigned long long) * kMaxChunks * (size_t)(n + 1));
     L.total = o;
     return L;
 }

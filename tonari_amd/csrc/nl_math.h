@@ -1,0 +1,154 @@
+// Scalar helpers shared by the kernels: correctly rounded arithmetic in the
+// input type, the reference's public predicate, and small vector types.
+#pragma once
+
+#include "nl_device.h"
+
+#include <cmath>
+
+namespace tnr {
+
+template <typename T>
+struct Ops;
+
+template <>
+struct Ops<float> {
+    static constexpr double eps = 1.1920928955078125e-07;
+    static constexpr double max = 3.4028234663852886e+38;
+    __device__ static float add(float a, float b) { return __fadd_rn(a, b); }
+    __device__ static float sub(float a, float b) { return __fsub_rn(a, b); }
+    __device__ static float mul(float a, float b) { return __fmul_rn(a, b); }
+    __device__ static float fma_(float a, float b, float c) { return __fmaf_rn(a, b, c); }
+    __device__ static float sqrt_(float a) { return __fsqrt_rn(a); }
+    // Nearest float not below / not above x.
+    __device__ static float down(double x) {
+        float f = (float)x;
+        if ((double)f > x) f = nextafterf(f, -INFINITY);
+        return f;
+    }
+    __device__ static float up(double x) {
+        float f = (float)x;
+        if ((double)f < x) f = nextafterf(f, INFINITY);
+        return f;
+    }
+};
+
+template <>
+struct Ops<double> {
+    static constexpr double eps = 2.220446049250313e-16;
+    static constexpr double max = 1.7976931348623157e+308;
+    __device__ static double add(double a, double b) { return __dadd_rn(a, b); }
+    __device__ static double sub(double a, double b) { return __dsub_rn(a, b); }
+    __device__ static double mul(double a, double b) { return __dmul_rn(a, b); }
+    __device__ static double fma_(double a, double b, double c) { return __fma_rn(a, b, c); }
+    __device__ static double sqrt_(double a) { return __dsqrt_rn(a); }
+    __device__ static double down(double x) { return x; }
+    __device__ static double up(double x) { return x; }
+};
+
+template <typename T>
+struct alignas(4 * sizeof(T)) Vec4 {
+    T x, y, z, w;
+};
+
+// The atom index rides in the fourth lane of a binned record.
+__device__ __forceinline__ float idx_as(int i, float) { return __int_as_float(i); }
+__device__ __forceinline__ double idx_as(int i, double) { return (double)i; }
+__device__ __forceinline__ int as_idx(float v) { return __float_as_int(v); }
+__device__ __forceinline__ int as_idx(double v) { return (int)v; }
+
+__device__ __forceinline__ unsigned long long load_status(const unsigned long long* s) {
+    return __atomic_load_n(s, __ATOMIC_RELAXED);
+}
+
+__device__ __forceinline__ int floor_div(int a, int b) {
+    int q = a / b;
+    if ((a % b != 0) && ((a < 0) != (b < 0))) --q;
+    return q;
+}
+
+// The public predicate of the reference (neighbors_cpu.cpp:247-261): D =
+// (p_t - p_s) + S0 c0 + S1 c1 + S2 c2 with every product and sum rounded in
+// T in this order, d2 = D0^2 + D1^2 + D2^2 left to right.  Writes D, returns d2.
+template <typename T>
+__device__ __forceinline__ T public_vector(const T ps[3], const T pt[3], long long S0,
+                                           long long S1, long long S2, const T* cell,
+                                           T D[3]) {
+    using O = Ops<T>;
+    const T s0 = (T)S0, s1 = (T)S1, s2 = (T)S2;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        T comp = O::sub(pt[c], ps[c]);
+        comp = O::add(comp, O::mul(s0, cell[c]));
+        comp = O::add(comp, O::mul(s1, cell[3 + c]));
+        comp = O::add(comp, O::mul(s2, cell[6 + c]));
+        D[c] = comp;
+    }
+    T d2 = O::mul(D[0], D[0]);
+    d2 = O::add(d2, O::mul(D[1], D[1]));
+    d2 = O::add(d2, O::mul(D[2], D[2]));
+    return d2;
+}
+
+// Same value for a cell whose off-diagonal entries are all zero: the skipped
+// products are signed zeros, whose addition leaves every nonzero sum
+// unchanged, so D equals the general formula (up to the sign of a zero).
+template <typename T>
+__device__ __forceinline__ T public_vector_diag(const T ps[3], const T pt[3], long long S0,
+                                                long long S1, long long S2, const T* cell,
+                                                T D[3]) {
+    using O = Ops<T>;
+    D[0] = O::add(O::sub(pt[0], ps[0]), O::mul((T)S0, cell[0]));
+    D[1] = O::add(O::sub(pt[1], ps[1]), O::mul((T)S1, cell[4]));
+    D[2] = O::add(O::sub(pt[2], ps[2]), O::mul((T)S2, cell[8]));
+    T d2 = O::mul(D[0], D[0]);
+    d2 = O::add(d2, O::mul(D[1], D[1]));
+    d2 = O::add(d2, O::mul(D[2], D[2]));
+    return d2;
+}
+
+__device__ __forceinline__ bool fits_i32(long long v) {
+    return v >= -2147483648ll && v <= 2147483647ll;
+}
+
+// ----------------------------------------------------------- wave reductions
+
+__device__ __forceinline__ long long wave_inclusive_scan(long long x) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan_i32(int x) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long x) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        const unsigned long long y = __shfl_xor(x, d);
+        x = y < x ? y : x;
+    }
+    return x;
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        const unsigned long long y = __shfl_xor(x, d);
+        x = y > x ? y : x;
+    }
+    return x;
+}
+
+}  // namespace tnr

@@ -1,0 +1,717 @@
+// Prologue kernels of a neighbor-list request: per-structure periodic
+// metadata (k_setup), per-atom wraps and reductions (k_atoms), per-structure
+// margins / algorithm / bin grid (k_plan), and the counting sort of cell-list
+// atoms into bins (k_bin, k_scatter).
+#pragma once
+
+#include "nl_math.h"
+
+namespace tnr {
+
+// ------------------------------------------------------------------ geometry
+
+// Moore-Penrose pseudo-inverse of the k active cell rows (stored in columns
+// 0..k-1 of w) by one-sided (Hestenes) Jacobi in float64: the algorithm of
+// geometry.cpp:15-118, carried out in double instead of long double.  Loops
+// run over all three columns with guards so every index is static (no
+// scratch memory).  Returns false when the active rows are linearly dependent.
+__device__ bool active_pinv(double w[3][3], int k, double dual[3][3]) {
+    double v[3][3] = {{1, 0, 0}, {0, 1, 0}, {0, 0, 1}};
+    const double eps = 2.220446049250313e-16;
+    for (int sweep = 0; sweep < 64; ++sweep) {
+        bool rotated = false;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) {
+#pragma unroll
+            for (int q = p + 1; q < 3; ++q) {
+                if (q >= k) continue;
+                double app = 0, aqq = 0, apq = 0;
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    app += w[c][p] * w[c][p];
+                    aqq += w[c][q] * w[c][q];
+                    apq += w[c][p] * w[c][q];
+                }
+                if (fabs(apq) <= 8 * eps * sqrt(app * aqq)) continue;
+                rotated = true;
+                const double zeta = (aqq - app) / (2 * apq);
+                const double t =
+                    zeta == 0.0 ? 1.0 : copysign(1.0, zeta) / (fabs(zeta) + hypot(1.0, zeta));
+                const double cs = 1.0 / hypot(1.0, t);
+                const double sn = cs * t;
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    const double a = w[c][p], b = w[c][q];
+                    w[c][p] = cs * a - sn * b;
+                    w[c][q] = sn * a + cs * b;
+                }
+#pragma unroll
+                for (int r = 0; r < 3; ++r) {
+                    const double a = v[r][p], b = v[r][q];
+                    v[r][p] = cs * a - sn * b;
+                    v[r][q] = sn * a + cs * b;
+                }
+            }
+        }
+        if (!rotated) break;
+    }
+    double sig2[3], smax = 0, smin = INFINITY;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        sig2[j] = w[0][j] * w[0][j] + w[1][j] * w[1][j] + w[2][j] * w[2][j];
+        if (j < k) {
+            const double s = sqrt(sig2[j]);
+            smax = fmax(smax, s);
+            smin = fmin(smin, s);
+        }
+    }
+    if (!(smin > eps * 3 * fmax(smax, 1.0))) return false;
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            double acc = 0;
+#pragma unroll
+            for (int j = 0; j < 3; ++j)
+                if (j < k) acc += w[c][j] * v[a][j] / sig2[j];
+            dual[c][a] = a < k ? acc : 0.0;
+        }
+    return true;
+}
+
+__device__ inline void cross3(const double a[3], const double b[3], double o[3]) {
+    o[0] = a[1] * b[2] - a[2] * b[1];
+    o[1] = a[2] * b[0] - a[0] * b[2];
+    o[2] = a[0] * b[1] - a[1] * b[0];
+}
+
+__device__ inline void normalize3(double v[3]) {
+    const double n = sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    if (n > 0 && isfinite(n)) {
+        v[0] /= n;
+        v[1] /= n;
+        v[2] /= n;
+    }
+}
+
+// One thread per structure: batch_ptr checks, periodic metadata
+// (geometry.cpp:123-219) and the grid frame used for binning.  Grid rows:
+// dual columns on periodic axes (the grid coordinate is the fractional
+// coordinate) and orthonormal complements of the periodic rows elsewhere.
+template <typename T>
+__global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb,
+                        int64_t n_atoms, double cutoff, StructRec* recs,
+                        unsigned long long* status) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    unsigned long long* flags = status + SS_FLAGS;
+    if (nb == 0) {
+        if (b == 0) {
+            unsigned long long st = 0;
+            if (bp[0] != 0) st |= ST_BP_START;
+            if (bp[0] != n_atoms) st |= ST_BP_END;
+            if (st) atomicOr(flags, st);
+        }
+        return;
+    }
+    if (b >= nb) return;
+    StructRec& r = recs[b];
+    unsigned long long st = 0;
+    const int64_t lo = bp[b], hi = bp[b + 1];
+    if (b == 0 && lo != 0) st |= ST_BP_START;
+    if (b == nb - 1 && hi != n_atoms) st |= ST_BP_END;
+    if (hi < lo) st |= ST_BP_ORDER;
+    const int64_t natoms = hi > lo ? hi - lo : 0;
+    r.atom0 = lo;
+    r.natoms = natoms;
+    r.bin0 = 0;
+    r.nbins = 0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        r.umin[a] = r.cmin[a] = ~0ull;
+        r.umax[a] = r.cmax[a] = 0ull;
+        r.lo[a] = 0.0;
+        r.inv_w[a] = 1.0;
+        r.reps[a] = 0;
+        r.nb[a] = 1;
+        r.reach[a] = 1;
+    }
+    r.maxp = 0;
+    r.maxw = 0;
+    r.algo = ALGO_NONE;
+    r.any_wrap = 0;
+
+    double cell[3][3];
+    bool finite = true;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            cell[a][c] = (double)cells[9 * b + 3 * a + c];
+            finite = finite && isfinite(cell[a][c]);
+        }
+    r.diagonal = cell[0][1] == 0 && cell[0][2] == 0 && cell[1][0] == 0 && cell[1][2] == 0 &&
+                 cell[2][0] == 0 && cell[2][1] == 0;
+    if (!finite) st |= ST_CELL_NONFINITE;
+    const bool px = pbc[3 * b] != 0, py = pbc[3 * b + 1] != 0, pz = pbc[3 * b + 2] != 0;
+    const int k = (int)px + (int)py + (int)pz;
+    r.active = (px ? 1 : 0) | (py ? 2 : 0) | (pz ? 4 : 0);
+    // slot j holds the j-th periodic axis, then the non-periodic ones, in
+    // increasing axis order (a lookup on the 3-bit mask keeps indices static)
+    int slot_axis[3] = {0, 1, 2};
+    switch (r.active) {
+        case 2: slot_axis[0] = 1; slot_axis[1] = 0; slot_axis[2] = 2; break;
+        case 4: slot_axis[0] = 2; slot_axis[1] = 0; slot_axis[2] = 1; break;
+        case 5: slot_axis[0] = 0; slot_axis[1] = 2; slot_axis[2] = 1; break;
+        case 6: slot_axis[0] = 1; slot_axis[1] = 2; slot_axis[2] = 0; break;
+        default: break;
+    }
+    r.nimages = 1;
+    double dual_slot[3][3] = {{0, 0, 0}, {0, 0, 0}, {0, 0, 0}};
+    if (finite && natoms > 0) {
+        double w[3][3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j)
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                w[c][j] = j < k ? cell[slot_axis[j] == 0 ? 0 : (slot_axis[j] == 1 ? 1 : 2)][c] : 0.0;
+        if (k > 0 && !active_pinv(w, k, dual_slot)) st |= ST_CELL_RANK;
+        int64_t reps[3] = {0, 0, 0};
+        if (!(st & ST_CELL_RANK)) {
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                if (j >= k) continue;
+                const double n2 = dual_slot[0][j] * dual_slot[0][j] +
+                                  dual_slot[1][j] * dual_slot[1][j] +
+                                  dual_slot[2][j] * dual_slot[2][j];
+                if (!isfinite(n2) || !isfinite(dual_slot[0][j]) || !isfinite(dual_slot[1][j]) ||
+                    !isfinite(dual_slot[2][j]))
+                    st |= ST_DUAL_RANGE;
+                const double rep = ceil(cutoff * sqrt(n2));
+                if (!(rep <= 2147483647.0))
+                    st |= ST_REPEAT_RANGE;
+                else
+                    reps[j] = (int64_t)rep;
+            }
+        }
+        // per-axis repeats and duals, image count with the 2^24 cap
+        int64_t rep_axis[3] = {0, 0, 0};
+        double dual_axis[3][3] = {{0, 0, 0}, {0, 0, 0}, {0, 0, 0}};
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            if (j >= k) continue;
+            const int a = slot_axis[j];
+#pragma unroll
+            for (int aa = 0; aa < 3; ++aa)
+                if (aa == a) {
+                    rep_axis[aa] = reps[j];
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) dual_axis[c][aa] = dual_slot[c][j];
+                }
+        }
+        const bool geometry_ok = !(st & (ST_REPEAT_RANGE | ST_CELL_RANK | ST_DUAL_RANGE));
+        int64_t count = 1;
+        if (geometry_ok) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                const int64_t f = 2 * rep_axis[a] + 1;
+                if (!(st & ST_IMAGE_CAP)) {
+                    if (count > kImageCap / f)
+                        st |= ST_IMAGE_CAP;
+                    else
+                        count *= f;
+                }
+            }
+        }
+        if (geometry_ok && !(st & ST_IMAGE_CAP)) {
+            r.nimages = count;
+#pragma unroll
+            for (int a = 0; a < 3; ++a) r.reps[a] = (int32_t)rep_axis[a];
+            atomicAdd((unsigned long long*)(status + SS_TOTAL_IMAGES), (unsigned long long)count);
+        }
+#pragma unroll
+        for (int e = 0; e < 9; ++e) r.dual[e] = dual_axis[e / 3][e % 3];
+        // grid frame
+        double g[3][3] = {{1, 0, 0}, {0, 1, 0}, {0, 0, 1}};
+#pragma unroll
+        for (int a = 0; a < 3; ++a)
+            if (r.active >> a & 1)
+#pragma unroll
+                for (int c = 0; c < 3; ++c) g[a][c] = dual_axis[c][a];
+        if (k == 2) {
+            const int i0 = slot_axis[0], i1 = slot_axis[1], ic = slot_axis[2];
+            double r0[3], r1[3], nrm[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                r0[c] = i0 == 0 ? cell[0][c] : (i0 == 1 ? cell[1][c] : cell[2][c]);
+                r1[c] = i1 == 0 ? cell[0][c] : (i1 == 1 ? cell[1][c] : cell[2][c]);
+            }
+            cross3(r0, r1, nrm);
+            normalize3(nrm);
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+                if (a == ic)
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) g[a][c] = nrm[c];
+        } else if (k == 1) {
+            const int i0 = slot_axis[0], i1 = slot_axis[1], i2 = slot_axis[2];
+            double rr[3];
+#pragma unroll
+            for (int c = 0; c < 3; ++c)
+                rr[c] = i0 == 0 ? cell[0][c] : (i0 == 1 ? cell[1][c] : cell[2][c]);
+            normalize3(rr);
+            double unit[3] = {0, 0, 0};
+            if (fabs(rr[0]) <= fabs(rr[1]) && fabs(rr[0]) <= fabs(rr[2]))
+                unit[0] = 1;
+            else if (fabs(rr[1]) <= fabs(rr[2]))
+                unit[1] = 1;
+            else
+                unit[2] = 1;
+            double e1[3], e2[3];
+            cross3(rr, unit, e1);
+            normalize3(e1);
+            cross3(rr, e1, e2);
+            normalize3(e2);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                if (a == i1)
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) g[a][c] = e1[c];
+                if (a == i2)
+#pragma unroll
+                    for (int c = 0; c < 3; ++c) g[a][c] = e2[c];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 9; ++e) r.grid[e] = g[e / 3][e % 3];
+    } else {
+#pragma unroll
+        for (int e = 0; e < 9; ++e) {
+            r.dual[e] = 0.0;
+            r.grid[e] = (e % 4 == 0) ? 1.0 : 0.0;
+        }
+    }
+    if (st) atomicOr(flags, st);
+}
+
+// Structure of atom i: the b with bp[b] <= i < bp[b + 1] (batch_ptr valid).
+__device__ __forceinline__ int structure_of(const int64_t* bp, int64_t nb, int64_t i) {
+    int64_t lo = 0, hi = nb;  // answer in [lo, hi)
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (bp[mid] <= i) lo = mid; else hi = mid;
+    }
+    return (int)lo;
+}
+
+// floor(sum_c x_c * y_c) with double-double accumulation (nearly exact), as
+// the reference's long-double fractional coordinate (neighbors_cpu.cpp:110-
+// 122); *ok becomes false when the value is non-finite or outside
+// [-2^31, 2^31).
+__device__ __forceinline__ int wrap_of(const double x[3], const double y[3], bool* ok) {
+    double hi = 0, lo = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const double p = x[c] * y[c];
+        const double pe = fma(x[c], y[c], -p);
+        const double s = hi + p;
+        const double bb = s - hi;
+        const double se = (hi - (s - bb)) + (p - bb);
+        lo += pe + se;
+        hi = s;
+    }
+    const double s = hi + lo;
+    lo = lo - (s - hi);
+    hi = s;
+    if (!isfinite(hi)) {
+        *ok = false;
+        return 0;
+    }
+    double f = floor(hi);
+    if (hi == f && lo < 0) f -= 1.0;
+    if (!(f >= -2147483648.0 && f <= 2147483647.0)) {
+        *ok = false;
+        return 0;
+    }
+    return (int)f;
+}
+
+template <typename T>
+__device__ __forceinline__ void grid_coords(const StructRec& r, const T q[3], double u[3]) {
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+        u[a] = r.grid[3 * a] * (double)q[0] + r.grid[3 * a + 1] * (double)q[1] +
+               r.grid[3 * a + 2] * (double)q[2];
+}
+
+// One thread per atom: finiteness, representative wraps and wrapped
+// positions (neighbors_cpu.cpp:92-133), and the per-structure reductions the
+// planner needs (grid-coordinate and Cartesian bounds, max |p|, max |wrap|).
+// A block whose atoms all lie in one structure writes one BlockPartial
+// without atomics; a block spanning several structures uses atomics on the
+// structure records (each such structure is small, so contention is low).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* bp,
+                                                   const T* cells, int64_t nb, int64_t n_atoms,
+                                                   StructRec* recs, BlockPartial* partials,
+                                                   int* atom_struct, int4* atom_wrap,
+                                                   Vec4<T>* atom_q, unsigned long long* status) {
+    __shared__ unsigned long long s_red[kWavesPerBlock][14];
+    __shared__ unsigned long long s_flags;
+    // Block-uniform early exit (the barrier below needs every thread).
+    if (threadIdx.x == 0) s_flags = load_status(status + SS_FLAGS);
+    __syncthreads();
+    if (s_flags & kAbortBits) return;
+    const int64_t first = (int64_t)blockIdx.x * kBlock;
+    const int64_t last = (first + kBlock < n_atoms ? first + kBlock : n_atoms) - 1;
+    const int64_t i = first + threadIdx.x;
+    const bool valid = i < n_atoms;
+    const int bfirst = structure_of(bp, nb, first);
+    const int blast = structure_of(bp, nb, last);
+    const bool uniform = bfirst == blast;
+    int b = bfirst;
+    bool good = false;
+    T q[3] = {T(0), T(0), T(0)};
+    int w[3] = {0, 0, 0};
+    double u[3] = {0, 0, 0};
+    double pmax = 0;
+    unsigned long long st = 0;
+    if (valid) {
+        b = uniform ? bfirst : structure_of(bp, nb, i);
+        atom_struct[i] = b;
+        const StructRec& r = recs[b];
+        T p[3];
+        bool finite = true;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            p[c] = pos[3 * i + c];
+            finite = finite && isfinite((double)p[c]);
+        }
+        if (!finite) {
+            st |= ST_POS_NONFINITE;
+        } else {
+            const double pd[3] = {(double)p[0], (double)p[1], (double)p[2]};
+            bool ok = true;
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                const double dcol[3] = {(double)(T)r.dual[a], (double)(T)r.dual[3 + a],
+                                        (double)(T)r.dual[6 + a]};
+                w[a] = wrap_of(pd, dcol, &ok);
+            }
+            if (!ok) {
+                st |= ST_WRAP_RANGE;
+            } else {
+                const T* cell = cells + 9 * b;
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    T x = p[c];
+#pragma unroll
+                    for (int a = 0; a < 3; ++a)
+                        x = Ops<T>::sub(x, Ops<T>::mul((T)w[a], cell[3 * a + c]));
+                    q[c] = x;
+                }
+                grid_coords(r, q, u);
+                pmax = fmax(fabs(pd[0]), fmax(fabs(pd[1]), fabs(pd[2])));
+                good = true;
+            }
+        }
+        atom_wrap[i] = make_int4(w[0], w[1], w[2], 0);
+        atom_q[i] = Vec4<T>{q[0], q[1], q[2], idx_as((int)i, T(0))};
+    }
+    if (st) atomicOr(status + SS_FLAGS, st);
+
+    unsigned long long v[14];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        v[a] = good ? order_key(u[a]) : ~0ull;
+        v[3 + a] = good ? order_key(u[a]) : 0ull;
+        v[6 + a] = good ? order_key((double)q[a]) : ~0ull;
+        v[9 + a] = good ? order_key((double)q[a]) : 0ull;
+    }
+    v[12] = good ? (unsigned long long)__double_as_longlong(pmax) : 0ull;
+    v[13] = good ? max(max((unsigned long long)llabs((long long)w[0]),
+                           (unsigned long long)llabs((long long)w[1])),
+                       (unsigned long long)llabs((long long)w[2]))
+                 : 0ull;
+    if (uniform) {
+        const int wv = threadIdx.x / kWave;
+#pragma unroll
+        for (int e = 0; e < 14; ++e) {
+            const bool is_min = (e < 3) || (e >= 6 && e < 9);
+            v[e] = is_min ? wave_min_u64(v[e]) : wave_max_u64(v[e]);
+        }
+        if (lane_id() == 0)
+#pragma unroll
+            for (int e = 0; e < 14; ++e) s_red[wv][e] = v[e];
+        __syncthreads();
+        if (threadIdx.x < 14) {
+            const int e = threadIdx.x;
+            const bool is_min = (e < 3) || (e >= 6 && e < 9);
+            unsigned long long x = s_red[0][e];
+#pragma unroll
+            for (int k = 1; k < kWavesPerBlock; ++k)
+                x = is_min ? min(x, s_red[k][e]) : max(x, s_red[k][e]);
+            unsigned long long* out = reinterpret_cast<unsigned long long*>(&partials[blockIdx.x]);
+            out[e] = x;
+        }
+    } else if (good) {
+        StructRec& r = recs[b];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            atomicMin(&r.umin[a], v[a]);
+            atomicMax(&r.umax[a], v[3 + a]);
+            atomicMin(&r.cmin[a], v[6 + a]);
+            atomicMax(&r.cmax[a], v[9 + a]);
+        }
+        atomicMax(&r.maxp, v[12]);
+        atomicMax(&r.maxw, (unsigned)v[13]);
+    }
+}
+
+// One wave per structure: combine the block partials and atomics, then (lane
+// 0) the broad-phase margin, the algorithm and the bin grid.  The margin
+// pad = 64 eps_T max(scale, rc) bounds the difference between the fused
+// broad-phase distance and the public predicate, with scale = 2 max|p| +
+// sum_a (R_a + 2 max|w|) max_c |cell_ac|, the operation scale of
+// neighbors_cpu.cpp:156-219.
+template <typename T>
+__global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int64_t n_atoms,
+                                                double cutoff, int requested, int reach_target,
+                                                StructRec* recs, const BlockPartial* partials,
+                                                long long* struct_bins,
+                                                unsigned long long* status) {
+    const int64_t b = blockIdx.x;
+    const int lane = lane_id();
+    if (b == 0 && lane == 0 && status[SS_TOTAL_IMAGES] > (unsigned long long)kImageCap)
+        atomicOr(status + SS_FLAGS, ST_BATCH_IMAGE_CAP);
+    if (b >= nb) return;
+    if (load_status(status + SS_FLAGS) & kAbortBits) {
+        if (lane == 0) struct_bins[b] = 0;
+        return;
+    }
+    StructRec& r = recs[b];
+    const int64_t n = r.natoms;
+    // reduce the partials of uniform blocks inside this structure
+    unsigned long long v[14];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        v[a] = r.umin[a];
+        v[3 + a] = r.umax[a];
+        v[6 + a] = r.cmin[a];
+        v[9 + a] = r.cmax[a];
+    }
+    v[12] = r.maxp;
+    v[13] = r.maxw;
+    if (n > 0) {
+        const int64_t k0 = r.atom0 / kBlock, k1 = (r.atom0 + n - 1) / kBlock;
+        for (int64_t kb = k0 + lane; kb <= k1; kb += kWave) {
+            const int64_t first = kb * kBlock;
+            const int64_t last = (first + kBlock < n_atoms ? first + kBlock : n_atoms) - 1;
+            if (first < r.atom0 || last >= r.atom0 + n) continue;  // shared block: atomics
+            const unsigned long long* p = reinterpret_cast<const unsigned long long*>(&partials[kb]);
+#pragma unroll
+            for (int e = 0; e < 14; ++e) {
+                const bool is_min = (e < 3) || (e >= 6 && e < 9);
+                v[e] = is_min ? min(v[e], p[e]) : max(v[e], p[e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 14; ++e) {
+        const bool is_min = (e < 3) || (e >= 6 && e < 9);
+        v[e] = is_min ? wave_min_u64(v[e]) : wave_max_u64(v[e]);
+    }
+    if (lane != 0) return;
+    if (n == 0) {
+        r.algo = ALGO_NONE;
+        r.nbins = 0;
+        struct_bins[b] = 0;
+        return;
+    }
+    double cell[9];
+#pragma unroll
+    for (int e = 0; e < 9; ++e) cell[e] = (double)cells[9 * b + e];
+    const double maxp = __longlong_as_double((long long)v[12]);
+    const double maxw = (double)v[13];
+    const int active = r.active;
+    const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
+    double scale = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const double sc = 2 * maxp + ((double)R0 + 2 * maxw) * fabs(cell[c]) +
+                          ((double)R1 + 2 * maxw) * fabs(cell[3 + c]) +
+                          ((double)R2 + 2 * maxw) * fabs(cell[6 + c]);
+        scale = fmax(scale, sc);
+    }
+    const double rc = cutoff;
+    const double pad = 64.0 * Ops<T>::eps * fmax(scale, rc);
+    r.pad = pad;
+    r.maxp = v[12];
+    r.maxw = (uint32_t)v[13];
+    r.any_wrap = v[13] != 0;
+    const double inner = rc - pad;
+    r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
+    r.outer2 = (double)Ops<T>::up((rc + pad) * (rc + pad));
+    r.cut2 = (double)(T)(cutoff * cutoff);
+    const bool safe = isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Ops<T>::max;
+
+    const int64_t nimages = r.nimages;
+    const bool large = n > kAutoBruteCandidates / nimages;
+    bool want_cell = requested == TNR_CELL_LIST || (requested == TNR_AUTO && large);
+    unsigned long long st = 0;
+    if (requested == TNR_CELL_LIST) {
+        // The reference CPU layout rule (neighbors_cpu.cpp:379-430): bins of
+        // the padded cutoff over the bounding box of the wrapped positions.
+        const double size = rc + pad;
+        double count = 1;
+        bool ok = safe;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const double span = key_value(v[9 + c]) - key_value(v[6 + c]) + 2 * size;
+            const double dim = span / size;
+            if (!isfinite(dim) || dim > 67108864.0) ok = false;
+            count *= fmax(1.0, ceil(dim));
+        }
+        if (!ok || count > 67108864.0 || ceil(count / 64.0) > (double)n * (double)nimages)
+            st |= ST_CELL_UNSAFE;
+    }
+    if (!safe) want_cell = false;
+    int algo = ALGO_BRUTE;
+    int64_t nbins = 0;
+    if (want_cell) {
+        const double rcu0 = rc + 2 * pad;
+        const double kt = (double)reach_target;
+        double ext[3], wdt[3], nbf[3], rcu[3], lo[3];
+        bool ok = true;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const double gn = sqrt(r.grid[3 * a] * r.grid[3 * a] +
+                                   r.grid[3 * a + 1] * r.grid[3 * a + 1] +
+                                   r.grid[3 * a + 2] * r.grid[3 * a + 2]);
+            rcu[a] = rcu0 * gn;
+            lo[a] = 0.0;
+            if (active >> a & 1) {
+                ext[a] = 1.0;
+                nbf[a] = fmin(fmax(ceil(kt / rcu[a]) - 1.0, 1.0), 1048576.0);
+                wdt[a] = 1.0 / nbf[a];
+            } else {
+                lo[a] = key_value(v[a]);
+                const double hi = key_value(v[3 + a]);
+                ext[a] = fmax(hi - lo[a], 0.0);
+                if (!isfinite(ext[a]) || !isfinite(lo[a])) ok = false;
+                wdt[a] = rcu[a] / kt * (1.0 + 1e-9);
+                if (ext[a] / wdt[a] > 1048575.0) wdt[a] = ext[a] / 1048575.0 * (1.0 + 1e-9);
+                if (!(wdt[a] > 0) || !isfinite(wdt[a])) wdt[a] = 1.0;
+                nbf[a] = fmin(floor(ext[a] / wdt[a]) + 1.0, 1048576.0);
+            }
+        }
+        const double capb = 2.0 * (double)n + 64.0;
+        for (int it = 0; it < 200 && nbf[0] * nbf[1] * nbf[2] > capb; ++it) {
+            const int a = (nbf[0] >= nbf[1] && nbf[0] >= nbf[2]) ? 0 : (nbf[1] >= nbf[2] ? 1 : 2);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                if (c != a) continue;
+                if (active >> c & 1) {
+                    nbf[c] = ceil(nbf[c] / 2.0);
+                    wdt[c] = 1.0 / nbf[c];
+                } else {
+                    wdt[c] *= 2.0;
+                    nbf[c] = fmin(floor(ext[c] / wdt[c]) + 1.0, 1048576.0);
+                }
+            }
+        }
+        int reach[3];
+        bool reach_ok = true;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const double rd = floor(rcu[a] / wdt[a] * (1.0 + 1e-12)) + 1.0;
+            reach_ok = reach_ok && rd < 256.0;
+            reach[a] = rd < 256.0 ? (int)rd : 1;
+        }
+        const int rows = (2 * reach[0] + 1) * (2 * reach[1] + 1);
+        int zs = 1;
+        if (active >> 2 & 1) {
+            const int span = 2 * reach[2] + 1;
+            zs = min(span, (span + (int)nbf[2] - 1) / (int)nbf[2] + 1);
+        }
+        const bool fits = ok && reach_ok && nbf[0] * nbf[1] * nbf[2] <= capb &&
+                          (long long)rows * zs <= kPieceCap &&
+                          (double)n * (double)(rows * zs) < 2147483647.0;
+        if (fits) {
+            algo = ALGO_CELL;
+            nbins = (int64_t)(nbf[0] * nbf[1] * nbf[2]);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                r.nb[a] = (int32_t)nbf[a];
+                r.inv_w[a] = (active >> a & 1) ? nbf[a] : 1.0 / wdt[a];
+                r.lo[a] = lo[a];
+                r.reach[a] = reach[a];
+            }
+            r.zseg = zs;
+        }
+    }
+    r.algo = algo;
+    r.nbins = nbins;
+    struct_bins[b] = nbins;
+    atomicOr(status + SS_PLAN, algo == ALGO_CELL ? 2ull : 1ull);
+    if (st) atomicOr(status + SS_FLAGS, st);
+}
+
+__global__ void k_struct_bin0(StructRec* recs, const long long* off, int64_t nb,
+                              unsigned long long* status, int64_t cap_bins) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < nb) recs[b].bin0 = off[b];
+    if (b == 0) {
+        status[SS_TOTAL_BINS] = (unsigned long long)off[nb];
+        if (off[nb] > cap_bins) atomicOr(status + SS_FLAGS, ST_CAPACITY);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ int64_t local_bin(const StructRec& r, const T q[3]) {
+    double u[3];
+    grid_coords(r, q, u);
+    int64_t k[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const double x = (u[a] - r.lo[a]) * r.inv_w[a];
+        double f = floor(x);
+        f = fmin(fmax(f, 0.0), (double)(r.nb[a] - 1));
+        k[a] = isfinite(f) ? (int64_t)f : 0;
+    }
+    return (k[0] * r.nb[1] + k[1]) * r.nb[2] + k[2];
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_bin(int64_t n_atoms, const StructRec* recs,
+                                                 const int* atom_struct, const Vec4<T>* atom_q,
+                                                 int* atom_bin, int* atom_rank, int* bin_count,
+                                                 const unsigned long long* status) {
+    if (load_status(status + SS_FLAGS) & kAbortBits) return;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_atoms) return;
+    const StructRec& r = recs[atom_struct[i]];
+    if (r.algo != ALGO_CELL) {
+        atom_bin[i] = -1;
+        return;
+    }
+    const Vec4<T> v = atom_q[i];
+    const T q[3] = {v.x, v.y, v.z};
+    const int64_t g = r.bin0 + local_bin(r, q);
+    atom_bin[i] = (int)g;
+    atom_rank[i] = atomicAdd(bin_count + g, 1);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<T>* atom_q,
+                                                     const int* atom_bin, const int* atom_rank,
+                                                     const int* bin_start, Vec4<T>* binned,
+                                                     const unsigned long long* status) {
+    if (load_status(status + SS_FLAGS) & kAbortBits) return;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_atoms) return;
+    const int g = atom_bin[i];
+    if (g < 0) return;
+    binned[bin_start[g] + atom_rank[i]] = atom_q[i];
+}
+
+}  // namespace tnr
