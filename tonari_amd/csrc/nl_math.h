@@ -70,10 +70,9 @@ __device__ __forceinline__ int floor_div(int a, int b) {
 // The public predicate of the reference (neighbors_cpu.cpp:247-261): D =
 // (p_t - p_s) + S0 c0 + S1 c1 + S2 c2 with every product and sum rounded in
 // T in this order, d2 = D0^2 + D1^2 + D2^2 left to right.  Writes D, returns d2.
-template <typename T>
-__device__ __forceinline__ T public_vector(const T ps[3], const T pt[3], long long S0,
-                                           long long S1, long long S2, const T* cell,
-                                           T D[3]) {
+template <typename T, typename I>
+__device__ __forceinline__ T public_vector(const T ps[3], const T pt[3], I S0, I S1, I S2,
+                                           const T* cell, T D[3]) {
     using O = Ops<T>;
     const T s0 = (T)S0, s1 = (T)S1, s2 = (T)S2;
 #pragma unroll
@@ -93,10 +92,9 @@ __device__ __forceinline__ T public_vector(const T ps[3], const T pt[3], long lo
 // Same value for a cell whose off-diagonal entries are all zero: the skipped
 // products are signed zeros, whose addition leaves every nonzero sum
 // unchanged, so D equals the general formula (up to the sign of a zero).
-template <typename T>
-__device__ __forceinline__ T public_vector_diag(const T ps[3], const T pt[3], long long S0,
-                                                long long S1, long long S2, const T* cell,
-                                                T D[3]) {
+template <typename T, typename I>
+__device__ __forceinline__ T public_vector_diag(const T ps[3], const T pt[3], I S0, I S1, I S2,
+                                                const T* cell, T D[3]) {
     using O = Ops<T>;
     D[0] = O::add(O::sub(pt[0], ps[0]), O::mul((T)S0, cell[0]));
     D[1] = O::add(O::sub(pt[1], ps[1]), O::mul((T)S1, cell[4]));
@@ -123,13 +121,34 @@ __device__ __forceinline__ long long wave_inclusive_scan(long long x) {
     return x;
 }
 
+// Inclusive wave64 scans of 32-bit values with DPP lane moves (no LDS
+// crossbar): four row shifts build 16-lane row prefixes, then row_bcast:15
+// carries row 0 into row 1 and row 2 into row 3, and row_bcast:31 carries
+// rows 0-1 into rows 2-3.  Lanes whose source lane is outside the row (or
+// whose row is masked off) read the identity 0.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ int dpp_move(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, false);
+}
+
 __device__ __forceinline__ int wave_inclusive_scan_i32(int x) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int y = __shfl_up(x, d);
-        if (lane >= d) x += y;
-    }
+    x += dpp_move<0x111, 0xf>(x);  // row_shr:1
+    x += dpp_move<0x112, 0xf>(x);  // row_shr:2
+    x += dpp_move<0x114, 0xf>(x);  // row_shr:4
+    x += dpp_move<0x118, 0xf>(x);  // row_shr:8
+    x += dpp_move<0x142, 0xa>(x);  // row_bcast:15 into rows 1, 3
+    x += dpp_move<0x143, 0xc>(x);  // row_bcast:31 into rows 2, 3
+    return x;
+}
+
+// Inclusive running maximum of non-negative values.
+__device__ __forceinline__ int wave_inclusive_max_i32(int x) {
+    x = max(x, dpp_move<0x111, 0xf>(x));
+    x = max(x, dpp_move<0x112, 0xf>(x));
+    x = max(x, dpp_move<0x114, 0xf>(x));
+    x = max(x, dpp_move<0x118, 0xf>(x));
+    x = max(x, dpp_move<0x142, 0xa>(x));
+    x = max(x, dpp_move<0x143, 0xc>(x));
     return x;
 }
 

@@ -9,9 +9,9 @@
 //              wraps, wrapped position, block reductions) -> k_plan (one wave
 //              per structure: margins, algorithm, bin grid) -> scan(bins per
 //              structure) -> k_bin -> scan(bin counts) -> k_scatter ->
-//              k_cell<count> + k_brute<count> -> scan(pairs per source) ->
+//              k_cell_count + k_brute<count> -> scan(pairs per source) ->
 //              k_finish -> one 4-word device-to-host copy (E, status).
-//   tnr_emit:  k_cell<emit> and/or k_brute<emit> write i/j/P/S/d/D in place.
+//   tnr_emit:  k_cell_emit and/or k_brute<emit> write i/j/P/S/d/D in place.
 //
 // Reference semantics (songfeitong/tonari):
 //   the public predicate             csrc/core/neighbors_cpu.cpp:247-261
@@ -133,7 +133,12 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
     if (n == 0) return;
     const bool cell = plan ? (plan & 2) != 0 : req->algorithm != TNR_BRUTE_FORCE;
     const bool brute = plan ? (plan & 1) != 0 : true;
-    if (cell) k_cell<T, MODE, EMIT><<<query_blocks(L.cap_bins), kBlock, 0, stream>>>(q);
+    if (cell) {
+        if constexpr (EMIT)
+            k_cell_emit<T, MODE><<<query_blocks(L.cap_bins), kBlock, 0, stream>>>(q);
+        else
+            k_cell_count<T, MODE><<<query_blocks(L.cap_bins), kBlock, 0, stream>>>(q);
+    }
     if (brute) k_brute<T, MODE, EMIT><<<query_blocks(n), kBlock, 0, stream>>>(q);
 }
 
