@@ -39,7 +39,10 @@ def assert_same_keys(actual: np.ndarray, expected: np.ndarray) -> None:
 
 def assert_sorted_by_source(pairs) -> None:
     src = pairs[:, 0]
-    src = src.detach().cpu().numpy() if hasattr(src, "detach") else np.asarray(src)
+    if hasattr(src, "detach"):
+        assert bool((src[1:] >= src[:-1]).all())
+        return
+    src = np.asarray(src)
     assert np.all(src[1:] >= src[:-1])
 
 
@@ -81,3 +84,35 @@ def assert_geometry_close(pairs, shifts, d, D, cfg) -> None:
         dref = np.sqrt(np.sum(ref * ref, axis=1))
         bad = np.abs(dn - dref) > rtol * (dref + cfg["cutoff"])
         assert not bad.any(), f"d differs at {np.argwhere(bad)[:5].tolist()}"
+
+
+def _signed(k: int) -> int:
+    return k - (1 << 64) if k >= (1 << 63) else k
+
+
+def multiset_hash_torch(pairs, shifts) -> int:
+    """``oracle.multiset_hash`` evaluated with torch int64 ops on the tensors' device.
+
+    int64 multiplication, xor and addition wrap modulo 2^64 exactly like the
+    uint64 arithmetic of the numpy version; the logical right shift is an
+    arithmetic shift masked to the low 64 - k bits.
+    """
+    import torch
+
+    from oracle import _MIX
+
+    def shr(x, k):
+        return (x >> k) & ((1 << (64 - k)) - 1)
+
+    mul1 = _signed(_MIX[1])
+    cols = [pairs[:, 0], pairs[:, 1], shifts[:, 0], shifts[:, 1], shifts[:, 2]]
+    x = torch.zeros(pairs.shape[0], dtype=torch.int64, device=pairs.device)
+    for c, k in zip(cols, _MIX):
+        x = (x ^ (c.to(torch.int64) * _signed(k))) * mul1
+        x = x ^ shr(x, 31)
+    x = x ^ shr(x, 30)
+    x = x * mul1
+    x = x ^ shr(x, 27)
+    x = x * _signed(_MIX[2])
+    x = x ^ shr(x, 31)
+    return int(x.sum().item()) & ((1 << 64) - 1)

@@ -1,0 +1,183 @@
+"""The C ABI of libtonari_hip.so without a GPU.
+
+Checks that the library loads, exports every function ``include/tonari_hip.h``
+declares, reports its ABI version and target, sizes workspaces, rejects bad
+requests before touching the device, and maps device status words to the
+reference's exception types and messages in the reference's priority order
+(csrc/torch/bindings_cuda.cpp:69-118, csrc/torch/neighbors_cuda.cu:513-521).
+No call here launches a kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from tonari_amd import _extensions as ext
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tonari_hip.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(ext.LIBRARY):
+        from tonari_amd import build
+
+        build.build()
+    return ext.open_library()
+
+
+def _declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(tnr_\w+)\s*\(", text, flags=re.M)
+
+
+def _header_define(name: str) -> int:
+    m = re.search(rf"#define\s+{name}\s+(\d+)", open(HEADER).read())
+    assert m, name
+    return int(m.group(1))
+
+
+def test_header_declares_the_python_exports():
+    assert sorted(_declared_functions()) == sorted(ext.EXPORTS)
+
+
+def test_library_exports_every_declared_function(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_target(lib):
+    assert lib.tnr_abi_version() == _header_define("TNR_ABI_VERSION") == ext.ABI_VERSION
+    assert lib.tnr_device_arch() == b"gfx950"
+
+
+def test_struct_layouts_match_header():
+    # offsets of tnr_request / tnr_outputs as laid out by the C compiler
+    assert ctypes.sizeof(ext.Request) == 80
+    assert ext.Request.cutoff.offset == 56 and ext.Request.stencil_reach.offset == 76
+    assert ctypes.sizeof(ext.Outputs) == 64 and ext.Outputs.targets.offset == 56
+
+
+def _request(**kw) -> ext.Request:
+    base = dict(dtype=0, algorithm=0, n_atoms=10, n_structures=1, positions=1 << 20,
+                batch_ptr=1 << 21, cell=1 << 22, pbc=1 << 23, cutoff=1.0, half_list=0,
+                include_self=0, sorted=0, stencil_reach=0)
+    base.update(kw)
+    return ext.Request(**base)
+
+
+def test_workspace_size(lib):
+    sizes = []
+    for n in (0, 1, 1000, 100_000):
+        for dtype in (0, 1):
+            size = lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=n, dtype=dtype)))
+            assert size > 0 and size % 256 == 0
+            sizes.append(size)
+    assert sizes == sorted(sizes) or sizes[-1] > sizes[0]
+    # grows with the atom count, and double precision needs more
+    r32 = lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=100_000)))
+    r64 = lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=100_000, dtype=1)))
+    assert r64 > r32 > lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=1000)))
+    assert lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=-1))) == 0
+
+
+def _count_async(lib, req, ws=1 << 24, ws_bytes=None, host=1 << 25):
+    err = ctypes.create_string_buffer(256)
+    if ws_bytes is None:
+        ws_bytes = lib.tnr_workspace_size(ctypes.byref(req))
+    code = lib.tnr_count_async(ctypes.byref(req), ws, ws_bytes, host, None, err, len(err))
+    return code, err.value.decode()
+
+
+@pytest.mark.parametrize(
+    "fields, message",
+    [
+        ({"dtype": 7}, "dtype float32 or float64"),
+        ({"algorithm": 5}, "algorithm must be"),
+        ({"cutoff": float("nan")}, "cutoff must be finite and positive"),
+        ({"cutoff": 0.0}, "cutoff must be finite and positive"),
+        ({"cutoff": float("inf")}, "cutoff must be finite and positive"),
+        ({"stencil_reach": 9}, "stencil_reach"),
+        ({"n_atoms": 2**31}, "fewer than 2\\^31 atoms"),
+        ({"n_structures": -1}, "invalid sizes"),
+    ],
+)
+def test_bad_requests_are_rejected_on_the_host(lib, fields, message):
+    code, text = _count_async(lib, _request(**fields), ws_bytes=1 << 30)
+    assert code == ext.TNR_INPUT_ERROR
+    assert re.search(message, text), text
+
+
+def test_workspace_checks(lib):
+    req = _request()
+    need = lib.tnr_workspace_size(ctypes.byref(req))
+    assert _count_async(lib, req, ws_bytes=need - 256)[0] == ext.TNR_INPUT_ERROR
+    assert _count_async(lib, req, ws=(1 << 24) + 8)[0] == ext.TNR_INPUT_ERROR
+    assert _count_async(lib, req, ws=0)[0] == ext.TNR_INPUT_ERROR
+    code, text = _count_async(lib, req, host=0)
+    assert code == ext.TNR_INPUT_ERROR and "host_result" in text
+
+
+def test_emit_with_no_pairs_is_a_no_op(lib):
+    req = _request()
+    need = lib.tnr_workspace_size(ctypes.byref(req))
+    err = ctypes.create_string_buffer(64)
+    out = ext.Outputs(n_pairs=0)
+    assert lib.tnr_emit(ctypes.byref(req), 1 << 24, need, ctypes.byref(out), None, err,
+                        len(err)) == ext.TNR_OK
+    assert lib.tnr_emit(ctypes.byref(req), 1 << 24, need, None, None, err,
+                        len(err)) == ext.TNR_INPUT_ERROR
+
+
+# Status bits of the device (tonari_amd/csrc/nl_device.h) and the message
+# and exception class each maps to.
+STATUS = [
+    (0, ext.TNR_INPUT_ERROR, "batch_ptr must start at zero"),
+    (1, ext.TNR_INPUT_ERROR, "batch_ptr must end at N_total"),
+    (2, ext.TNR_INPUT_ERROR, "batch_ptr must be nondecreasing"),
+    (3, ext.TNR_INPUT_ERROR, "cell must contain only finite values"),
+    (4, ext.TNR_INPUT_ERROR, "active periodic cell vectors must be linearly independent"),
+    (5, ext.TNR_INPUT_ERROR, "active periodic cell dual is outside the float64 range"),
+    (6, ext.TNR_INPUT_ERROR, "periodic image range exceeds int32 cell shifts"),
+    (7, ext.TNR_INPUT_ERROR, "periodic image count exceeds the 2^24 resource limit"),
+    (8, ext.TNR_INPUT_ERROR, "batched periodic image count exceeds the 2^24 resource limit"),
+    (9, ext.TNR_SEARCH_ERROR, "positions must contain only finite values"),
+    (10, ext.TNR_SEARCH_ERROR, "atom representatives require periodic wraps outside the int32"),
+    (12, ext.TNR_SEARCH_ERROR, "cell_list cannot safely process this structure"),
+    (11, ext.TNR_SEARCH_ERROR, "a cell shift required by the neighbor list exceeds the int32"),
+    (13, ext.TNR_SEARCH_ERROR, "neighbor-list workspace capacity exceeded"),
+]
+
+
+def _finish(lib, flags, pairs=0):
+    host = (ctypes.c_int64 * 4)(flags, pairs, 0, 0)
+    n = ctypes.c_int64(-1)
+    err = ctypes.create_string_buffer(256)
+    code = lib.tnr_count_finish(host, ctypes.byref(n), err, len(err))
+    return code, err.value.decode(), n.value
+
+
+@pytest.mark.parametrize("bit, code, message", STATUS)
+def test_status_words_map_to_reference_errors(lib, bit, code, message):
+    got, text, _ = _finish(lib, 1 << bit)
+    assert got == code
+    assert text.startswith(message)
+
+
+def test_status_priority_follows_reference_order(lib):
+    # Several faults at once report the first in the reference's order.
+    for k in range(len(STATUS) - 1):
+        bits = sum(1 << b for b, _, _ in STATUS[k:])
+        code, text, _ = _finish(lib, bits)
+        assert text.startswith(STATUS[k][2]) and code == STATUS[k][1]
+
+
+def test_finish_reports_pair_count(lib):
+    code, text, n = _finish(lib, 0, 12345)
+    assert code == ext.TNR_OK and n == 12345
