@@ -109,7 +109,7 @@ def time_phases(cfg, t, reps: int):
     )
     ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    host = torch.empty(4, dtype=torch.int64, pin_memory=True)
+    host = torch.empty(8, dtype=torch.int64, pin_memory=True)
     err = ctypes.create_string_buffer(512)
     stream = torch.cuda.current_stream(dev).cuda_stream
     count_ms, emit_ms = [], []
@@ -134,7 +134,7 @@ def time_phases(cfg, t, reps: int):
             outs = {q: torch.empty(shapes[q][0], dtype=shapes[q][1], device=dev)
                     for q in set(quantities)}
         ptr = lambda q: outs[q].data_ptr() if q in outs else None  # noqa: E731
-        o = Outputs(n_pairs=E, plan=int(host[3]), pairs=ptr("P"), shifts=ptr("S"),
+        o = Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[7]), pairs=ptr("P"), shifts=ptr("S"),
                     distances=ptr("d"), vectors=ptr("D"), sources=ptr("i"), targets=ptr("j"))
         # EMIT_BATCH back-to-back launches keep the queue full, so the
         # interval is kernel time rather than host submission latency.

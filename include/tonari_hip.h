@@ -40,12 +40,16 @@
 extern "C" {
 #endif
 
-#define TNR_ABI_VERSION 1
+#define TNR_ABI_VERSION 2
 
 #define TNR_OK 0
 #define TNR_INPUT_ERROR 1
 #define TNR_SEARCH_ERROR 2
 #define TNR_DEVICE_ERROR 3
+
+/* Slots of host_result: status flags, E, total periodic images, plan mask,
+ * total cell-list bins, two internal tickets, total cell-list tasks. */
+#define TNR_HOST_RESULT_SLOTS 8
 
 #define TNR_FLOAT32 0
 #define TNR_FLOAT64 1
@@ -75,7 +79,8 @@ typedef struct tnr_request {
 /* Output buffers for tnr_emit; any pointer may be NULL (not requested). */
 typedef struct tnr_outputs {
     int64_t n_pairs;    /* E returned by tnr_count */
-    int64_t plan;       /* host_result[3] of tnr_count (kernel families in use); 0 = all */
+    int64_t plan;       /* host_result[3] of tnr_count (kernel families in use) */
+    int64_t n_tasks;    /* host_result[7] of tnr_count (cell-list tasks) */
     int64_t* pairs;     /* P: int64[E][2] (source, target) */
     int32_t* shifts;    /* S: int32[E][3] */
     void* distances;    /* d: T[E] */
@@ -96,8 +101,8 @@ size_t tnr_workspace_size(const tnr_request* req);
 /*
  * Validates the request on the device, builds per-structure geometry and the
  * cell-list bins, counts pairs per source and scans the counts.  Copies the
- * status words into `host_result` (pinned host memory, at least 4 int64:
- * status flags, E, total periodic images, plan mask) and synchronises
+ * status words into `host_result` (pinned host memory of
+ * TNR_HOST_RESULT_SLOTS int64) and synchronises
  * `stream`; *n_pairs receives E.  Equivalent to tnr_count_async followed by
  * hipStreamSynchronize(stream) and tnr_count_finish.
  */

@@ -61,7 +61,8 @@ def test_struct_layouts_match_header():
     # offsets of tnr_request / tnr_outputs as laid out by the C compiler
     assert ctypes.sizeof(ext.Request) == 80
     assert ext.Request.cutoff.offset == 56 and ext.Request.stencil_reach.offset == 76
-    assert ctypes.sizeof(ext.Outputs) == 64 and ext.Outputs.targets.offset == 56
+    assert ctypes.sizeof(ext.Outputs) == 72 and ext.Outputs.targets.offset == 64
+    assert ext.Outputs.n_tasks.offset == 16
 
 
 def _request(**kw) -> ext.Request:
@@ -152,11 +153,12 @@ STATUS = [
     (12, ext.TNR_SEARCH_ERROR, "cell_list cannot safely process this structure"),
     (11, ext.TNR_SEARCH_ERROR, "a cell shift required by the neighbor list exceeds the int32"),
     (13, ext.TNR_SEARCH_ERROR, "neighbor-list workspace capacity exceeded"),
+    (14, ext.TNR_SEARCH_ERROR, "a device-wide scan of the neighbor search did not complete"),
 ]
 
 
 def _finish(lib, flags, pairs=0):
-    host = (ctypes.c_int64 * 4)(flags, pairs, 0, 0)
+    host = (ctypes.c_int64 * 8)(flags, pairs, 0, 0, 0, 0, 0, 0)
     n = ctypes.c_int64(-1)
     err = ctypes.create_string_buffer(256)
     code = lib.tnr_count_finish(host, ctypes.byref(n), err, len(err))

@@ -14,7 +14,8 @@ from functools import lru_cache
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
+HOST_RESULT_SLOTS = 8
 
 TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR = 0, 1, 2, 3
 ALGORITHMS = {"auto": 0, "brute_force": 1, "cell_list": 2}
@@ -55,6 +56,7 @@ class Outputs(ctypes.Structure):
     _fields_ = [
         ("n_pairs", ctypes.c_int64),
         ("plan", ctypes.c_int64),
+        ("n_tasks", ctypes.c_int64),
         ("pairs", ctypes.c_void_p),
         ("shifts", ctypes.c_void_p),
         ("distances", ctypes.c_void_p),

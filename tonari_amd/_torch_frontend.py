@@ -22,6 +22,7 @@ from torch import Tensor
 
 from ._extensions import (
     ALGORITHMS,
+    HOST_RESULT_SLOTS,
     TNR_INPUT_ERROR,
     TNR_OK,
     Outputs,
@@ -155,7 +156,7 @@ def neighbor_list_hip(
         stream = torch.cuda.current_stream(device).cuda_stream
         ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-        host = torch.empty(4, dtype=torch.int64, pin_memory=True)
+        host = torch.empty(HOST_RESULT_SLOTS, dtype=torch.int64, pin_memory=True)
         n_pairs = ctypes.c_int64(0)
         code = lib.tnr_count(
             ctypes.byref(req), workspace.data_ptr(), ws_bytes, host.data_ptr(), stream,
@@ -186,6 +187,7 @@ def neighbor_list_hip(
             ptrs = Outputs(
                 n_pairs=count,
                 plan=int(host[3]),
+                n_tasks=int(host[7]),
                 pairs=out["P"].data_ptr() if "P" in out else None,
                 shifts=out["S"].data_ptr() if "S" in out else None,
                 distances=out["d"].data_ptr() if "d" in out else None,

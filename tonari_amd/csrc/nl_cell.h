@@ -1,0 +1,719 @@
+// Cell-list query kernels: the stencil walk over the bins of a structure in
+// a counting flavour (k_cell_count: pairs per source, persistent grid that
+// also counts the brute-force structures) and an emitting flavour
+// (k_cell_emit: writes i/j/P/S/d/D at the scanned offsets).
+//
+// Work unit: one source bin per wave.  Its stencil (neighbouring bins with
+// their periodic images) is flattened into candidates; up to CH chunks of 64
+// candidates at a time are gathered into registers as image positions plus a
+// 32-bit identity key, and the bin's sources are broadcast one at a time
+// against them.  Stencils with more chunks than CH take several register
+// passes; stencils with more than kMapCap candidates take the slow path.
+//
+// Reference: the cell-list query of csrc/torch/neighbors_cell_cuda.cu:294-442
+// (one warp per source walking linked lists) and csrc/core/neighbors_cpu.cpp:
+// 515-584; both apply the public predicate of neighbors_cpu.cpp:247-261.
+// Here a fused broad-phase distance classifies a candidate as inside
+// (d2 < inner2), outside (d2 >= outer2) or in the thin band between, which
+// the public predicate decides (cell_decide).  Both passes make the same
+// decisions: they run the same instructions on the same data.
+#pragma once
+
+#include "nl_query.h"
+
+namespace tnr {
+
+constexpr int kMapCap = kMaskWords * kWave;  // candidates whose piece is mapped in LDS
+constexpr int kListCap = 1024;               // emit: compacted hits per flush
+
+// Chunks of 64 candidates held in registers per pass (at most).
+template <typename T>
+struct RegChunks;
+template <>
+struct RegChunks<float> {
+    static constexpr int value = 16;
+};
+template <>
+struct RegChunks<double> {
+    static constexpr int value = 8;
+};
+
+// Stencil of one source bin, one per wave in LDS.
+struct StencilLds {
+    int pre[kPieceCap + 1];        // exclusive prefix of piece lengths
+    int delta[kPieceCap];          // binned index = candidate index + delta
+    int kid[kPieceCap];            // packed image shift (k + 512 per 10 bits)
+    unsigned char piece[kMapCap];  // piece of each candidate (when C <= kMapCap)
+};
+
+__device__ __forceinline__ int pack_k(int kx, int ky, int kz) {
+    return (kx + 512) | ((ky + 512) << 10) | ((kz + 512) << 20);
+}
+__device__ __forceinline__ void unpack_k(int v, int& kx, int& ky, int& kz) {
+    kx = (v & 1023) - 512;
+    ky = ((v >> 10) & 1023) - 512;
+    kz = ((v >> 20) & 1023) - 512;
+}
+
+// Broad-phase translation k . cell of image k; every pass that needs it
+// evaluates this same expression, so the broad-phase decisions agree.
+template <typename T>
+__device__ __forceinline__ void image_translation(int kk, const T c[9], T& tx, T& ty, T& tz) {
+    using O = Ops<T>;
+    int kx, ky, kz;
+    unpack_k(kk, kx, ky, kz);
+    const T fx = (T)kx, fy = (T)ky, fz = (T)kz;
+    tx = O::fma_(fz, c[6], O::fma_(fy, c[3], O::mul(fx, c[0])));
+    ty = O::fma_(fz, c[7], O::fma_(fy, c[4], O::mul(fx, c[1])));
+    tz = O::fma_(fz, c[8], O::fma_(fy, c[5], O::mul(fx, c[2])));
+}
+
+// Wave-uniform description of one source bin of a cell-list structure.
+template <typename T>
+struct CellBin {
+    int b;            // structure
+    int sb, se;       // binned sources [sb, se)
+    int C;            // flattened stencil candidates
+    int nch;          // chunks of 64 candidates
+    int npieces;
+    T c[9];           // cell (rows are cell vectors)
+    T outer2, inner2, cut2;
+    bool wrapped, diagonal;
+};
+
+// Structure of the last task looked up by this wave: tasks [lo, hi) belong
+// to structure b.  Consecutive tasks of a wave usually share a structure.
+struct StructCache {
+    int b;
+    int64_t lo, hi;
+};
+
+__device__ __forceinline__ int structure_of_task(const int64_t* off, int64_t nb, int64_t g,
+                                                 StructCache& sc) {
+    if (g >= sc.lo && g < sc.hi) return sc.b;
+    int64_t lo = 0, hi = nb;
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (off[mid] <= g) lo = mid; else hi = mid;
+    }
+    sc.b = (int)lo;
+    sc.lo = off[lo];
+    sc.hi = off[lo + 1];
+    return sc.b;
+}
+
+// Loads the structure and bin of a cell-list task and builds the bin's
+// stencil for the sources of the task: r.parts waves split a bin's sources,
+// each building the stencil itself.  Pieces are runs of
+// consecutive z-bins of one (x, y) row with one periodic image k, one lane
+// per piece; pieces with |k_a| > R_a are dropped, which keeps exactly the
+// reference's image box.  Fills the piece table of st and resolves the
+// piece of every candidate into st.piece when C <= kMapCap.  Returns false when the bin holds no
+// source.
+template <typename T>
+__device__ __forceinline__ bool cell_bin(const QueryArgs<T>& a, int64_t task, StructCache& sc,
+                                         CellBin<T>& cb, StencilLds& st) {
+    const int lane = lane_id();
+    cb.b = structure_of_task(a.struct_task_off, a.nb, task, sc);
+    const StructRec& r = a.recs[cb.b];
+    const int parts = r.parts;
+    const unsigned local = (unsigned)(task - sc.lo);  // tasks of a structure fit in 32 bits
+    const unsigned lbin = local / (unsigned)parts;
+    const int part = (int)(local - lbin * (unsigned)parts);
+    const int64_t g = r.bin0 + lbin;
+    const int sb = uniform(a.bin_start[g]), se = uniform(a.bin_start[g + 1]);
+    // sources of this part: the part-th share of the bin's sources
+    const int q = (se - sb + parts - 1) / parts;
+    cb.sb = sb + part * q;
+    cb.se = min(se, cb.sb + q);
+    if (cb.sb >= cb.se) return false;
+    const T* cell = a.cells + 9 * cb.b;
+#pragma unroll
+    for (int e = 0; e < 9; ++e) cb.c[e] = cell[e];
+    cb.outer2 = (T)r.outer2;
+    cb.inner2 = (T)r.inner2;
+    cb.cut2 = (T)r.cut2;
+    cb.wrapped = r.any_wrap != 0;
+    cb.diagonal = r.diagonal != 0;
+    const int nx = r.nb[0], ny = r.nb[1], nz = r.nb[2];  // each at least 1
+    const int Kx = r.reach[0], Ky = r.reach[1], Kz = r.reach[2];
+    const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
+    const bool perx = r.active & 1, pery = r.active >> 1 & 1, perz = r.active >> 2 & 1;
+    const int zs = r.zseg;
+    const int iz = (int)(lbin % (unsigned)nz);
+    const unsigned rest = lbin / (unsigned)nz;
+    const int iy = (int)(rest % (unsigned)ny);
+    const int ix = (int)(rest / (unsigned)ny);
+    const int RY = 2 * Ky + 1;
+    const int npieces = (2 * Kx + 1) * RY * zs;
+    cb.npieces = npieces;
+    const int* bstart = a.bin_start + r.bin0;
+    // p / zs and row / RY through a float reciprocal: p < 2^8 and divisors
+    // below 2^8, so (p + 1/2) / d lies at least 1/512 from an integer while
+    // the float error stays below 2^-15.
+    const float rzs = 1.0f / (float)zs, rry = 1.0f / (float)RY;
+    const int zlo = iz - Kz, zhi = iz + Kz;
+    int kz0 = 0;  // image of the lowest stencil z-bin (zlo < nz)
+    if (perz)
+        for (int zz = zlo; zz < 0; zz += nz) --kz0;
+    // clear the piece marks
+#pragma unroll
+    for (int q = 0; q < kMapCap / (8 * kWave); ++q)
+        reinterpret_cast<unsigned long long*>(st.piece)[q * kWave + lane] = 0ull;
+
+    int carry = 0;
+    for (int base = 0; base < npieces; base += kWave) {
+        const int p = base + lane;
+        int len = 0, start = 0, kx = 0, ky = 0, kz = 0;
+        if (p < npieces) {
+            const int row = (int)(((float)p + 0.5f) * rzs);
+            const int seg = p - row * zs;
+            const int rx = (int)(((float)row + 0.5f) * rry);
+            int jx = ix + rx - Kx, jy = iy + (row - rx * RY) - Ky;
+            bool ok;
+            if (perx) {
+                while (jx < 0) { jx += nx; --kx; }
+                while (jx >= nx) { jx -= nx; ++kx; }
+                ok = abs(kx) <= R0;
+            } else {
+                ok = jx >= 0 && jx < nx;
+            }
+            if (pery) {
+                while (jy < 0) { jy += ny; --ky; }
+                while (jy >= ny) { jy -= ny; ++ky; }
+                ok = ok && abs(ky) <= R1;
+            } else {
+                ok = ok && jy >= 0 && jy < ny;
+            }
+            int z0, z1;
+            if (perz) {
+                kz = kz0 + seg;
+                const int zbeg = seg == 0 ? zlo : kz * nz;
+                const int zend = min(zhi, (kz + 1) * nz - 1);
+                ok = ok && zbeg <= zhi && abs(kz) <= R2;
+                z0 = zbeg - kz * nz;
+                z1 = zend - kz * nz;
+            } else {
+                z0 = max(0, zlo);
+                z1 = min(nz - 1, zhi);
+                ok = ok && seg == 0 && z0 <= z1;
+            }
+            if (ok) {
+                const int rowbase = (jx * ny + jy) * nz;
+                start = bstart[rowbase + z0];
+                len = bstart[rowbase + z1 + 1] - start;
+            }
+        }
+        const int inc = wave_inclusive_scan_i32(len);
+        if (p < npieces) {
+            const int ex = carry + inc - len;
+            const int kk = pack_k(kx, ky, kz);
+            st.pre[p] = ex;
+            st.delta[p] = start - ex;
+            st.kid[p] = kk;
+            if (len > 0 && ex < kMapCap) st.piece[ex] = (unsigned char)p;
+        }
+        carry += __builtin_amdgcn_readlane(inc, kWave - 1);
+    }
+    if (lane == 0) st.pre[npieces] = carry;
+    cb.C = uniform(carry);
+    cb.nch = (cb.C + kWave - 1) / kWave;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (cb.C <= kMapCap) {
+        // piece of candidate v: running maximum of the piece marks up to v
+        int run = 0;
+        for (int j = 0; j < cb.nch; ++j) {
+            const int v = j * kWave + lane;
+            const int p = max(wave_inclusive_max_i32((int)st.piece[v]), run);
+            run = __builtin_amdgcn_readlane(p, kWave - 1);
+            st.piece[v] = (unsigned char)p;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    }
+    return true;
+}
+
+// The band between inner2 and outer2: decided by the public predicate on the
+// original positions and the output shift.
+template <typename T>
+__device__ __forceinline__ bool cell_band(const QueryArgs<T>& a, int tid, int kk, int bidx,
+                                          T sx, T sy, T sz, int si, const CellBin<T>& cb) {
+    int kx, ky, kz;
+    unpack_k(kk, kx, ky, kz);
+    T ps[3], pt[3];
+    long long S0 = kx, S1 = ky, S2 = kz;
+    if (cb.wrapped) {
+        const int4 wt = a.atom_wrap[tid];
+        const int4 ws = a.atom_wrap[si];
+        S0 += (long long)ws.x - wt.x;
+        S1 += (long long)ws.y - wt.y;
+        S2 += (long long)ws.z - wt.z;
+#pragma unroll
+        for (int cc = 0; cc < 3; ++cc) {
+            ps[cc] = a.pos[3 * (int64_t)si + cc];
+            pt[cc] = a.pos[3 * (int64_t)tid + cc];
+        }
+    } else {
+        const Vec4<T> rec = a.binned[bidx];
+        ps[0] = sx; ps[1] = sy; ps[2] = sz;
+        pt[0] = rec.x; pt[1] = rec.y; pt[2] = rec.z;
+    }
+    T D[3];
+    return public_vector(ps, pt, S0, S1, S2, cb.c, D) < cb.cut2;
+}
+
+template <typename T>
+__device__ __forceinline__ void shift_check(const QueryArgs<T>& a, int tid, int kk, int si) {
+    int kx, ky, kz;
+    unpack_k(kk, kx, ky, kz);
+    const int4 wt = a.atom_wrap[tid];
+    const int4 ws = a.atom_wrap[si];
+    if (!(fits_i32((long long)kx - wt.x + ws.x) && fits_i32((long long)ky - wt.y + ws.y) &&
+          fits_i32((long long)kz - wt.z + ws.z)))
+        atomicOr(a.status + SS_FLAGS, ST_SHIFT_RANGE);
+}
+
+// Full decision for candidate v (piece p) of the stencil against the source
+// at (sx, sy, sz) with index si: broad phase, identity and band.  Used by the
+// rare paths; its broad phase is the register path's, operation for operation.
+template <typename T, int MODE>
+__device__ __forceinline__ bool cell_decide(const QueryArgs<T>& a, const StencilLds& st,
+                                            const CellBin<T>& cb, int p, int v, T sx, T sy,
+                                            T sz, int si, int* tid_out, int* kk_out,
+                                            Vec4<T>* rec_out) {
+    using O = Ops<T>;
+    const int bidx = v + st.delta[p];
+    const Vec4<T> rec = a.binned[bidx];
+    const int tid = as_idx(rec.w);
+    const int kk = st.kid[p];
+    *tid_out = tid;
+    *kk_out = kk;
+    *rec_out = rec;
+    int kx, ky, kz;
+    unpack_k(kk, kx, ky, kz);
+    T trx, trY, trz;
+    image_translation(kk, cb.c, trx, trY, trz);
+    const T dx = O::sub(O::add(rec.x, trx), sx), dy = O::sub(O::add(rec.y, trY), sy),
+            dz = O::sub(O::add(rec.z, trz), sz);
+    const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
+    const bool kzero = kk == pack_k(0, 0, 0);
+    const bool zsf = tid == si && kzero;
+    bool ok = (d2 < cb.outer2 || zsf) &&
+              identity_ok<MODE>(si, tid, kzero, lex_negative(kx, ky, kz));
+    if (ok && !zsf && !(d2 < cb.inner2)) ok = cell_band(a, tid, kk, bidx, sx, sy, sz, si, cb);
+    return ok;
+}
+
+// Candidate v of a stencil too large for the piece map: its piece by binary
+// search over the piece starts.
+__device__ __forceinline__ int stencil_piece(const StencilLds& st, int v, int npieces) {
+    int top = 1;
+    while (top * 2 <= npieces) top *= 2;
+    int p = 0;
+    for (int step = top; step > 0; step >>= 1) {
+        const int q = p + step;
+        if (q < npieces && st.pre[q] <= v) p = q;
+    }
+    return p;
+}
+
+// Writes one kept candidate of source si: the output shift is the image k
+// corrected by the representatives' wraps; D uses the original positions.
+template <typename T>
+__device__ __forceinline__ void cell_write(const QueryArgs<T>& a, long long o, int si, int tid,
+                                           int kk, T rx, T ry, T rz, T sx, T sy, T sz,
+                                           const CellBin<T>& cb) {
+    int kx, ky, kz;
+    unpack_k(kk, kx, ky, kz);
+    T ps[3] = {sx, sy, sz}, pt[3] = {rx, ry, rz};
+    if (cb.wrapped) {
+        const int4 wt = a.atom_wrap[tid];
+        const int4 ws = a.atom_wrap[si];
+        kx = shift_i32(kx, wt.x, ws.x);
+        ky = shift_i32(ky, wt.y, ws.y);
+        kz = shift_i32(kz, wt.z, ws.z);
+#pragma unroll
+        for (int cc = 0; cc < 3; ++cc) {
+            ps[cc] = a.pos[3 * (int64_t)si + cc];
+            pt[cc] = a.pos[3 * (int64_t)tid + cc];
+        }
+    }
+    write_hit(a, o, si, tid, kx, ky, kz, ps, pt, cb.c, cb.diagonal);
+}
+
+// Stencils with more than kMapCap candidates (coarse grids): one chunk at a
+// time, the piece of each candidate found by binary search.
+template <typename T, int MODE, bool EMIT>
+__device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLds& st,
+                                       const CellBin<T>& cb) {
+    const int lane = lane_id();
+    for (int sg = cb.sb; sg < cb.se; sg += kWave) {
+        const int ns = min(kWave, cb.se - sg);
+        Vec4<T> sq = {T(0), T(0), T(0), T(0)};
+        int sidx = 0;
+        if (lane < ns) {
+            sq = a.binned[sg + lane];
+            sidx = as_idx(sq.w);
+        }
+        long long acc = 0, cur = 0;
+        if (EMIT && lane < ns) cur = a.offsets[sidx];
+        for (int j = 0; j < cb.nch; ++j) {
+            const int v = j * kWave + lane;
+            const bool valid = v < cb.C;
+            const int p = valid ? stencil_piece(st, v, cb.npieces) : 0;
+            for (int gi = 0; gi < ns; ++gi) {
+                const T sx = read_lane(sq.x, gi), sy = read_lane(sq.y, gi),
+                        sz = read_lane(sq.z, gi);
+                const int si = read_lane(sidx, gi);
+                int tid = 0, kk = 0;
+                Vec4<T> rec = {T(0), T(0), T(0), T(0)};
+                const bool ok = valid && cell_decide<T, MODE>(a, st, cb, p, v, sx, sy, sz, si,
+                                                              &tid, &kk, &rec);
+                const unsigned long long m = ballot(ok);
+                if (!EMIT) {
+                    if (cb.wrapped && ok) shift_check(a, tid, kk, si);
+                    if (lane == gi) acc += __popcll(m);
+                } else if (m) {
+                    const long long base = read_lane(cur, gi);
+                    if (ok)
+                        cell_write(a, base + lanes_below(m), si, tid, kk, rec.x, rec.y, rec.z, sx,
+                                   sy, sz, cb);
+                    if (lane == gi) cur += __popcll(m);
+                }
+            }
+        }
+        if (!EMIT && lane < ns) a.counts[sidx] = acc;
+    }
+}
+
+// Candidates of one register pass: chunks c0 .. c0 + NC - 1 of the stencil,
+// lane l of chunk j holding candidate (c0 + j) * 64 + l.  Slots past the
+// last candidate hold a far position that fails every test.
+template <typename T, int NC>
+struct Chunks {
+    T x[NC], y[NC], z[NC];  // image positions (broad phase)
+    unsigned key[NC];       // identity keys
+};
+
+template <typename T, int MODE, int NC>
+__device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const StencilLds& st,
+                                            const CellBin<T>& cb, int c0, Chunks<T, NC>& cd) {
+    using O = Ops<T>;
+    const int lane = lane_id();
+    const T far = T(1e18);
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        cd.x[j] = cd.y[j] = cd.z[j] = far;
+        cd.key[j] = MODE == 0 ? ~0u : 0u;
+        if (c0 + j < cb.nch) {
+            const int v = (c0 + j) * kWave + lane;
+            if (v < cb.C) {
+                const int p = st.piece[v];
+                const Vec4<T> rec = a.binned[v + st.delta[p]];
+                const int kk = st.kid[p];
+                int kx, ky, kz;
+                unpack_k(kk, kx, ky, kz);
+                cd.key[j] = identity_key<MODE>(as_idx(rec.w), kk == pack_k(0, 0, 0),
+                                               lex_negative(kx, ky, kz));
+                T tx, ty, tz;
+                image_translation(kk, cb.c, tx, ty, tz);
+                cd.x[j] = O::add(rec.x, tx);
+                cd.y[j] = O::add(rec.y, ty);
+                cd.z[j] = O::add(rec.z, tz);
+            }
+        }
+    }
+}
+
+// Full decisions for chunk jc of the stencil against one source: used when
+// the broad phase left a candidate of the chunk in the band.  Rare: the band
+// is about 1e-3 of the cutoff wide.
+template <typename T, int MODE>
+__device__ __forceinline__ unsigned long long band_chunk(const QueryArgs<T>& a,
+                                                         const StencilLds& st,
+                                                         const CellBin<T>& cb, int jc, T sx,
+                                                         T sy, T sz, int si) {
+    const int v = jc * kWave + lane_id();
+    bool ok = false;
+    if (v < cb.C) {
+        int tid, kk;
+        Vec4<T> rec;
+        ok = cell_decide<T, MODE>(a, st, cb, st.piece[v], v, sx, sy, sz, si, &tid, &kk, &rec);
+    }
+    return __builtin_amdgcn_ballot_w64(ok);
+}
+
+// Hit masks of one source (sx, sy, sz, si) against the NC chunks of a pass:
+// lane j of mv receives the mask of chunk c0 + j; returns the hit count.  The
+// fused broad phase gives the inside and band masks of every chunk without
+// branches; the rare chunks with band candidates are then decided in full.
+template <typename T, int MODE, int NC>
+__device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLds& st,
+                                          const CellBin<T>& cb, const Chunks<T, NC>& cd, int c0,
+                                          T sx, T sy, T sz, int si, unsigned long long& mv) {
+    using O = Ops<T>;
+    const int lane = lane_id();
+    unsigned band = 0;
+    int cnt = 0;
+    mv = 0;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+        const T dx = O::sub(cd.x[j], sx), dy = O::sub(cd.y[j], sy), dz = O::sub(cd.z[j], sz);
+        const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
+        unsigned long long mk = __builtin_amdgcn_ballot_w64(d2 < cb.outer2);
+        if constexpr (MODE != 1) mk &= __builtin_amdgcn_ballot_w64(identity_pass<MODE>(cd.key[j], si));
+        const unsigned long long mi = __builtin_amdgcn_ballot_w64(d2 < cb.inner2);
+        const unsigned long long m = mk & mi;
+        band |= (mk & ~mi) ? (1u << j) : 0u;
+        cnt += __popcll(m);
+        if (lane == j) mv = m;
+    }
+    if (band) {
+        for (int j = 0; j < NC; ++j) {
+            if (!((band >> j) & 1u)) continue;
+            const unsigned long long full = band_chunk<T, MODE>(a, st, cb, c0 + j, sx, sy, sz, si);
+            const unsigned long long old = (unsigned long long)read_lane((long long)mv, j);
+            cnt += __popcll(full) - __popcll(old);
+            if (lane == j) mv = full;
+        }
+    }
+    return cnt;
+}
+
+// Counting, register path of one bin: source groups of 64, register passes
+// of NC chunks.  Writes counts[s] and, per source, the hit mask of every
+// chunk (masks[binned index][chunk]) for the emitting pass.
+template <typename T, int MODE, int NC>
+__device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLds& st,
+                                          const CellBin<T>& cb) {
+    const int lane = lane_id();
+    const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
+    for (int sg = cb.sb; sg < cb.se; sg += kWave) {
+        const int ns = min(kWave, cb.se - sg);
+        const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
+        const int sidx = as_idx(sq.w);
+        long long acc = 0;  // lane gi: pairs of source gi so far
+        for (int c0 = 0; c0 < cb.nch; c0 += NC) {
+            Chunks<T, NC> cd;
+            gather_pass<T, MODE, NC>(a, st, cb, c0, cd);
+            const bool store = lane < NC && c0 + lane < cb.nch;
+#pragma unroll 1
+            for (int gi = 0; gi < ns; ++gi) {
+                const T sx = read_lane(sq.x, gi), sy = read_lane(sq.y, gi),
+                        sz = read_lane(sq.z, gi);
+                const int si = read_lane(sidx, gi);
+                unsigned long long mv;  // lane j: hit mask of chunk c0 + j
+                const int cnt = pass_masks<T, MODE, NC>(a, st, cb, cd, c0, sx, sy, sz, si, mv);
+                if (cb.wrapped) {
+                    for (int j = 0; j < NC && c0 + j < cb.nch; ++j) {
+                        const unsigned long long m = (unsigned long long)read_lane((long long)mv, j);
+                        if ((m >> lane) & 1ull) {
+                            const int v = (c0 + j) * kWave + lane;
+                            const int p = st.piece[v];
+                            shift_check(a, as_idx(a.binned[v + st.delta[p]].w), st.kid[p], si);
+                        }
+                    }
+                }
+                if (store) a.masks[(int64_t)(sg + gi) * kMaskWords + c0 + lane] = mv;
+                if (lane == gi) acc += cnt;
+            }
+        }
+        if (lane < ns) a.counts[sidx] = acc;
+    }
+}
+
+// The register path with the fewest chunks per pass that hold the bin's
+// stencil (passes of RegChunks<T> chunks beyond that).
+template <typename T, int MODE>
+__device__ __forceinline__ void count_bin_any(const QueryArgs<T>& a, const StencilLds& st,
+                                              const CellBin<T>& cb) {
+    constexpr int CH = RegChunks<T>::value;
+    if (cb.nch <= 4)
+        count_bin<T, MODE, 4>(a, st, cb);
+    else if (cb.nch <= 8 || CH == 8)
+        count_bin<T, MODE, 8>(a, st, cb);
+    else if (cb.nch <= 12)
+        count_bin<T, MODE, (CH > 12 ? 12 : CH)>(a, st, cb);
+    else
+        count_bin<T, MODE, CH>(a, st, cb);
+}
+
+// Emitting, register path of one bin: no distance tests, the hit masks of
+// the counting pass are decoded.  Sources are taken S = 64 / nch at a time,
+// lane (s, j) holding the mask of chunk j of source s; a wave scan of the
+// mask popcounts places every hit in the wave's LDS list (entry = owner lane
+// << 6 | bit), which is written out in rounds of 64 consecutive pairs.
+template <typename T>
+__device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds& st,
+                                         const CellBin<T>& cb, unsigned short* list) {
+    const int lane = lane_id();
+    const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
+    const int nch = cb.nch;
+    const int S = kWave / nch;
+    // lane = sl * nch + j
+    const int sl = (int)(((float)lane + 0.5f) / (float)nch);
+    const int j = lane - sl * nch;
+    for (int sg = cb.sb; sg < cb.se; sg += kWave) {
+        const int ns = min(kWave, cb.se - sg);
+        const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
+        const int sidx = as_idx(sq.w);
+        const long long cur = lane < ns ? a.offsets[sidx] : 0;  // lane gi: first output of gi
+        auto mask_of = [&](int s0_) -> unsigned long long {
+            const int gi_ = s0_ + sl;
+            return sl < S && gi_ < ns ? a.masks[(int64_t)(sg + gi_) * kMaskWords + j] : 0ull;
+        };
+        unsigned long long m_next = mask_of(0);
+        for (int s0 = 0; s0 < ns; s0 += S) {
+            const int gi = s0 + sl;
+            const unsigned long long m = m_next;
+            if (s0 + S < ns) m_next = mask_of(s0 + S);
+            const int c = __popcll(m);
+            const int incl = wave_inclusive_scan_i32(c);
+            const int pos = incl - c;  // list position of this lane's first hit
+            const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+            // output of list entry r owned by this lane: cur[gi] + (pos - first) + (r - pos)
+            const int first = __shfl(pos, min(sl, S - 1) * nch);
+            const long long ob = __shfl(cur, min(gi, kWave - 1)) - first;
+            const int tag = (min(gi, kWave - 1) << 6) | j;  // owner data: source lane, chunk
+            for (int base = 0; base < total; base += kListCap) {
+                const int L = min(kListCap, total - base);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                {
+                    unsigned long long mm = m;
+                    int r = pos - base;
+                    while (mm) {
+                        const int bit = __builtin_ctzll(mm);
+                        mm &= mm - 1;
+                        if (r >= 0 && r < L) list[r] = (unsigned short)((lane << 6) | bit);
+                        ++r;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                // rounds of 64 entries; the next round's record is loaded ahead.
+                // The owner lookup (a lane shuffle) runs with every lane active.
+                int e = 0, tg = 0, kk = 0;
+                Vec4<T> rec = zero4;
+                auto fetch = [&](int r, int& e_, int& tg_, int& kk_, Vec4<T>& rec_) {
+                    e_ = r < L ? (int)list[r] : 0;
+                    tg_ = __shfl(tag, e_ >> 6);
+                    if (r < L) {
+                        const int v = (tg_ & 63) * kWave + (e_ & 63);
+                        const int p = st.piece[v];
+                        kk_ = st.kid[p];
+                        rec_ = a.binned[v + st.delta[p]];
+                    }
+                };
+                fetch(lane, e, tg, kk, rec);
+                for (int r0 = 0; r0 < L; r0 += kWave) {
+                    int e_n = 0, tg_n = 0, kk_n = 0;
+                    Vec4<T> rec_n = zero4;
+                    if (r0 + kWave < L) fetch(r0 + kWave + lane, e_n, tg_n, kk_n, rec_n);
+                    const int g = tg >> 6;
+                    const long long o = __shfl(ob, e >> 6) + base + r0 + lane;
+                    const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
+                    const int si = __shfl(sidx, g);
+                    if (r0 + lane < L)
+                        cell_write(a, o, si, as_idx(rec.w), kk, rec.x, rec.y, rec.z, sx, sy, sz,
+                                   cb);
+                    e = e_n;
+                    tg = tg_n;
+                    kk = kk_n;
+                    rec = rec_n;
+                }
+            }
+        }
+    }
+}
+
+// Static XCD-aware split of W work items over the waves of a grid: block b
+// runs on XCD b % 8 (the hardware deals blocks round-robin), items are cut
+// into 8 contiguous ranges and the waves of XCD x stride over range x, so
+// neighbouring bins share one L2.
+struct WaveRange {
+    int64_t first, end, step;
+};
+__device__ __forceinline__ WaveRange xcd_range(int64_t W, int wv) {
+    const unsigned nblk = gridDim.x;
+    WaveRange r;
+    if ((nblk & 7u) != 0) {
+        r.first = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+        r.end = W;
+        r.step = (int64_t)nblk * kWavesPerBlock;
+        return r;
+    }
+    const int64_t per = (W + 7) / 8;
+    const int64_t x = blockIdx.x & 7u;
+    r.first = x * per + (int64_t)(blockIdx.x >> 3) * kWavesPerBlock + wv;
+    r.end = min(W, (x + 1) * per);
+    r.step = (int64_t)(nblk >> 3) * kWavesPerBlock;
+    return r;
+}
+
+// Counting pass, persistent grid: every wave walks its share of the
+// (source bin, part) tasks of the cell-list structures, then of the source atoms of the
+// brute-force structures, and writes counts[s] for each source s.  The
+// status word is read once: abort bits only come from earlier kernels.
+template <typename T, int MODE>
+__global__ __launch_bounds__(kBlock) void k_cell_count(
+    QueryArgs<T> a) {
+    __shared__ StencilLds s_st[kWavesPerBlock];
+
+    if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
+    const unsigned long long plan = load_status(a.status + SS_PLAN);
+    const int wv = uniform(threadIdx.x / kWave);
+    StencilLds& st = s_st[wv];
+
+    if (plan & 2) {
+        const WaveRange wr = xcd_range(a.struct_task_off[a.nb], wv);
+        StructCache sc{0, 0, 0};
+        for (int64_t t = wr.first; t < wr.end; t += wr.step) {
+            CellBin<T> cb;
+            if (!cell_bin<T>(a, t, sc, cb, st)) continue;
+            if (cb.C > kMapCap)
+                cell_slow<T, MODE, false>(a, st, cb);
+            else
+                count_bin_any<T, MODE>(a, st, cb);
+        }
+    }
+    if (plan & 1) {
+        const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+        for (int64_t s = (int64_t)blockIdx.x * kWavesPerBlock + wv; s < a.n_atoms; s += nwaves) {
+            const int b = a.atom_struct[s];
+            const StructRec& r = a.recs[b];
+            if (r.algo == ALGO_BRUTE) brute_source<T, MODE, false>(a, (int)s, b, r);
+        }
+    }
+}
+
+static_assert(kMapCap == kMaskWords * kWave, "one mask word per chunk of the piece map");
+
+// Emitting pass: one wave per (source bin, part) task, blocks mapped
+// XCD-aware (block b runs on XCD b % 8; XCD x takes the x-th eighth of the
+// tasks).  The grid covers the tasks of the count (out->n_tasks), so the
+// kernel can run again on the same workspace.
+template <typename T, int MODE>
+__global__ __launch_bounds__(kBlock) void k_cell_emit(
+    QueryArgs<T> a) {
+    __shared__ StencilLds s_st[kWavesPerBlock];
+    __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
+
+    if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
+    const int wv = uniform(threadIdx.x / kWave);
+    const WaveRange wr = xcd_range(a.struct_task_off[a.nb], wv);
+    const int64_t t = wr.first;
+    if (t >= wr.end) return;
+    StencilLds& st = s_st[wv];
+    StructCache sc{0, 0, 0};
+    CellBin<T> cb;
+    if (!cell_bin<T>(a, t, sc, cb, st)) return;
+    if (cb.C > kMapCap)
+        cell_slow<T, MODE, true>(a, st, cb);
+    else
+        emit_bin<T>(a, st, cb, s_list[wv]);
+}
+
+}  // namespace tnr

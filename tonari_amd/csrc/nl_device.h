@@ -16,7 +16,17 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kPieceCap = 192;            // stencil pieces per source bin
-constexpr int kStencilReach = 2;          // bins per cutoff along each grid axis
+// Automatic stencil reach: the smallest reach whose estimated stencil holds
+// at most this many candidates (one register pass of the counting kernel
+// holds 1024 float or 512 double candidates).
+template <typename T>
+struct kAutoCandidates {
+    static constexpr double value = 768.0;
+};
+template <>
+struct kAutoCandidates<double> {
+    static constexpr double value = 512.0;
+};
 constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
 constexpr int64_t kAutoBruteCandidates = 4096;     // N_b * images at or below: brute force
 
@@ -36,6 +46,7 @@ enum StatusBit : unsigned long long {
     ST_SHIFT_RANGE = 1ull << 11,
     ST_CELL_UNSAFE = 1ull << 12,
     ST_CAPACITY = 1ull << 13,
+    ST_SCAN_STALL = 1ull << 14,
 };
 // Bits that make every later kernel skip its work (inputs are unusable).
 constexpr unsigned long long kAbortBits =
@@ -49,6 +60,9 @@ enum StatusSlot : int {
     SS_TOTAL_IMAGES = 2,
     SS_PLAN = 3,          // bit 0: some brute-force structure, bit 1: some cell-list one
     SS_TOTAL_BINS = 4,
+    SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
+    SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
+    SS_TOTAL_TASKS = 7,   // cell-list tasks (bin parts) of the batch
     SS_SLOTS = 64,
 };
 
@@ -63,6 +77,8 @@ struct alignas(16) StructRec {
     int64_t nimages;
     int64_t bin0;
     int64_t nbins;
+    int64_t task0;       // first cell-list task (bin part) of the structure
+    int32_t parts;       // tasks per bin: waves that split a bin's sources
     double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
     double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
     double lo[3];        // grid origin (inactive axes)
@@ -74,6 +90,8 @@ struct alignas(16) StructRec {
     unsigned long long umin[3], umax[3];   // ordered keys of grid-coordinate bounds
     unsigned long long cmin[3], cmax[3];   // ordered keys of Cartesian wrapped bounds
     unsigned long long maxp;               // bits of max_c |p_c| (non-negative double)
+    unsigned long long flags;   // input-error bits found by k_setup for this structure
+    int64_t img_total;   // images this structure adds to the batch total (0 if invalid)
     uint32_t maxw;       // max_a |wrap_a| (2^31 fits)
     int32_t reps[3];     // image repeats R_a
     int32_t nb[3];       // bins per axis
@@ -93,19 +111,23 @@ struct alignas(16) BlockPartial {
     unsigned long long maxw;
 };
 
-constexpr int kMaxChunks = 8;   // candidate chunks of 64 held in registers
-
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
-    size_t status, structs, struct_bins, struct_bin_off, atom_struct, atom_wrap, atom_q,
+    size_t status, structs, struct_bins, struct_bin_off, struct_tasks, struct_task_off,
+        atom_struct, atom_wrap, atom_q,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials,
-        block_partials, masks, total;
-    int64_t cap_bins, n_partials, n_atom_blocks;
+        block_partials, masks, tiles_bins, tiles_pairs, total;
+    int64_t cap_bins, n_partials, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
 };
+
+// Hit masks stored per cell-list source: one 64-bit word per chunk of 64
+// stencil candidates, for stencils of up to kMaskWords * 64 candidates.
+constexpr int kMaskWords = 32;
 
 constexpr int64_t kScanItems = 8;
 constexpr int64_t kScanChunk = kBlock * kScanItems;
+constexpr int64_t kScanTile = kScanChunk;  // items per tile of the single-pass scan
 
 inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -124,6 +146,8 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.structs = take(sizeof(StructRec) * (size_t)(b > 0 ? b : 1));
     L.struct_bins = take(sizeof(int64_t) * (size_t)(b + 1));
     L.struct_bin_off = take(sizeof(int64_t) * (size_t)(b + 2));
+    L.struct_tasks = take(sizeof(int64_t) * (size_t)(b + 1));
+    L.struct_task_off = take(sizeof(int64_t) * (size_t)(b + 2));
     L.atom_struct = take(sizeof(int32_t) * (size_t)(n + 1));
     L.atom_wrap = take(sizeof(int32_t) * 4 * (size_t)(n + 1));
     L.atom_q = take(tsize * 4 * (size_t)(n + 1));
@@ -137,7 +161,11 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.partials = take(sizeof(int64_t) * (size_t)(L.n_partials + 1));
     L.n_atom_blocks = (n + kBlock - 1) / kBlock;
     L.block_partials = take(sizeof(BlockPartial) * (size_t)(L.n_atom_blocks + 1));
-    L.masks = take(sizeof(unsigned long long) * kMaxChunks * (size_t)(n + 1));
+    L.masks = take(sizeof(unsigned long long) * kMaskWords * (size_t)(n + 1));
+    L.n_tiles_bins = (L.cap_bins + kScanTile - 1) / kScanTile + 1;
+    L.n_tiles_pairs = (n + kScanTile - 1) / kScanTile + 1;
+    L.tiles_bins = take(sizeof(unsigned long long) * (size_t)L.n_tiles_bins);
+    L.tiles_pairs = take(sizeof(unsigned long long) * (size_t)L.n_tiles_pairs);
     L.total = o;
     return L;
 }

@@ -1,7 +1,7 @@
 // Prologue kernels of a neighbor-list request: per-structure periodic
 // metadata (k_setup), per-atom wraps and reductions (k_atoms), per-structure
 // margins / algorithm / bin grid (k_plan), and the counting sort of cell-list
-// atoms into bins (k_bin, k_scatter).
+// atoms into bins (k_bin, k_scatter; the scans are in nl_scan.h).
 #pragma once
 
 #include "nl_math.h"
@@ -98,20 +98,23 @@ __device__ inline void normalize3(double v[3]) {
 // (geometry.cpp:123-219) and the grid frame used for binning.  Grid rows:
 // dual columns on periodic axes (the grid coordinate is the fractional
 // coordinate) and orthonormal complements of the periodic rows elsewhere.
+// Block 0 first zeroes the status block of the request (every later kernel
+// reads it).  Per-structure errors go to the record (k_plan folds them into
+// the status words), so no thread races the zeroing.
 template <typename T>
 __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb,
                         int64_t n_atoms, double cutoff, StructRec* recs,
                         unsigned long long* status) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    unsigned long long* flags = status + SS_FLAGS;
-    if (nb == 0) {
-        if (b == 0) {
+    if (blockIdx.x == 0) {
+        for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
+        __syncthreads();
+        if (nb == 0 && threadIdx.x == 0) {
             unsigned long long st = 0;
             if (bp[0] != 0) st |= ST_BP_START;
             if (bp[0] != n_atoms) st |= ST_BP_END;
-            if (st) atomicOr(flags, st);
+            status[SS_FLAGS] = st;
         }
-        return;
     }
     if (b >= nb) return;
     StructRec& r = recs[b];
@@ -125,6 +128,8 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
     r.natoms = natoms;
     r.bin0 = 0;
     r.nbins = 0;
+    r.task0 = 0;
+    r.parts = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         r.umin[a] = r.cmin[a] = ~0ull;
@@ -139,6 +144,7 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
     r.maxw = 0;
     r.algo = ALGO_NONE;
     r.any_wrap = 0;
+    r.img_total = 0;
 
     double cell[3][3];
     bool finite = true;
@@ -226,7 +232,7 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
             r.nimages = count;
 #pragma unroll
             for (int a = 0; a < 3; ++a) r.reps[a] = (int32_t)rep_axis[a];
-            atomicAdd((unsigned long long*)(status + SS_TOTAL_IMAGES), (unsigned long long)count);
+            r.img_total = count;
         }
 #pragma unroll
         for (int e = 0; e < 9; ++e) r.dual[e] = dual_axis[e / 3][e % 3];
@@ -290,7 +296,7 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
             r.grid[e] = (e % 4 == 0) ? 1.0 : 0.0;
         }
     }
-    if (st) atomicOr(flags, st);
+    r.flags = st;
 }
 
 // Structure of atom i: the b with bp[b] <= i < bp[b + 1] (batch_ptr valid).
@@ -349,14 +355,25 @@ __device__ __forceinline__ void grid_coords(const StructRec& r, const T q[3], do
 // A block whose atoms all lie in one structure writes one BlockPartial
 // without atomics; a block spanning several structures uses atomics on the
 // structure records (each such structure is small, so contention is low).
+// The grid also zeroes the bin counters and the tile states of the two
+// single-pass scans, which later kernels of the request use.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* bp,
                                                    const T* cells, int64_t nb, int64_t n_atoms,
                                                    StructRec* recs, BlockPartial* partials,
                                                    int* atom_struct, int4* atom_wrap,
-                                                   Vec4<T>* atom_q, unsigned long long* status) {
+                                                   Vec4<T>* atom_q, unsigned long long* status,
+                                                   int* bin_count, int64_t n_bin_count,
+                                                   unsigned long long* tiles, int64_t n_tiles) {
     __shared__ unsigned long long s_red[kWavesPerBlock][14];
     __shared__ unsigned long long s_flags;
+    {
+        const int64_t stride = (int64_t)gridDim.x * kBlock;
+        for (int64_t k = (int64_t)blockIdx.x * kBlock + threadIdx.x; k < n_bin_count; k += stride)
+            bin_count[k] = 0;
+        for (int64_t k = (int64_t)blockIdx.x * kBlock + threadIdx.x; k < n_tiles; k += stride)
+            tiles[k] = 0;
+    }
     // Block-uniform early exit (the barrier below needs every thread).
     if (threadIdx.x == 0) s_flags = load_status(status + SS_FLAGS);
     __syncthreads();
@@ -386,7 +403,9 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
             p[c] = pos[3 * i + c];
             finite = finite && isfinite((double)p[c]);
         }
-        if (!finite) {
+        if (r.flags & kAbortBits) {
+            // a structure with input errors: the request fails, nothing to compute
+        } else if (!finite) {
             st |= ST_POS_NONFINITE;
         } else {
             const double pd[3] = {(double)p[0], (double)p[1], (double)p[2]};
@@ -477,18 +496,26 @@ template <typename T>
 __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int64_t n_atoms,
                                                 double cutoff, int requested, int reach_target,
                                                 StructRec* recs, const BlockPartial* partials,
-                                                long long* struct_bins,
+                                                long long* struct_bins, long long* struct_tasks,
                                                 unsigned long long* status) {
     const int64_t b = blockIdx.x;
     const int lane = lane_id();
-    if (b == 0 && lane == 0 && status[SS_TOTAL_IMAGES] > (unsigned long long)kImageCap)
-        atomicOr(status + SS_FLAGS, ST_BATCH_IMAGE_CAP);
     if (b >= nb) return;
-    if (load_status(status + SS_FLAGS) & kAbortBits) {
-        if (lane == 0) struct_bins[b] = 0;
+    StructRec& r = recs[b];
+    // fold the structure's own input errors and images into the status words
+    if (lane == 0) {
+        if (r.flags) atomicOr(status + SS_FLAGS, r.flags);
+        if (r.img_total > 0)
+            atomicAdd((unsigned long long*)(status + SS_TOTAL_IMAGES),
+                      (unsigned long long)r.img_total);
+    }
+    if ((r.flags & kAbortBits) || (load_status(status + SS_FLAGS) & kAbortBits)) {
+        if (lane == 0) {
+            struct_bins[b] = 0;
+            struct_tasks[b] = 0;
+        }
         return;
     }
-    StructRec& r = recs[b];
     const int64_t n = r.natoms;
     // reduce the partials of uniform blocks inside this structure
     unsigned long long v[14];
@@ -524,7 +551,9 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
     if (n == 0) {
         r.algo = ALGO_NONE;
         r.nbins = 0;
+        r.parts = 1;
         struct_bins[b] = 0;
+        struct_tasks[b] = 0;
         return;
     }
     double cell[9];
@@ -578,8 +607,17 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
     int algo = ALGO_BRUTE;
     int64_t nbins = 0;
     if (want_cell) {
+        // Bin grid for a stencil reach of kt bins per padded cutoff.  With
+        // reach_target 0 the reach is chosen per structure: the smallest
+        // kt whose estimated stencil (bins in reach times atoms per bin)
+        // holds at most kAutoCandidates<T> candidates, else the one with
+        // the fewest candidates.
         const double rcu0 = rc + 2 * pad;
-        const double kt = (double)reach_target;
+        double best_c = INFINITY;
+        int k_lo = reach_target > 0 ? reach_target : 1;
+        int k_hi = reach_target > 0 ? reach_target : 4;
+        for (int kt_i = k_lo; kt_i <= k_hi; ++kt_i) {
+        const double kt = (double)kt_i;
         double ext[3], wdt[3], nbf[3], rcu[3], lo[3];
         bool ok = true;
 #pragma unroll
@@ -636,34 +674,42 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
         const bool fits = ok && reach_ok && nbf[0] * nbf[1] * nbf[2] <= capb &&
                           (long long)rows * zs <= kPieceCap &&
                           (double)n * (double)(rows * zs) < 2147483647.0;
-        if (fits) {
-            algo = ALGO_CELL;
-            nbins = (int64_t)(nbf[0] * nbf[1] * nbf[2]);
+        if (!fits) continue;
+        // estimated candidates of a stencil and sources of a bin
+        const double bins_f = nbf[0] * nbf[1] * nbf[2];
+        const double per_bin = (double)n / bins_f;
+        double span_bins = 1.0;
 #pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                r.nb[a] = (int32_t)nbf[a];
-                r.inv_w[a] = (active >> a & 1) ? nbf[a] : 1.0 / wdt[a];
-                r.lo[a] = lo[a];
-                r.reach[a] = reach[a];
-            }
-            r.zseg = zs;
+        for (int a = 0; a < 3; ++a) {
+            const double w = 2.0 * reach[a] + 1.0;
+            span_bins *= (active >> a & 1) ? w : fmin(w, nbf[a]);
+        }
+        const double cand = span_bins * per_bin;
+        const bool take = best_c == INFINITY || (best_c > kAutoCandidates<T>::value && cand < best_c);
+        if (!take) continue;
+        best_c = cand;
+        algo = ALGO_CELL;
+        nbins = (int64_t)bins_f;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            r.nb[a] = (int32_t)nbf[a];
+            r.inv_w[a] = (active >> a & 1) ? nbf[a] : 1.0 / wdt[a];
+            r.lo[a] = lo[a];
+            r.reach[a] = reach[a];
+        }
+        r.zseg = zs;
+        // waves that share a bin's sources: one per ~6 sources, at most 4
+        r.parts = (int32_t)fmin(fmax(floor(per_bin / 6.0), 1.0), 4.0);
+        if (cand <= kAutoCandidates<T>::value) break;
         }
     }
     r.algo = algo;
     r.nbins = nbins;
+    if (algo != ALGO_CELL) r.parts = 1;
     struct_bins[b] = nbins;
+    struct_tasks[b] = nbins * r.parts;
     atomicOr(status + SS_PLAN, algo == ALGO_CELL ? 2ull : 1ull);
     if (st) atomicOr(status + SS_FLAGS, st);
-}
-
-__global__ void k_struct_bin0(StructRec* recs, const long long* off, int64_t nb,
-                              unsigned long long* status, int64_t cap_bins) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b < nb) recs[b].bin0 = off[b];
-    if (b == 0) {
-        status[SS_TOTAL_BINS] = (unsigned long long)off[nb];
-        if (off[nb] > cap_bins) atomicOr(status + SS_FLAGS, ST_CAPACITY);
-    }
 }
 
 template <typename T>

@@ -1,5 +1,7 @@
-// Device-wide exclusive scans (reduce, scan of block totals, apply) and
-// small fill kernels.
+// Device-wide exclusive scans: a single-pass scan with decoupled look-back
+// (k_scan_lookback), the one-block scan of the bins per structure
+// (k_struct_scan), the three-kernel scan (reduce, scan of block totals,
+// apply) and small fill kernels.
 #pragma once
 
 #include "nl_math.h"
@@ -98,6 +100,148 @@ __global__ __launch_bounds__(kBlock) void k_scan_apply(const In* in, int64_t n,
         run += v[j];
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = (Out)partial[np];
+}
+
+// ------------------------------------------------------- single-pass scan
+
+// Tile state of the single-pass scan: bits 62-63 hold the flag (0 not ready,
+// 1 tile aggregate, 2 inclusive prefix), bits 0-61 the value.
+constexpr unsigned long long kTileAggregate = 1ull << 62;
+constexpr unsigned long long kTilePrefix = 2ull << 62;
+constexpr unsigned long long kTileValue = (1ull << 62) - 1;
+constexpr int kLookbackSpins = 1 << 22;
+
+__device__ __forceinline__ void tile_publish(unsigned long long* t, unsigned long long w) {
+    __hip_atomic_store(t, w, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long tile_read(const unsigned long long* t) {
+    return __hip_atomic_load(t, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Exclusive scan of n (min(n, *n_dev) when n_dev is given) non-negative values of
+// `in` into out[0..n], out[n] = total, in one launch.  Blocks take tiles of
+// kScanTile items in the order they start (an atomic ticket), so every
+// earlier tile belongs to a block that is already running; a block publishes
+// its tile aggregate, then walks back over the earlier tiles until it meets
+// an inclusive prefix (decoupled look-back).  The wait on an earlier tile is
+// bounded (kLookbackSpins polls); on expiry the block raises ST_SCAN_STALL
+// and finishes, so every wave exits.  `tiles` must hold zeros and `ticket`
+// zero.  When total_slot is given the total is also stored there.
+template <typename In, typename Out>
+__global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t n,
+                                                           const unsigned long long* n_dev,
+                                                           Out* out, unsigned long long* tiles,
+                                                           unsigned long long* ticket,
+                                                           unsigned long long* status,
+                                                           unsigned long long* total_slot) {
+    __shared__ long long s_tile, s_excl;
+    if (threadIdx.x == 0) s_tile = (long long)atomicAdd(ticket, 1ull);
+    __syncthreads();
+    if (n_dev) n = min(n, (int64_t)*n_dev);
+    const int64_t tile = s_tile;
+    const int64_t ntiles = n > 0 ? (n + kScanTile - 1) / kScanTile : 1;
+    if (tile >= ntiles) return;
+    const int64_t base = tile * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    long long v[kScanItems];
+    long long s = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int64_t i = base + k;
+        v[k] = i < n ? (long long)in[i] : 0;
+        s += v[k];
+    }
+    long long total;
+    const long long ex = block_exclusive_scan(s, &total);
+    if (threadIdx.x == 0) {
+        long long excl = 0;
+        if (tile > 0) {
+            tile_publish(tiles + tile, kTileAggregate | (unsigned long long)total);
+            for (int64_t t = tile - 1; t >= 0; --t) {
+                unsigned long long w = tile_read(tiles + t);
+                for (int spin = 0; (w >> 62) == 0 && spin < kLookbackSpins; ++spin) {
+                    __builtin_amdgcn_s_sleep(1);
+                    w = tile_read(tiles + t);
+                }
+                if ((w >> 62) == 0) {
+                    atomicOr(status + SS_FLAGS, ST_SCAN_STALL);
+                    break;
+                }
+                excl += (long long)(w & kTileValue);
+                if ((w & ~kTileValue) == kTilePrefix) break;
+            }
+        }
+        tile_publish(tiles + tile, kTilePrefix | (unsigned long long)(excl + total));
+        s_excl = excl;
+    }
+    __syncthreads();
+    long long run = s_excl + ex;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        const int64_t i = base + k;
+        if (i < n) out[i] = (Out)run;
+        run += v[k];
+    }
+    if (tile == ntiles - 1 && threadIdx.x == 0) {
+        out[n] = (Out)(s_excl + total);
+        if (total_slot) *total_slot = (unsigned long long)(s_excl + total);
+    }
+}
+
+// One block: exclusive scans of the bins and of the cell-list tasks per
+// structure into bin_off[0..nb] and task_off[0..nb] (and each structure's
+// first bin and task), their totals, and the batch checks that need every
+// structure's plan: total periodic images and bin capacity.
+__global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
+                                                         const long long* struct_tasks,
+                                                         int64_t nb, long long* bin_off,
+                                                         long long* task_off, StructRec* recs,
+                                                         unsigned long long* status,
+                                                         int64_t cap_bins) {
+    __shared__ long long carry_b, carry_t;
+    if (threadIdx.x == 0) carry_b = carry_t = 0;
+    __syncthreads();
+    for (int64_t base = 0; base < nb; base += kScanChunk) {
+        const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
+        long long vb[kScanItems], vt[kScanItems];
+        long long sb = 0, stt = 0;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            vb[k] = i0 + k < nb ? struct_bins[i0 + k] : 0;
+            vt[k] = i0 + k < nb ? struct_tasks[i0 + k] : 0;
+            sb += vb[k];
+            stt += vt[k];
+        }
+        long long tot_b, tot_t;
+        long long run_b = block_exclusive_scan(sb, &tot_b) + carry_b;
+        long long run_t = block_exclusive_scan(stt, &tot_t) + carry_t;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            if (i0 + k < nb) {
+                bin_off[i0 + k] = run_b;
+                task_off[i0 + k] = run_t;
+                recs[i0 + k].bin0 = run_b;
+                recs[i0 + k].task0 = run_t;
+            }
+            run_b += vb[k];
+            run_t += vt[k];
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            carry_b += tot_b;
+            carry_t += tot_t;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        bin_off[nb] = carry_b;
+        task_off[nb] = carry_t;
+        status[SS_TOTAL_BINS] = (unsigned long long)carry_b;
+        status[SS_TOTAL_TASKS] = (unsigned long long)carry_t;
+        unsigned long long st = 0;
+        if (carry_b > cap_bins) st |= ST_CAPACITY;
+        if (status[SS_TOTAL_IMAGES] > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+        if (st) atomicOr(status + SS_FLAGS, st);
+    }
 }
 
 template <typename In, typename Out>

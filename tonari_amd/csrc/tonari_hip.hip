@@ -4,13 +4,15 @@
 // brute-force count/emit) and nl_scan.h (device-wide scans).
 //
 // Pipeline of one request (all on the caller's stream):
-//   tnr_count: zero status -> k_setup (per structure: batch_ptr checks, active
-//              pseudo-inverse, image repeats, grid frame) -> k_atoms (per atom:
-//              wraps, wrapped position, block reductions) -> k_plan (one wave
-//              per structure: margins, algorithm, bin grid) -> scan(bins per
-//              structure) -> k_bin -> scan(bin counts) -> k_scatter ->
-//              k_cell_count + k_brute<count> -> scan(pairs per source) ->
-//              k_finish -> one 4-word device-to-host copy (E, status).
+//   tnr_count: k_setup (zeroes the status words; per structure: batch_ptr
+//              checks, active pseudo-inverse, image repeats, grid frame) ->
+//              k_atoms (per atom: wraps, wrapped position, block reductions;
+//              zeroes the bin counters and scan tiles) -> k_plan (one wave per
+//              structure: margins, algorithm, bin grid) -> k_struct_scan (bins
+//              per structure) -> k_bin -> k_scan_lookback(bin counts) -> k_scatter ->
+//              k_cell_count (persistent: cell-list bins, then brute-force
+//              sources) -> k_scan_lookback(pairs per source; E) -> one
+//              8-word device-to-host copy (status, E, plan, bins).
 //   tnr_emit:  k_cell_emit and/or k_brute<emit> write i/j/P/S/d/D in place.
 //
 // Reference semantics (songfeitong/tonari):
@@ -25,6 +27,7 @@
 // fused multiply-adds explicitly, the exact predicate uses the _rn
 // intrinsics so that its rounding sequence is the reference's.
 
+#include "nl_cell.h"
 #include "nl_prologue.h"
 #include "nl_query.h"
 #include "nl_scan.h"
@@ -33,6 +36,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -40,9 +44,6 @@
 
 namespace tnr {
 
-__global__ void k_finish(const long long* offsets, int64_t n_atoms, unsigned long long* status) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) status[SS_PAIRS] = (unsigned long long)offsets[n_atoms];
-}
 
 // ------------------------------------------------------------------- host
 
@@ -51,6 +52,8 @@ struct Views {
     StructRec* recs;
     long long* struct_bins;
     long long* struct_bin_off;
+    long long* struct_tasks;
+    long long* struct_task_off;
     int* atom_struct;
     int4* atom_wrap;
     void* atom_q;
@@ -64,6 +67,8 @@ struct Views {
     long long* partials;
     BlockPartial* block_partials;
     unsigned long long* masks;
+    unsigned long long* tiles_bins;
+    unsigned long long* tiles_pairs;
 };
 
 static Views views(void* ws, const Layout& L) {
@@ -73,6 +78,8 @@ static Views views(void* ws, const Layout& L) {
     v.recs = (StructRec*)(base + L.structs);
     v.struct_bins = (long long*)(base + L.struct_bins);
     v.struct_bin_off = (long long*)(base + L.struct_bin_off);
+    v.struct_tasks = (long long*)(base + L.struct_tasks);
+    v.struct_task_off = (long long*)(base + L.struct_task_off);
     v.atom_struct = (int*)(base + L.atom_struct);
     v.atom_wrap = (int4*)(base + L.atom_wrap);
     v.atom_q = base + L.atom_q;
@@ -86,6 +93,8 @@ static Views views(void* ws, const Layout& L) {
     v.partials = (long long*)(base + L.partials);
     v.block_partials = (BlockPartial*)(base + L.block_partials);
     v.masks = (unsigned long long*)(base + L.masks);
+    v.tiles_bins = (unsigned long long*)(base + L.tiles_bins);
+    v.tiles_pairs = (unsigned long long*)(base + L.tiles_pairs);
     return v;
 }
 
@@ -94,12 +103,51 @@ static unsigned blocks_for(int64_t n, int per = kBlock) {
     return (unsigned)(b > 0 ? b : 1);
 }
 
-// Waves of a grid-stride query kernel: enough for ~8 waves per SIMD.
-static unsigned query_blocks(int64_t work_waves) {
+// Blocks of the persistent counting kernel: as many as the device holds at
+// once (occupancy x CUs), rounded down to a multiple of 8 so that every XCD
+// gets the same number, and no more than the work needs.  The occupancy is
+// looked up once per device and kernel instantiation and cached (the only
+// state the library keeps; it is idempotent and safe under concurrent use).
+template <typename T, int MODE>
+static int64_t count_resident_blocks() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_cell_count<T, MODE>, kBlock, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+        per_cu = 2;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    v = per_cu * cus;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
+
+template <typename T, int MODE>
+static unsigned count_blocks(int64_t work_waves) {
     const int64_t want = (work_waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    int64_t cap = 8192;
+    const int64_t cap = count_resident_blocks<T, MODE>() / 8 * 8;
     int64_t b = want < cap ? want : cap;
-    if (b > 8) b = (b + 7) / 8 * 8;
+    b = (b + 7) / 8 * 8;
+    return (unsigned)(b > 0 ? b : 8);
+}
+
+// Blocks of the emitting cell-list kernel: one wave per task, 8 equal
+// XCD ranges of ceil(tasks / 8) tasks.
+static unsigned emit_blocks(int64_t tasks) {
+    const int64_t per = (tasks + 7) / 8;
+    const int64_t b = 8 * ((per + kWavesPerBlock - 1) / kWavesPerBlock);
+    return (unsigned)(b > 0 ? b : 8);
+}
+
+static unsigned brute_blocks(int64_t n) {
+    const int64_t want = (n + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int64_t b = want < 8192 ? want : 8192;
     return (unsigned)(b > 0 ? b : 1);
 }
 
@@ -109,7 +157,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.pos = (const T*)req->positions;
     q.cells = (const T*)req->cell;
     q.recs = v.recs;
-    q.struct_bin_off = (const int64_t*)v.struct_bin_off;
+    q.struct_task_off = (const int64_t*)v.struct_task_off;
     q.atom_struct = v.atom_struct;
     q.atom_wrap = v.atom_wrap;
     q.atom_q = (const Vec4<T>*)v.atom_q;
@@ -117,40 +165,42 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.binned = (const Vec4<T>*)v.binned;
     q.counts = v.counts;
     q.offsets = v.offsets;
-    q.masks = v.masks;
     q.status = v.status;
+    q.masks = v.masks;
     q.n_atoms = req->n_atoms;
     q.nb = req->n_structures;
     return q;
 }
 
-// plan: bit 0 launches the brute-force family, bit 1 the cell-list family;
-// 0 (unknown, as during counting) launches every family the request allows.
+// Counting: one persistent kernel covers both families (the plan is only
+// known on the device).  Emitting: plan bit 0 launches the brute-force
+// family, bit 1 the cell-list family over n_tasks tasks (bin parts).
 template <typename T, int MODE, bool EMIT>
 static void launch_queries(const tnr_request* req, const Layout& L, const QueryArgs<T>& q,
-                           int64_t plan, hipStream_t stream) {
+                           int64_t plan, int64_t n_tasks, hipStream_t stream) {
     const int64_t n = req->n_atoms;
     if (n == 0) return;
-    const bool cell = plan ? (plan & 2) != 0 : req->algorithm != TNR_BRUTE_FORCE;
-    const bool brute = plan ? (plan & 1) != 0 : true;
-    if (cell) {
-        if constexpr (EMIT)
-            k_cell_emit<T, MODE><<<query_blocks(L.cap_bins), kBlock, 0, stream>>>(q);
-        else
-            k_cell_count<T, MODE><<<query_blocks(L.cap_bins), kBlock, 0, stream>>>(q);
+    if constexpr (!EMIT) {
+        (void)plan;
+        (void)n_tasks;
+        k_cell_count<T, MODE><<<count_blocks<T, MODE>(4 * (L.cap_bins > n ? L.cap_bins : n)),
+                                kBlock, 0, stream>>>(q);
+    } else {
+        if ((plan & 2) && n_tasks > 0)
+            k_cell_emit<T, MODE><<<emit_blocks(n_tasks), kBlock, 0, stream>>>(q);
+        if (plan & 1) k_brute<T, MODE, true><<<brute_blocks(n), kBlock, 0, stream>>>(q);
     }
-    if (brute) k_brute<T, MODE, EMIT><<<query_blocks(n), kBlock, 0, stream>>>(q);
 }
 
 template <typename T, bool EMIT>
 static void dispatch_queries(const tnr_request* req, const Layout& L, const QueryArgs<T>& q,
-                             int64_t plan, hipStream_t stream) {
+                             int64_t plan, int64_t n_tasks, hipStream_t stream) {
     const int mode = (req->half_list ? 2 : 0) | (req->include_self ? 1 : 0);
     switch (mode) {
-        case 0: launch_queries<T, 0, EMIT>(req, L, q, plan, stream); break;
-        case 1: launch_queries<T, 1, EMIT>(req, L, q, plan, stream); break;
-        case 2: launch_queries<T, 2, EMIT>(req, L, q, plan, stream); break;
-        default: launch_queries<T, 3, EMIT>(req, L, q, plan, stream); break;
+        case 0: launch_queries<T, 0, EMIT>(req, L, q, plan, n_tasks, stream); break;
+        case 1: launch_queries<T, 1, EMIT>(req, L, q, plan, n_tasks, stream); break;
+        case 2: launch_queries<T, 2, EMIT>(req, L, q, plan, n_tasks, stream); break;
+        default: launch_queries<T, 3, EMIT>(req, L, q, plan, n_tasks, stream); break;
     }
 }
 
@@ -159,37 +209,44 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                             hipStream_t stream) {
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
-    k_fill_i64<<<1, 64, 0, stream>>>((long long*)v.status, SS_SLOTS, 0);
+    // k_setup zeroes the status words; k_atoms zeroes the bin counters and
+    // the tile states of both single-pass scans.
     k_setup<T><<<blocks_for(nb > 0 ? nb : 1, 64), 64, 0, stream>>>(
         req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, v.recs, v.status);
-    if (n > 0)
+    if (n > 0) {
+        const int64_t n_tiles =
+            (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) +
+            L.n_tiles_pairs;
         k_atoms<T><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->positions, req->batch_ptr, (const T*)req->cell, nb, n, v.recs,
-            v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q, v.status);
-    const int reach = req->stencil_reach > 0 ? req->stencil_reach : kStencilReach;
+            v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q, v.status,
+            v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
+    }
+    const int reach = req->stencil_reach;  // 0: chosen per structure
     k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kWave, 0, stream>>>(
         (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
-        v.block_partials, v.struct_bins, v.status);
-    (void)device_scan<long long, long long>(v.struct_bins, nb, v.struct_bin_off, v.partials,
-                                            stream);
-    k_struct_bin0<<<blocks_for(nb > 0 ? nb : 1, 64), 64, 0, stream>>>(
-        v.recs, v.struct_bin_off, nb, v.status, L.cap_bins);
+        v.block_partials, v.struct_bins, v.struct_tasks, v.status);
+    k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks, nb, v.struct_bin_off,
+                                            v.struct_task_off, v.recs, v.status, L.cap_bins);
     if (n > 0 && req->algorithm != TNR_BRUTE_FORCE) {
-        k_fill_i32<<<blocks_for(L.cap_bins + 1), kBlock, 0, stream>>>(v.bin_count,
-                                                                      L.cap_bins + 1, 0);
         k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
                                                        (const Vec4<T>*)v.atom_q, v.atom_bin,
                                                        v.atom_rank, v.bin_count, v.status);
-        (void)device_scan<int, int>(v.bin_count, L.cap_bins, v.bin_start, v.partials, stream);
+        k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
+            v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
+            v.status + SS_TICKET_BINS, v.status, nullptr);
         k_scatter<T><<<blocks_for(n), kBlock, 0, stream>>>(n, (const Vec4<T>*)v.atom_q,
                                                            v.atom_bin, v.atom_rank,
                                                            v.bin_start, (Vec4<T>*)v.binned,
                                                            v.status);
     }
     const QueryArgs<T> q = query_args<T>(req, v);
-    dispatch_queries<T, false>(req, L, q, 0, stream);
-    (void)device_scan<long long, long long>(v.counts, n, v.offsets, v.partials, stream);
-    k_finish<<<1, 1, 0, stream>>>(v.offsets, n, v.status);
+    dispatch_queries<T, false>(req, L, q, 0, 0, stream);
+    // pairs per source -> offsets; the total (E) goes to the status words
+    k_scan_lookback<long long, long long>
+        <<<(unsigned)((n + kScanTile - 1) / kScanTile > 0 ? (n + kScanTile - 1) / kScanTile : 1),
+           kBlock, 0, stream>>>(v.counts, n, nullptr, v.offsets, v.tiles_pairs,
+                                v.status + SS_TICKET_PAIRS, v.status, v.status + SS_PAIRS);
     return hipGetLastError();
 }
 
@@ -205,7 +262,7 @@ static hipError_t run_emit(const tnr_request* req, void* ws, const Layout& L,
     q.src = out->sources;
     q.dst = out->targets;
     q.limit = out->n_pairs;
-    dispatch_queries<T, true>(req, L, q, out->plan, stream);
+    dispatch_queries<T, true>(req, L, q, out->plan, out->n_tasks, stream);
     return hipGetLastError();
 }
 
@@ -236,6 +293,7 @@ static const StatusMessage kMessages[] = {
     {ST_SHIFT_RANGE, TNR_SEARCH_ERROR,
      "a cell shift required by the neighbor list exceeds the int32 output range"},
     {ST_CAPACITY, TNR_SEARCH_ERROR, "neighbor-list workspace capacity exceeded"},
+    {ST_SCAN_STALL, TNR_SEARCH_ERROR, "a device-wide scan of the neighbor search did not complete"},
 };
 
 static int put_error(char* err, size_t len, int code, const char* msg) {
@@ -303,7 +361,8 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
                                              : tnr::run_count<double>(req, workspace, L, s);
     if (e == hipSuccess) {
         const tnr::Views v = tnr::views(workspace, L);
-        e = hipMemcpyAsync(host_result, v.status, 4 * sizeof(int64_t), hipMemcpyDeviceToHost, s);
+        e = hipMemcpyAsync(host_result, v.status, TNR_HOST_RESULT_SLOTS * sizeof(int64_t),
+                           hipMemcpyDeviceToHost, s);
     }
     if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
     return TNR_OK;
