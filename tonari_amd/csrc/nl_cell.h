@@ -31,7 +31,7 @@ template <typename T>
 struct RegChunks;
 template <>
 struct RegChunks<float> {
-    static constexpr int value = 16;
+    static constexpr int value = 12;
 };
 template <>
 struct RegChunks<double> {
@@ -88,7 +88,7 @@ struct StructCache {
     int64_t lo, hi;
 };
 
-__device__ __forceinline__ int structure_of_task(const int64_t* off, int64_t nb, int64_t g,
+__device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb, int64_t g,
                                                  StructCache& sc) {
     if (g >= sc.lo && g < sc.hi) return sc.b;
     int64_t lo = 0, hi = nb;
@@ -107,20 +107,26 @@ __device__ __forceinline__ int structure_of_task(const int64_t* off, int64_t nb,
 // each building the stencil itself.  Pieces are runs of
 // consecutive z-bins of one (x, y) row with one periodic image k, one lane
 // per piece; pieces with |k_a| > R_a are dropped, which keeps exactly the
-// reference's image box.  Fills the piece table of st and resolves the
+// reference's image box.  Fills the piece table of st (and, when tr is
+// given, the broad-phase translation of every piece) and resolves the
 // piece of every candidate into st.piece when C <= kMapCap.  Returns false when the bin holds no
 // source.
+// A task is one part of a bin: parts waves split the bin's sources.  The
+// counting kernel (tr given) uses the counting tasks (r.cparts per bin), the
+// emitting kernel the emitting tasks (r.parts per bin).
 template <typename T>
 __device__ __forceinline__ bool cell_bin(const QueryArgs<T>& a, int64_t task, StructCache& sc,
-                                         CellBin<T>& cb, StencilLds& st) {
+                                         CellBin<T>& cb, StencilLds& st,
+                                         T (*tr)[kPieceCap] = nullptr) {
     const int lane = lane_id();
-    cb.b = structure_of_task(a.struct_task_off, a.nb, task, sc);
-    const StructRec& r = a.recs[cb.b];
-    const int parts = r.parts;
+    cb.b = structure_of_item(tr ? a.struct_ctask_off : a.struct_task_off, a.nb, task, sc);
+    const int parts = tr ? a.recs[cb.b].cparts : a.recs[cb.b].parts;
     const unsigned local = (unsigned)(task - sc.lo);  // tasks of a structure fit in 32 bits
-    const unsigned lbin = local / (unsigned)parts;
-    const int part = (int)(local - lbin * (unsigned)parts);
-    const int64_t g = r.bin0 + lbin;
+    const unsigned lb = local / (unsigned)parts;
+    const int part = (int)(local - lb * (unsigned)parts);
+    const int64_t g = a.recs[cb.b].bin0 + lb;
+    const StructRec& r = a.recs[cb.b];
+    const unsigned lbin = (unsigned)(g - r.bin0);  // bins of a structure fit in 32 bits
     const int sb = uniform(a.bin_start[g]), se = uniform(a.bin_start[g + 1]);
     // sources of this part: the part-th share of the bin's sources
     const int q = (se - sb + parts - 1) / parts;
@@ -212,6 +218,7 @@ __device__ __forceinline__ bool cell_bin(const QueryArgs<T>& a, int64_t task, St
             st.delta[p] = start - ex;
             st.kid[p] = kk;
             if (len > 0 && ex < kMapCap) st.piece[ex] = (unsigned char)p;
+            if (tr) image_translation(kk, cb.c, tr[0][p], tr[1][p], tr[2][p]);
         }
         carry += __builtin_amdgcn_readlane(inc, kWave - 1);
     }
@@ -399,7 +406,8 @@ struct Chunks {
 
 template <typename T, int MODE, int NC>
 __device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const StencilLds& st,
-                                            const CellBin<T>& cb, int c0, Chunks<T, NC>& cd) {
+                                            const T (*tr)[kPieceCap], const CellBin<T>& cb,
+                                            int c0, Chunks<T, NC>& cd) {
     using O = Ops<T>;
     const int lane = lane_id();
     const T far = T(1e18);
@@ -417,11 +425,9 @@ __device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const Stencil
                 unpack_k(kk, kx, ky, kz);
                 cd.key[j] = identity_key<MODE>(as_idx(rec.w), kk == pack_k(0, 0, 0),
                                                lex_negative(kx, ky, kz));
-                T tx, ty, tz;
-                image_translation(kk, cb.c, tx, ty, tz);
-                cd.x[j] = O::add(rec.x, tx);
-                cd.y[j] = O::add(rec.y, ty);
-                cd.z[j] = O::add(rec.z, tz);
+                cd.x[j] = O::add(rec.x, tr[0][p]);
+                cd.y[j] = O::add(rec.y, tr[1][p]);
+                cd.z[j] = O::add(rec.z, tr[2][p]);
             }
         }
     }
@@ -487,7 +493,7 @@ __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLd
 // chunk (masks[binned index][chunk]) for the emitting pass.
 template <typename T, int MODE, int NC>
 __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLds& st,
-                                          const CellBin<T>& cb) {
+                                          const T (*tr)[kPieceCap], const CellBin<T>& cb) {
     const int lane = lane_id();
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
     for (int sg = cb.sb; sg < cb.se; sg += kWave) {
@@ -497,7 +503,7 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
         long long acc = 0;  // lane gi: pairs of source gi so far
         for (int c0 = 0; c0 < cb.nch; c0 += NC) {
             Chunks<T, NC> cd;
-            gather_pass<T, MODE, NC>(a, st, cb, c0, cd);
+            gather_pass<T, MODE, NC>(a, st, tr, cb, c0, cd);
             const bool store = lane < NC && c0 + lane < cb.nch;
 #pragma unroll 1
             for (int gi = 0; gi < ns; ++gi) {
@@ -528,16 +534,14 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
 // stencil (passes of RegChunks<T> chunks beyond that).
 template <typename T, int MODE>
 __device__ __forceinline__ void count_bin_any(const QueryArgs<T>& a, const StencilLds& st,
-                                              const CellBin<T>& cb) {
+                                              const T (*tr)[kPieceCap], const CellBin<T>& cb) {
     constexpr int CH = RegChunks<T>::value;
     if (cb.nch <= 4)
-        count_bin<T, MODE, 4>(a, st, cb);
+        count_bin<T, MODE, 4>(a, st, tr, cb);
     else if (cb.nch <= 8 || CH == 8)
-        count_bin<T, MODE, 8>(a, st, cb);
-    else if (cb.nch <= 12)
-        count_bin<T, MODE, (CH > 12 ? 12 : CH)>(a, st, cb);
+        count_bin<T, MODE, 8>(a, st, tr, cb);
     else
-        count_bin<T, MODE, CH>(a, st, cb);
+        count_bin<T, MODE, CH>(a, st, tr, cb);
 }
 
 // Emitting, register path of one bin: no distance tests, the hit masks of
@@ -654,29 +658,32 @@ __device__ __forceinline__ WaveRange xcd_range(int64_t W, int wv) {
 }
 
 // Counting pass, persistent grid: every wave walks its share of the
-// (source bin, part) tasks of the cell-list structures, then of the source atoms of the
+// counting tasks (bin parts) of the cell-list structures, then of the source atoms of the
 // brute-force structures, and writes counts[s] for each source s.  The
 // status word is read once: abort bits only come from earlier kernels.
 template <typename T, int MODE>
-__global__ __launch_bounds__(kBlock) void k_cell_count(
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? 4 : 1))) void
+k_cell_count(
     QueryArgs<T> a) {
     __shared__ StencilLds s_st[kWavesPerBlock];
+    __shared__ T s_tr[kWavesPerBlock][3][kPieceCap];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
     const unsigned long long plan = load_status(a.status + SS_PLAN);
     const int wv = uniform(threadIdx.x / kWave);
     StencilLds& st = s_st[wv];
+    T(*tr)[kPieceCap] = s_tr[wv];
 
     if (plan & 2) {
-        const WaveRange wr = xcd_range(a.struct_task_off[a.nb], wv);
+        const WaveRange wr = xcd_range(a.struct_ctask_off[a.nb], wv);
         StructCache sc{0, 0, 0};
         for (int64_t t = wr.first; t < wr.end; t += wr.step) {
             CellBin<T> cb;
-            if (!cell_bin<T>(a, t, sc, cb, st)) continue;
+            if (!cell_bin<T>(a, t, sc, cb, st, tr)) continue;
             if (cb.C > kMapCap)
                 cell_slow<T, MODE, false>(a, st, cb);
             else
-                count_bin_any<T, MODE>(a, st, cb);
+                count_bin_any<T, MODE>(a, st, tr, cb);
         }
     }
     if (plan & 1) {

@@ -16,6 +16,10 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kPieceCap = 192;            // stencil pieces per source bin
+// Sources of a cell-list bin per wave of the query kernels (a bin's sources
+// are split over up to 4 waves).
+constexpr double kSourcesPerPart = 6.0;
+
 // Automatic stencil reach: the smallest reach whose estimated stencil holds
 // at most this many candidates (one register pass of the counting kernel
 // holds 1024 float or 512 double candidates).
@@ -62,7 +66,8 @@ enum StatusSlot : int {
     SS_TOTAL_BINS = 4,
     SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
-    SS_TOTAL_TASKS = 7,   // cell-list tasks (bin parts) of the batch
+    SS_TOTAL_TASKS = 7,   // emitting cell-list tasks (bin parts) of the batch
+    SS_TOTAL_CTASKS = 8,  // counting cell-list tasks of the batch
     SS_SLOTS = 64,
 };
 
@@ -77,8 +82,10 @@ struct alignas(16) StructRec {
     int64_t nimages;
     int64_t bin0;
     int64_t nbins;
-    int64_t task0;       // first cell-list task (bin part) of the structure
-    int32_t parts;       // tasks per bin: waves that split a bin's sources
+    int64_t task0;       // first emitting task (bin part) of the structure
+    int64_t ctask0;      // first counting task of the structure
+    int32_t parts;       // emitting tasks per bin: waves that split a bin's sources
+    int32_t cparts;      // counting tasks per bin
     double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
     double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
     double lo[3];        // grid origin (inactive axes)
@@ -115,7 +122,7 @@ struct alignas(16) BlockPartial {
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
     size_t status, structs, struct_bins, struct_bin_off, struct_tasks, struct_task_off,
-        atom_struct, atom_wrap, atom_q,
+        struct_ctasks, struct_ctask_off, atom_struct, atom_wrap, atom_q,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials,
         block_partials, masks, tiles_bins, tiles_pairs, total;
     int64_t cap_bins, n_partials, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
@@ -148,6 +155,8 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.struct_bin_off = take(sizeof(int64_t) * (size_t)(b + 2));
     L.struct_tasks = take(sizeof(int64_t) * (size_t)(b + 1));
     L.struct_task_off = take(sizeof(int64_t) * (size_t)(b + 2));
+    L.struct_ctasks = take(sizeof(int64_t) * (size_t)(b + 1));
+    L.struct_ctask_off = take(sizeof(int64_t) * (size_t)(b + 2));
     L.atom_struct = take(sizeof(int32_t) * (size_t)(n + 1));
     L.atom_wrap = take(sizeof(int32_t) * 4 * (size_t)(n + 1));
     L.atom_q = take(tsize * 4 * (size_t)(n + 1));

@@ -129,7 +129,9 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
     r.bin0 = 0;
     r.nbins = 0;
     r.task0 = 0;
+    r.ctask0 = 0;
     r.parts = 1;
+    r.cparts = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         r.umin[a] = r.cmin[a] = ~0ull;
@@ -497,6 +499,7 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
                                                 double cutoff, int requested, int reach_target,
                                                 StructRec* recs, const BlockPartial* partials,
                                                 long long* struct_bins, long long* struct_tasks,
+                                                long long* struct_ctasks,
                                                 unsigned long long* status) {
     const int64_t b = blockIdx.x;
     const int lane = lane_id();
@@ -513,6 +516,7 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
         if (lane == 0) {
             struct_bins[b] = 0;
             struct_tasks[b] = 0;
+            struct_ctasks[b] = 0;
         }
         return;
     }
@@ -552,8 +556,10 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
         r.algo = ALGO_NONE;
         r.nbins = 0;
         r.parts = 1;
+        r.cparts = 1;
         struct_bins[b] = 0;
         struct_tasks[b] = 0;
+        struct_ctasks[b] = 0;
         return;
     }
     double cell[9];
@@ -698,16 +704,20 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
             r.reach[a] = reach[a];
         }
         r.zseg = zs;
-        // waves that share a bin's sources: one per ~6 sources, at most 4
-        r.parts = (int32_t)fmin(fmax(floor(per_bin / 6.0), 1.0), 4.0);
+        // waves that share a bin's sources: one per kSourcesPerPart, at most 4
+        r.parts = (int32_t)fmin(fmax(floor(per_bin / kSourcesPerPart), 1.0), 4.0);
         if (cand <= kAutoCandidates<T>::value) break;
         }
     }
     r.algo = algo;
     r.nbins = nbins;
     if (algo != ALGO_CELL) r.parts = 1;
+    // the counting pass tests more candidates per source than the emitting
+    // pass writes pairs, so it splits a bin over at most two waves
+    r.cparts = r.parts >= 2 ? 2 : 1;
     struct_bins[b] = nbins;
     struct_tasks[b] = nbins * r.parts;
+    struct_ctasks[b] = nbins * r.cparts;
     atomicOr(status + SS_PLAN, algo == ALGO_CELL ? 2ull : 1ull);
     if (st) atomicOr(status + SS_FLAGS, st);
 }

@@ -187,58 +187,60 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     }
 }
 
-// One block: exclusive scans of the bins and of the cell-list tasks per
-// structure into bin_off[0..nb] and task_off[0..nb] (and each structure's
-// first bin and task), their totals, and the batch checks that need every
-// structure's plan: total periodic images and bin capacity.
+// One block: exclusive scans of the bins, the emitting tasks and the
+// counting tasks per structure into bin_off, task_off and ctask_off
+// ([0..nb]; each structure's first bin and tasks go to its record), their
+// totals, and the batch checks that need every structure's plan: total
+// periodic images and bin capacity.
 __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
                                                          const long long* struct_tasks,
+                                                         const long long* struct_ctasks,
                                                          int64_t nb, long long* bin_off,
-                                                         long long* task_off, StructRec* recs,
+                                                         long long* task_off,
+                                                         long long* ctask_off, StructRec* recs,
                                                          unsigned long long* status,
                                                          int64_t cap_bins) {
-    __shared__ long long carry_b, carry_t;
-    if (threadIdx.x == 0) carry_b = carry_t = 0;
+    __shared__ long long carry[3];
+    if (threadIdx.x < 3) carry[threadIdx.x] = 0;
     __syncthreads();
+    const long long* in[3] = {struct_bins, struct_tasks, struct_ctasks};
+    long long* out[3] = {bin_off, task_off, ctask_off};
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
-        long long vb[kScanItems], vt[kScanItems];
-        long long sb = 0, stt = 0;
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            vb[k] = i0 + k < nb ? struct_bins[i0 + k] : 0;
-            vt[k] = i0 + k < nb ? struct_tasks[i0 + k] : 0;
-            sb += vb[k];
-            stt += vt[k];
-        }
-        long long tot_b, tot_t;
-        long long run_b = block_exclusive_scan(sb, &tot_b) + carry_b;
-        long long run_t = block_exclusive_scan(stt, &tot_t) + carry_t;
+        for (int q = 0; q < 3; ++q) {
+            long long v[kScanItems];
+            long long sum = 0;
 #pragma unroll
-        for (int k = 0; k < kScanItems; ++k) {
-            if (i0 + k < nb) {
-                bin_off[i0 + k] = run_b;
-                task_off[i0 + k] = run_t;
-                recs[i0 + k].bin0 = run_b;
-                recs[i0 + k].task0 = run_t;
+            for (int k = 0; k < kScanItems; ++k) {
+                v[k] = i0 + k < nb ? in[q][i0 + k] : 0;
+                sum += v[k];
             }
-            run_b += vb[k];
-            run_t += vt[k];
+            long long tot;
+            long long run = block_exclusive_scan(sum, &tot) + carry[q];
+#pragma unroll
+            for (int k = 0; k < kScanItems; ++k) {
+                if (i0 + k < nb) {
+                    out[q][i0 + k] = run;
+                    if (q == 0) recs[i0 + k].bin0 = run;
+                    if (q == 1) recs[i0 + k].task0 = run;
+                    if (q == 2) recs[i0 + k].ctask0 = run;
+                }
+                run += v[k];
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) carry[q] += tot;
+            __syncthreads();
         }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            carry_b += tot_b;
-            carry_t += tot_t;
-        }
-        __syncthreads();
     }
     if (threadIdx.x == 0) {
-        bin_off[nb] = carry_b;
-        task_off[nb] = carry_t;
-        status[SS_TOTAL_BINS] = (unsigned long long)carry_b;
-        status[SS_TOTAL_TASKS] = (unsigned long long)carry_t;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) out[q][nb] = carry[q];
+        status[SS_TOTAL_BINS] = (unsigned long long)carry[0];
+        status[SS_TOTAL_TASKS] = (unsigned long long)carry[1];
+        status[SS_TOTAL_CTASKS] = (unsigned long long)carry[2];
         unsigned long long st = 0;
-        if (carry_b > cap_bins) st |= ST_CAPACITY;
+        if (carry[0] > cap_bins) st |= ST_CAPACITY;
         if (status[SS_TOTAL_IMAGES] > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
         if (st) atomicOr(status + SS_FLAGS, st);
     }

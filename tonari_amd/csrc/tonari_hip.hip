@@ -54,6 +54,8 @@ struct Views {
     long long* struct_bin_off;
     long long* struct_tasks;
     long long* struct_task_off;
+    long long* struct_ctasks;
+    long long* struct_ctask_off;
     int* atom_struct;
     int4* atom_wrap;
     void* atom_q;
@@ -80,6 +82,8 @@ static Views views(void* ws, const Layout& L) {
     v.struct_bin_off = (long long*)(base + L.struct_bin_off);
     v.struct_tasks = (long long*)(base + L.struct_tasks);
     v.struct_task_off = (long long*)(base + L.struct_task_off);
+    v.struct_ctasks = (long long*)(base + L.struct_ctasks);
+    v.struct_ctask_off = (long long*)(base + L.struct_ctask_off);
     v.atom_struct = (int*)(base + L.atom_struct);
     v.atom_wrap = (int4*)(base + L.atom_wrap);
     v.atom_q = base + L.atom_q;
@@ -158,6 +162,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.cells = (const T*)req->cell;
     q.recs = v.recs;
     q.struct_task_off = (const int64_t*)v.struct_task_off;
+    q.struct_ctask_off = (const int64_t*)v.struct_ctask_off;
     q.atom_struct = v.atom_struct;
     q.atom_wrap = v.atom_wrap;
     q.atom_q = (const Vec4<T>*)v.atom_q;
@@ -183,7 +188,7 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
     if constexpr (!EMIT) {
         (void)plan;
         (void)n_tasks;
-        k_cell_count<T, MODE><<<count_blocks<T, MODE>(4 * (L.cap_bins > n ? L.cap_bins : n)),
+        k_cell_count<T, MODE><<<count_blocks<T, MODE>(2 * (L.cap_bins > n ? L.cap_bins : n)),
                                 kBlock, 0, stream>>>(q);
     } else {
         if ((plan & 2) && n_tasks > 0)
@@ -225,9 +230,10 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     const int reach = req->stencil_reach;  // 0: chosen per structure
     k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kWave, 0, stream>>>(
         (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
-        v.block_partials, v.struct_bins, v.struct_tasks, v.status);
-    k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks, nb, v.struct_bin_off,
-                                            v.struct_task_off, v.recs, v.status, L.cap_bins);
+        v.block_partials, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.status);
+    k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks, v.struct_ctasks, nb,
+                                            v.struct_bin_off, v.struct_task_off,
+                                            v.struct_ctask_off, v.recs, v.status, L.cap_bins);
     if (n > 0 && req->algorithm != TNR_BRUTE_FORCE) {
         k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
                                                        (const Vec4<T>*)v.atom_q, v.atom_bin,
