@@ -1,22 +1,35 @@
 // Cell-list query kernels: the stencil walk over the bins of a structure in
-// a counting flavour (k_cell_count: pairs per source, persistent grid that
-// also counts the brute-force structures) and an emitting flavour
-// (k_cell_emit: writes i/j/P/S/d/D at the scanned offsets).
+// a counting flavour (k_cell_count: pairs per source and hit masks; a
+// persistent grid that also counts the brute-force structures) and an
+// emitting flavour (k_cell_emit: writes i/j/P/S/d/D at the scanned offsets).
 //
-// Work unit: one source bin per wave.  Its stencil (neighbouring bins with
-// their periodic images) is flattened into candidates; up to CH chunks of 64
-// candidates at a time are gathered into registers as image positions plus a
-// 32-bit identity key, and the bin's sources are broadcast one at a time
-// against them.  Stencils with more chunks than CH take several register
-// passes; stencils with more than kMapCap candidates take the slow path.
+// Work unit: one source bin per workgroup.  The four waves build the bin's
+// stencil once in LDS: the neighbouring bins with their periodic images,
+// cut into pieces (runs of consecutive z-bins of one (x, y) row with one
+// image k), flattened into candidates.  When the stencil holds at most
+// StageCap<T> candidates, their records (wrapped position and atom index) are
+// staged in LDS as well, so the distance tests and the pair writes read
+// candidates from LDS only; larger stencils read them from the binned array.
+// The waves then split the bin's sources.
+//
+//   counting: up to CH chunks of 64 candidates at a time are gathered into
+//             registers as image positions plus a 32-bit identity key, and
+//             the wave's sources are broadcast one at a time against them;
+//             one 64-bit hit mask per (source, chunk) is stored.
+//   emitting: no distance tests; the hit masks are decoded into an LDS list
+//             of (source, candidate) entries that are written 64 pairs per
+//             round, every lane busy and consecutive lanes writing
+//             consecutive pairs.
+//
+// Stencils with more than kMapCap candidates take a slow path that decides
+// every candidate in both passes.
 //
 // Reference: the cell-list query of csrc/torch/neighbors_cell_cuda.cu:294-442
 // (one warp per source walking linked lists) and csrc/core/neighbors_cpu.cpp:
 // 515-584; both apply the public predicate of neighbors_cpu.cpp:247-261.
 // Here a fused broad-phase distance classifies a candidate as inside
 // (d2 < inner2), outside (d2 >= outer2) or in the thin band between, which
-// the public predicate decides (cell_decide).  Both passes make the same
-// decisions: they run the same instructions on the same data.
+// the public predicate decides (cell_decide).
 #pragma once
 
 #include "nl_query.h"
@@ -24,7 +37,7 @@
 namespace tnr {
 
 constexpr int kMapCap = kMaskWords * kWave;  // candidates whose piece is mapped in LDS
-constexpr int kListCap = 1024;               // emit: compacted hits per flush
+constexpr int kListCap = 512;                // emit: compacted hits per flush
 
 // Chunks of 64 candidates held in registers per pass (at most).
 template <typename T>
@@ -38,12 +51,39 @@ struct RegChunks<double> {
     static constexpr int value = 8;
 };
 
-// Stencil of one source bin, one per wave in LDS.
+// Candidates of a stencil staged in LDS (at most); a multiple of kBlock.
+template <typename T>
+struct StageCap;
+template <>
+struct StageCap<float> {
+    static constexpr int value = 1024;
+};
+template <>
+struct StageCap<double> {
+    static constexpr int value = 768;
+};
+
+// Stencil of the workgroup's current bin in LDS.
 struct StencilLds {
-    int pre[kPieceCap + 1];        // exclusive prefix of piece lengths
-    int delta[kPieceCap];          // binned index = candidate index + delta
-    int kid[kPieceCap];            // packed image shift (k + 512 per 10 bits)
-    unsigned char piece[kMapCap];  // piece of each candidate (when C <= kMapCap)
+    int pre[kPieceCap + 1];             // exclusive prefix of piece lengths
+    int delta[kPieceCap];               // binned index = candidate index + delta
+    int kid[kPieceCap];                 // packed image shift (k + 512 per 10 bits)
+    unsigned char kfl[kPieceCap];       // bit 0: k == 0, bit 1: k < 0 (lexicographic)
+    unsigned char piece[kMapCap];       // piece of each candidate (when C <= kMapCap)
+    int wtot[kWavesPerBlock];           // block scan: wave totals
+    int wmax[kWavesPerBlock];           // block running maximum: wave maxima
+};
+
+// Tables of the emitting fast path: the image shift of every piece, and the
+// products fl(k * cell[a][c]) of the public formula for |k| <= kProdK per
+// axis a and component c (the output shift S equals the image shift k when
+// no representative is wrapped).
+constexpr int kProdK = 8;
+template <typename T>
+struct EmitTables {
+    int4 pk[kPieceCap];                  // (kx, ky, kz, 0)
+    T prod[3][2 * kProdK + 1][4];        // [axis][k + kProdK][component]
+    int kbig;                            // some piece has |k_a| > kProdK
 };
 
 __device__ __forceinline__ int pack_k(int kx, int ky, int kz) {
@@ -68,7 +108,8 @@ __device__ __forceinline__ void image_translation(int kk, const T c[9], T& tx, T
     tz = O::fma_(fz, c[8], O::fma_(fy, c[5], O::mul(fx, c[2])));
 }
 
-// Wave-uniform description of one source bin of a cell-list structure.
+// Workgroup-uniform description of one source bin of a cell-list structure;
+// sb, se hold the sources of the calling wave once they are split.
 template <typename T>
 struct CellBin {
     int b;            // structure
@@ -81,8 +122,8 @@ struct CellBin {
     bool wrapped, diagonal;
 };
 
-// Structure of the last task looked up by this wave: tasks [lo, hi) belong
-// to structure b.  Consecutive tasks of a wave usually share a structure.
+// Structure of the last bin looked up by this workgroup: bins [lo, hi)
+// belong to structure b.  Consecutive bins usually share a structure.
 struct StructCache {
     int b;
     int64_t lo, hi;
@@ -102,36 +143,28 @@ __device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb,
     return sc.b;
 }
 
-// Loads the structure and bin of a cell-list task and builds the bin's
-// stencil for the sources of the task: r.parts waves split a bin's sources,
-// each building the stencil itself.  Pieces are runs of
-// consecutive z-bins of one (x, y) row with one periodic image k, one lane
-// per piece; pieces with |k_a| > R_a are dropped, which keeps exactly the
-// reference's image box.  Fills the piece table of st (and, when tr is
-// given, the broad-phase translation of every piece) and resolves the
-// piece of every candidate into st.piece when C <= kMapCap.  Returns false when the bin holds no
-// source.
-// A task is one part of a bin: parts waves split the bin's sources.  The
-// counting kernel (tr given) uses the counting tasks (r.cparts per bin), the
-// emitting kernel the emitting tasks (r.parts per bin).
+// Builds the stencil of global bin g with the whole workgroup (every thread
+// calls it; it holds workgroup barriers).  Pieces are runs of consecutive
+// z-bins of one (x, y) row with one periodic image k, one thread per piece;
+// pieces with |k_a| > R_a are dropped, which keeps exactly the reference's
+// image box.  Fills the piece tables of st (and, when tr is given, the
+// broad-phase translation of every piece) and, when C <= kMapCap, the piece
+// of every candidate in st.piece (a workgroup running maximum of the marks
+// left at every piece start).  Returns false, before any barrier, when the
+// bin holds no source.  The caller separates two calls with a barrier.
 template <typename T>
-__device__ __forceinline__ bool cell_bin(const QueryArgs<T>& a, int64_t task, StructCache& sc,
-                                         CellBin<T>& cb, StencilLds& st,
-                                         T (*tr)[kPieceCap] = nullptr) {
+__device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, StructCache& sc,
+                                          CellBin<T>& cb, StencilLds& st,
+                                          T (*tr)[kPieceCap] = nullptr,
+                                          EmitTables<T>* et = nullptr) {
+    const int tid = threadIdx.x;
     const int lane = lane_id();
-    cb.b = structure_of_item(tr ? a.struct_ctask_off : a.struct_task_off, a.nb, task, sc);
-    const int parts = tr ? a.recs[cb.b].cparts : a.recs[cb.b].parts;
-    const unsigned local = (unsigned)(task - sc.lo);  // tasks of a structure fit in 32 bits
-    const unsigned lb = local / (unsigned)parts;
-    const int part = (int)(local - lb * (unsigned)parts);
-    const int64_t g = a.recs[cb.b].bin0 + lb;
+    const int wv = tid / kWave;
+    cb.b = structure_of_item(a.struct_bin_off, a.nb, g, sc);
     const StructRec& r = a.recs[cb.b];
     const unsigned lbin = (unsigned)(g - r.bin0);  // bins of a structure fit in 32 bits
-    const int sb = uniform(a.bin_start[g]), se = uniform(a.bin_start[g + 1]);
-    // sources of this part: the part-th share of the bin's sources
-    const int q = (se - sb + parts - 1) / parts;
-    cb.sb = sb + part * q;
-    cb.se = min(se, cb.sb + q);
+    cb.sb = uniform(a.bin_start[g]);
+    cb.se = uniform(a.bin_start[g + 1]);
     if (cb.sb >= cb.se) return false;
     const T* cell = a.cells + 9 * cb.b;
 #pragma unroll
@@ -151,95 +184,173 @@ __device__ __forceinline__ bool cell_bin(const QueryArgs<T>& a, int64_t task, St
     const int iy = (int)(rest % (unsigned)ny);
     const int ix = (int)(rest / (unsigned)ny);
     const int RY = 2 * Ky + 1;
-    const int npieces = (2 * Kx + 1) * RY * zs;
+    const int npieces = (2 * Kx + 1) * RY * zs;  // at most kPieceCap < kBlock
     cb.npieces = npieces;
     const int* bstart = a.bin_start + r.bin0;
-    // p / zs and row / RY through a float reciprocal: p < 2^8 and divisors
-    // below 2^8, so (p + 1/2) / d lies at least 1/512 from an integer while
-    // the float error stays below 2^-15.
-    const float rzs = 1.0f / (float)zs, rry = 1.0f / (float)RY;
     const int zlo = iz - Kz, zhi = iz + Kz;
     int kz0 = 0;  // image of the lowest stencil z-bin (zlo < nz)
     if (perz)
         for (int zz = zlo; zz < 0; zz += nz) --kz0;
-    // clear the piece marks
-#pragma unroll
-    for (int q = 0; q < kMapCap / (8 * kWave); ++q)
-        reinterpret_cast<unsigned long long*>(st.piece)[q * kWave + lane] = 0ull;
-
-    int carry = 0;
-    for (int base = 0; base < npieces; base += kWave) {
-        const int p = base + lane;
-        int len = 0, start = 0, kx = 0, ky = 0, kz = 0;
-        if (p < npieces) {
-            const int row = (int)(((float)p + 0.5f) * rzs);
-            const int seg = p - row * zs;
-            const int rx = (int)(((float)row + 0.5f) * rry);
-            int jx = ix + rx - Kx, jy = iy + (row - rx * RY) - Ky;
-            bool ok;
-            if (perx) {
-                while (jx < 0) { jx += nx; --kx; }
-                while (jx >= nx) { jx -= nx; ++kx; }
-                ok = abs(kx) <= R0;
-            } else {
-                ok = jx >= 0 && jx < nx;
-            }
-            if (pery) {
-                while (jy < 0) { jy += ny; --ky; }
-                while (jy >= ny) { jy -= ny; ++ky; }
-                ok = ok && abs(ky) <= R1;
-            } else {
-                ok = ok && jy >= 0 && jy < ny;
-            }
-            int z0, z1;
-            if (perz) {
-                kz = kz0 + seg;
-                const int zbeg = seg == 0 ? zlo : kz * nz;
-                const int zend = min(zhi, (kz + 1) * nz - 1);
-                ok = ok && zbeg <= zhi && abs(kz) <= R2;
-                z0 = zbeg - kz * nz;
-                z1 = zend - kz * nz;
-            } else {
-                z0 = max(0, zlo);
-                z1 = min(nz - 1, zhi);
-                ok = ok && seg == 0 && z0 <= z1;
-            }
-            if (ok) {
-                const int rowbase = (jx * ny + jy) * nz;
-                start = bstart[rowbase + z0];
-                len = bstart[rowbase + z1 + 1] - start;
-            }
+    // clear the piece marks (the previous bin's users passed a barrier)
+    reinterpret_cast<unsigned long long*>(st.piece)[tid] = 0ull;
+    static_assert(kMapCap == 8 * kBlock, "one 8-byte word of piece marks per thread");
+    if (et) {
+        if (tid == 0) et->kbig = 0;
+        constexpr int NP = 3 * (2 * kProdK + 1) * 3;
+        static_assert(NP <= kBlock, "one product per thread");
+        if (tid < NP) {
+            const int ax = tid / (3 * (2 * kProdK + 1));
+            const int rest_ = tid - ax * 3 * (2 * kProdK + 1);
+            const int kv = rest_ / 3 - kProdK, c = rest_ % 3;
+            et->prod[ax][kv + kProdK][c] = Ops<T>::mul((T)kv, cell[3 * ax + c]);
         }
-        const int inc = wave_inclusive_scan_i32(len);
-        if (p < npieces) {
-            const int ex = carry + inc - len;
-            const int kk = pack_k(kx, ky, kz);
-            st.pre[p] = ex;
-            st.delta[p] = start - ex;
-            st.kid[p] = kk;
-            if (len > 0 && ex < kMapCap) st.piece[ex] = (unsigned char)p;
-            if (tr) image_translation(kk, cb.c, tr[0][p], tr[1][p], tr[2][p]);
-        }
-        carry += __builtin_amdgcn_readlane(inc, kWave - 1);
     }
-    if (lane == 0) st.pre[npieces] = carry;
-    cb.C = uniform(carry);
-    cb.nch = (cb.C + kWave - 1) / kWave;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    if (cb.C <= kMapCap) {
-        // piece of candidate v: running maximum of the piece marks up to v
-        int run = 0;
-        for (int j = 0; j < cb.nch; ++j) {
-            const int v = j * kWave + lane;
-            const int p = max(wave_inclusive_max_i32((int)st.piece[v]), run);
-            run = __builtin_amdgcn_readlane(p, kWave - 1);
-            st.piece[v] = (unsigned char)p;
+
+    const int p = tid;
+    int len = 0, start = 0, kx = 0, ky = 0, kz = 0;
+    if (p < npieces) {
+        // p / zs and row / RY through a float reciprocal: p < 2^8 and divisors
+        // below 2^8, so (p + 1/2) / d lies at least 1/512 from an integer while
+        // the float error stays below 2^-15.
+        const float rzs = 1.0f / (float)zs, rry = 1.0f / (float)RY;
+        const int row = (int)(((float)p + 0.5f) * rzs);
+        const int seg = p - row * zs;
+        const int rx = (int)(((float)row + 0.5f) * rry);
+        int jx = ix + rx - Kx, jy = iy + (row - rx * RY) - Ky;
+        bool ok;
+        if (perx) {
+            while (jx < 0) { jx += nx; --kx; }
+            while (jx >= nx) { jx -= nx; ++kx; }
+            ok = abs(kx) <= R0;
+        } else {
+            ok = jx >= 0 && jx < nx;
         }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (pery) {
+            while (jy < 0) { jy += ny; --ky; }
+            while (jy >= ny) { jy -= ny; ++ky; }
+            ok = ok && abs(ky) <= R1;
+        } else {
+            ok = ok && jy >= 0 && jy < ny;
+        }
+        int z0, z1;
+        if (perz) {
+            kz = kz0 + seg;
+            const int zbeg = seg == 0 ? zlo : kz * nz;
+            const int zend = min(zhi, (kz + 1) * nz - 1);
+            ok = ok && zbeg <= zhi && abs(kz) <= R2;
+            z0 = zbeg - kz * nz;
+            z1 = zend - kz * nz;
+        } else {
+            z0 = max(0, zlo);
+            z1 = min(nz - 1, zhi);
+            ok = ok && seg == 0 && z0 <= z1;
+        }
+        if (ok) {
+            const int rowbase = (jx * ny + jy) * nz;
+            start = bstart[rowbase + z0];
+            len = bstart[rowbase + z1 + 1] - start;
+        }
+    }
+    // workgroup exclusive scan of the piece lengths
+    const int inc = wave_inclusive_scan_i32(len);
+    if (lane == kWave - 1) st.wtot[wv] = inc;
+    __syncthreads();  // also orders the mark clearing before the marks
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+        const int t = st.wtot[w];
+        before += w < wv ? t : 0;
+        total += t;
+    }
+    if (p < npieces) {
+        const int ex = before + inc - len;
+        const int kk = pack_k(kx, ky, kz);
+        st.pre[p] = ex;
+        st.delta[p] = start - ex;
+        st.kid[p] = kk;
+        st.kfl[p] = (unsigned char)((kx == 0 && ky == 0 && kz == 0 ? 1 : 0) |
+                                    (lex_negative(kx, ky, kz) ? 2 : 0));
+        if (len > 0 && ex < kMapCap) st.piece[ex] = (unsigned char)p;
+        if (tr) image_translation(kk, cb.c, tr[0][p], tr[1][p], tr[2][p]);
+        if (et) {
+            et->pk[p] = make_int4(kx, ky, kz, 0);
+            if (abs(kx) > kProdK || abs(ky) > kProdK || abs(kz) > kProdK) et->kbig = 1;
+        }
+    }
+    if (tid == 0) st.pre[npieces] = total;
+    cb.C = uniform(total);
+    cb.nch = (cb.C + kWave - 1) / kWave;
+    __syncthreads();
+    if (cb.C <= kMapCap) {
+        // piece of candidate v: running maximum of the marks up to v, eight
+        // candidates per thread
+        unsigned long long w8 = reinterpret_cast<const unsigned long long*>(st.piece)[tid];
+        int run = 0;
+        int m[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            run = max(run, (int)((w8 >> (8 * k)) & 0xffull));
+            m[k] = run;
+        }
+        const int incm = wave_inclusive_max_i32(run);
+        int exm = __shfl_up(incm, 1);
+        if (lane == 0) exm = 0;
+        if (lane == kWave - 1) st.wmax[wv] = incm;
+        __syncthreads();
+        int carry = exm;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w)
+            if (w < wv) carry = max(carry, st.wmax[w]);
+        w8 = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) w8 |= (unsigned long long)max(carry, m[k]) << (8 * k);
+        reinterpret_cast<unsigned long long*>(st.piece)[tid] = w8;
+        __syncthreads();
     }
     return true;
+}
+
+// Copies the records of the C <= StageCap<T> candidates into LDS (every
+// thread calls it; ends with a workgroup barrier).
+template <typename T>
+__device__ __forceinline__ void stage_candidates(const QueryArgs<T>& a, const StencilLds& st,
+                                                 int C, Vec4<T>* cand) {
+    constexpr int NS = StageCap<T>::value / kBlock;
+    const int tid = threadIdx.x;
+    Vec4<T> rec[NS];
+    // every load is issued before the first is needed: slots past C re-read
+    // candidate 0 (C >= 1) and are not stored
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const int v0 = tid + k * kBlock;
+        const int v = v0 < C ? v0 : 0;
+        rec[k] = a.binned[v + st.delta[st.piece[v]]];
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const int v = tid + k * kBlock;
+        if (v < C) cand[v] = rec[k];
+    }
+    __syncthreads();
+}
+
+// Sources of the calling wave: the wv-th quarter of the bin's sources.
+template <typename T>
+__device__ __forceinline__ void wave_sources(CellBin<T>& cb) {
+    const int wv = uniform(threadIdx.x / kWave);
+    const int n = cb.se - cb.sb;
+    const int q = (n + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int s0 = cb.sb + wv * q;
+    cb.se = min(cb.se, s0 + q);
+    cb.sb = s0;
+}
+
+// Record of candidate v in piece p: from LDS when staged.
+template <typename T, bool STAGED>
+__device__ __forceinline__ Vec4<T> cand_record(const QueryArgs<T>& a, const StencilLds& st,
+                                               const Vec4<T>* cand, int p, int v) {
+    if constexpr (STAGED) return cand[v];
+    return a.binned[v + st.delta[p]];
 }
 
 // The band between inner2 and outer2: decided by the public predicate on the
@@ -328,14 +439,14 @@ __device__ __forceinline__ int stencil_piece(const StencilLds& st, int v, int np
 
 // Writes one kept candidate of source si: the output shift is the image k
 // corrected by the representatives' wraps; D uses the original positions.
-template <typename T>
+template <typename T, bool WRAPPED>
 __device__ __forceinline__ void cell_write(const QueryArgs<T>& a, long long o, int si, int tid,
                                            int kk, T rx, T ry, T rz, T sx, T sy, T sz,
                                            const CellBin<T>& cb) {
     int kx, ky, kz;
     unpack_k(kk, kx, ky, kz);
     T ps[3] = {sx, sy, sz}, pt[3] = {rx, ry, rz};
-    if (cb.wrapped) {
+    if (WRAPPED) {
         const int4 wt = a.atom_wrap[tid];
         const int4 ws = a.atom_wrap[si];
         kx = shift_i32(kx, wt.x, ws.x);
@@ -384,9 +495,14 @@ __device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLd
                     if (lane == gi) acc += __popcll(m);
                 } else if (m) {
                     const long long base = read_lane(cur, gi);
-                    if (ok)
-                        cell_write(a, base + lanes_below(m), si, tid, kk, rec.x, rec.y, rec.z, sx,
-                                   sy, sz, cb);
+                    if (ok) {
+                        if (cb.wrapped)
+                            cell_write<T, true>(a, base + lanes_below(m), si, tid, kk, rec.x,
+                                                rec.y, rec.z, sx, sy, sz, cb);
+                        else
+                            cell_write<T, false>(a, base + lanes_below(m), si, tid, kk, rec.x,
+                                                 rec.y, rec.z, sx, sy, sz, cb);
+                    }
                     if (lane == gi) cur += __popcll(m);
                 }
             }
@@ -406,6 +522,7 @@ struct Chunks {
 
 template <typename T, int MODE, int NC>
 __device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const StencilLds& st,
+                                            const Vec4<T>* cand, bool staged,
                                             const T (*tr)[kPieceCap], const CellBin<T>& cb,
                                             int c0, Chunks<T, NC>& cd) {
     using O = Ops<T>;
@@ -419,12 +536,9 @@ __device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const Stencil
             const int v = (c0 + j) * kWave + lane;
             if (v < cb.C) {
                 const int p = st.piece[v];
-                const Vec4<T> rec = a.binned[v + st.delta[p]];
-                const int kk = st.kid[p];
-                int kx, ky, kz;
-                unpack_k(kk, kx, ky, kz);
-                cd.key[j] = identity_key<MODE>(as_idx(rec.w), kk == pack_k(0, 0, 0),
-                                               lex_negative(kx, ky, kz));
+                const Vec4<T> rec = staged ? cand[v] : a.binned[v + st.delta[p]];
+                const int f = st.kfl[p];
+                cd.key[j] = identity_key<MODE>(as_idx(rec.w), (f & 1) != 0, (f & 2) != 0);
                 cd.x[j] = O::add(rec.x, tr[0][p]);
                 cd.y[j] = O::add(rec.y, tr[1][p]);
                 cd.z[j] = O::add(rec.z, tr[2][p]);
@@ -463,9 +577,9 @@ __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLd
     const int lane = lane_id();
     unsigned band = 0;
     int cnt = 0;
-    mv = 0;
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
+    int mlo = 0, mhi = 0;  // lane j: the two halves of the mask of chunk c0 + j
+    static_for<NC>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
         const T dx = O::sub(cd.x[j], sx), dy = O::sub(cd.y[j], sy), dz = O::sub(cd.z[j], sz);
         const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
         unsigned long long mk = __builtin_amdgcn_ballot_w64(d2 < cb.outer2);
@@ -474,8 +588,10 @@ __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLd
         const unsigned long long m = mk & mi;
         band |= (mk & ~mi) ? (1u << j) : 0u;
         cnt += __popcll(m);
-        if (lane == j) mv = m;
-    }
+        mlo = write_lane<j>(mlo, (int)(unsigned)m);
+        mhi = write_lane<j>(mhi, (int)(unsigned)(m >> 32));
+    });
+    mv = ((unsigned long long)(unsigned)mhi << 32) | (unsigned)mlo;
     if (band) {
         for (int j = 0; j < NC; ++j) {
             if (!((band >> j) & 1u)) continue;
@@ -488,11 +604,12 @@ __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLd
     return cnt;
 }
 
-// Counting, register path of one bin: source groups of 64, register passes
-// of NC chunks.  Writes counts[s] and, per source, the hit mask of every
-// chunk (masks[binned index][chunk]) for the emitting pass.
+// Counting, register path of the wave's sources: source groups of 64,
+// register passes of NC chunks.  Writes counts[s] and, per source, the hit
+// mask of every chunk (masks[binned index][chunk]) for the emitting pass.
 template <typename T, int MODE, int NC>
 __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLds& st,
+                                          const Vec4<T>* cand, bool staged,
                                           const T (*tr)[kPieceCap], const CellBin<T>& cb) {
     const int lane = lane_id();
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
@@ -503,7 +620,7 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
         long long acc = 0;  // lane gi: pairs of source gi so far
         for (int c0 = 0; c0 < cb.nch; c0 += NC) {
             Chunks<T, NC> cd;
-            gather_pass<T, MODE, NC>(a, st, tr, cb, c0, cd);
+            gather_pass<T, MODE, NC>(a, st, cand, staged, tr, cb, c0, cd);
             const bool store = lane < NC && c0 + lane < cb.nch;
 #pragma unroll 1
             for (int gi = 0; gi < ns; ++gi) {
@@ -530,28 +647,39 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
     }
 }
 
-// The register path with the fewest chunks per pass that hold the bin's
-// stencil (passes of RegChunks<T> chunks beyond that).
+// The register path with exactly as many chunks per pass as the bin's
+// stencil holds (passes of RegChunks<T> chunks beyond that).
 template <typename T, int MODE>
 __device__ __forceinline__ void count_bin_any(const QueryArgs<T>& a, const StencilLds& st,
+                                              const Vec4<T>* cand, bool staged,
                                               const T (*tr)[kPieceCap], const CellBin<T>& cb) {
     constexpr int CH = RegChunks<T>::value;
-    if (cb.nch <= 4)
-        count_bin<T, MODE, 4>(a, st, tr, cb);
-    else if (cb.nch <= 8 || CH == 8)
-        count_bin<T, MODE, 8>(a, st, tr, cb);
-    else
-        count_bin<T, MODE, CH>(a, st, tr, cb);
+    switch (cb.nch < CH ? cb.nch : CH) {
+#define TNR_COUNT_NC(n) \
+    case n:             \
+        if constexpr (n <= CH) count_bin<T, MODE, n>(a, st, cand, staged, tr, cb); \
+        break;
+        TNR_COUNT_NC(1) TNR_COUNT_NC(2) TNR_COUNT_NC(3) TNR_COUNT_NC(4) TNR_COUNT_NC(5)
+        TNR_COUNT_NC(6) TNR_COUNT_NC(7) TNR_COUNT_NC(8) TNR_COUNT_NC(9) TNR_COUNT_NC(10)
+        TNR_COUNT_NC(11) TNR_COUNT_NC(12)
+#undef TNR_COUNT_NC
+        default: break;
+    }
 }
 
-// Emitting, register path of one bin: no distance tests, the hit masks of
-// the counting pass are decoded.  Sources are taken S = 64 / nch at a time,
-// lane (s, j) holding the mask of chunk j of source s; a wave scan of the
-// mask popcounts places every hit in the wave's LDS list (entry = owner lane
-// << 6 | bit), which is written out in rounds of 64 consecutive pairs.
-template <typename T>
+// Emitting, register path of the wave's sources: no distance tests, the hit
+// masks of the counting pass are decoded.  Sources are taken S = 64 / nch at
+// a time, lane (s, j) holding the mask of chunk j of source s; a wave scan of
+// the mask popcounts places every hit in the wave's LDS list (entry = owner
+// lane << 6 | bit), which is written out in rounds of 64 consecutive pairs.
+// With STAGED the candidate records come from LDS; without WRAPPED the
+// source and target positions are the records themselves.  Both together
+// leave a round with no global load, so the pair stores stream without
+// waits (a wait for a load also waits for every earlier store).
+template <typename T, bool STAGED, bool WRAPPED>
 __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds& st,
-                                         const CellBin<T>& cb, unsigned short* list) {
+                                         const Vec4<T>* cand, const CellBin<T>& cb,
+                                         unsigned short* list) {
     const int lane = lane_id();
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
     const int nch = cb.nch;
@@ -608,7 +736,7 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                         const int v = (tg_ & 63) * kWave + (e_ & 63);
                         const int p = st.piece[v];
                         kk_ = st.kid[p];
-                        rec_ = a.binned[v + st.delta[p]];
+                        rec_ = cand_record<T, STAGED>(a, st, cand, p, v);
                     }
                 };
                 fetch(lane, e, tg, kk, rec);
@@ -621,8 +749,8 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                     const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                     const int si = __shfl(sidx, g);
                     if (r0 + lane < L)
-                        cell_write(a, o, si, as_idx(rec.w), kk, rec.x, rec.y, rec.z, sx, sy, sz,
-                                   cb);
+                        cell_write<T, WRAPPED>(a, o, si, as_idx(rec.w), kk, rec.x, rec.y, rec.z,
+                                               sx, sy, sz, cb);
                     e = e_n;
                     tg = tg_n;
                     kk = kk_n;
@@ -633,60 +761,234 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
     }
 }
 
-// Static XCD-aware split of W work items over the waves of a grid: block b
-// runs on XCD b % 8 (the hardware deals blocks round-robin), items are cut
-// into 8 contiguous ranges and the waves of XCD x stride over range x, so
-// neighbouring bins share one L2.
-struct WaveRange {
+// Emitting fast path: staged candidates, no wrapped representative (the
+// output shift is the image shift k and positions are the records), every
+// |k_a| <= kProdK.  The same decode as emit_bin; a round reads only LDS:
+// the list entry, the owner lane's tag, the candidate record and piece, the
+// piece's shift and the products fl(k_a * cell[a][c]), and evaluates D with
+// the public formula's operation order.  Each source's output range
+// [offsets[s], offsets[s] + hits) is checked against E once; a source that
+// does not fit raises ST_CAPACITY and writes nothing.
+template <typename T>
+__device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLds& st,
+                                          const Vec4<T>* cand, const EmitTables<T>& et,
+                                          const CellBin<T>& cb, unsigned short* list) {
+    using O = Ops<T>;
+    const int lane = lane_id();
+    const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
+    const int nch = cb.nch;
+    const int S = kWave / nch;
+    const int sl = (int)(((float)lane + 0.5f) / (float)nch);  // lane = sl * nch + j
+    const int j = lane - sl * nch;
+    const bool want_d = a.dist != nullptr;
+    const bool want_vec = a.vec != nullptr || want_d;
+    for (int sg = cb.sb; sg < cb.se; sg += kWave) {
+        const int ns = min(kWave, cb.se - sg);
+        const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
+        const int sidx = as_idx(sq.w);
+        const long long cur = lane < ns ? a.offsets[sidx] : 0;  // lane gi: first output of gi
+        auto mask_of = [&](int s0_) -> unsigned long long {
+            const int gi_ = s0_ + sl;
+            return sl < S && gi_ < ns ? a.masks[(int64_t)(sg + gi_) * kMaskWords + j] : 0ull;
+        };
+        unsigned long long m_next = mask_of(0);
+        for (int s0 = 0; s0 < ns; s0 += S) {
+            const int gi = min(s0 + sl, kWave - 1);
+            unsigned long long m = m_next;
+            if (s0 + S < ns) m_next = mask_of(s0 + S);
+            int c = __popcll(m);
+            int incl = wave_inclusive_scan_i32(c);
+            // output range check of each source of the group (lane sl * nch)
+            {
+                const int first = __shfl(incl - c, min(sl, S - 1) * nch);
+                const int last = __shfl(incl, min(sl, S - 1) * nch + nch - 1);
+                const long long o0 = __shfl(cur, gi);
+                const bool bad = sl < S && s0 + sl < ns &&
+                                 (o0 < 0 || o0 + (last - first) > a.limit);
+                if (__builtin_amdgcn_ballot_w64(bad)) {
+                    if (bad) {
+                        m = 0;
+                        atomicOr(a.status + SS_FLAGS, ST_CAPACITY);
+                    }
+                    c = __popcll(m);
+                    incl = wave_inclusive_scan_i32(c);
+                }
+            }
+            const int pos = incl - c;  // list position of this lane's first hit
+            const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+            const int first = __shfl(pos, min(sl, S - 1) * nch);
+            const long long ob = __shfl(cur, gi) - first;
+            const int tag = (gi << 6) | j;  // owner data: source lane, chunk
+            for (int base = 0; base < total; base += kListCap) {
+                const int L = min(kListCap, total - base);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                if (total <= kListCap) {
+                    // every entry fits: the two mask halves, no range checks
+                    unsigned lo = (unsigned)m, hi = (unsigned)(m >> 32);
+                    int r = pos;
+                    while (lo) {
+                        const int bit = __builtin_ctz(lo);
+                        lo &= lo - 1;
+                        list[r++] = (unsigned short)((lane << 6) | bit);
+                    }
+                    while (hi) {
+                        const int bit = __builtin_ctz(hi) + 32;
+                        hi &= hi - 1;
+                        list[r++] = (unsigned short)((lane << 6) | bit);
+                    }
+                } else {
+                    unsigned long long mm = m;
+                    int r = pos - base;
+                    while (mm) {
+                        const int bit = __builtin_ctzll(mm);
+                        mm &= mm - 1;
+                        if (r >= 0 && r < L) list[r] = (unsigned short)((lane << 6) | bit);
+                        ++r;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+                // rounds of 64 entries; the next round's LDS reads are issued ahead
+                // entry e = owner lane w << 6 | bit; the owner lane holds the
+                // tag (source lane, chunk) and the output base of its word
+                auto fetch = [&](int r, int& w_, int& tg_, Vec4<T>& rec_, int4& k_) {
+                    const int e_ = list[min(r, L - 1)];
+                    w_ = e_ >> 6;
+                    tg_ = __shfl(tag, w_);
+                    const int v = ((tg_ & 63) << 6) | (e_ & 63);
+                    rec_ = cand[v];
+                    k_ = et.pk[st.piece[v]];
+                };
+                int w, tg;
+                Vec4<T> rec;
+                int4 k;
+                fetch(lane, w, tg, rec, k);
+                for (int r0 = 0; r0 < L; r0 += kWave) {
+                    int w_n, tg_n;
+                    Vec4<T> rec_n;
+                    int4 k_n;
+                    fetch(r0 + kWave + lane, w_n, tg_n, rec_n, k_n);
+                    const int g = tg >> 6;
+                    const long long o = __shfl(ob, w) + base + r0 + lane;
+                    const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
+                    const int si = __shfl(sidx, g);
+                    if (r0 + lane < L) {
+                        const int t = as_idx(rec.w);
+                        if (a.pairs) {
+                            long2 v;
+                            v.x = si;
+                            v.y = t;
+                            *reinterpret_cast<long2*>(a.pairs + 2 * o) = v;
+                        }
+                        if (a.src) a.src[o] = si;
+                        if (a.dst) a.dst[o] = t;
+                        if (a.shifts) {
+                            Triple<int32_t> v;
+                            v.x = k.x;
+                            v.y = k.y;
+                            v.z = k.z;
+                            *reinterpret_cast<Triple<int32_t>*>(a.shifts + 3 * o) = v;
+                        }
+                        if (want_vec) {
+                            T D0 = O::sub(rec.x, sx), D1 = O::sub(rec.y, sy), D2 = O::sub(rec.z, sz);
+                            if (cb.diagonal) {
+                                D0 = O::add(D0, et.prod[0][k.x + kProdK][0]);
+                                D1 = O::add(D1, et.prod[1][k.y + kProdK][1]);
+                                D2 = O::add(D2, et.prod[2][k.z + kProdK][2]);
+                            } else {
+                                const T* px = et.prod[0][k.x + kProdK];
+                                const T* py = et.prod[1][k.y + kProdK];
+                                const T* pz = et.prod[2][k.z + kProdK];
+                                D0 = O::add(O::add(O::add(D0, px[0]), py[0]), pz[0]);
+                                D1 = O::add(O::add(O::add(D1, px[1]), py[1]), pz[1]);
+                                D2 = O::add(O::add(O::add(D2, px[2]), py[2]), pz[2]);
+                            }
+                            if (a.vec) {
+                                Triple<T> v;
+                                v.x = D0;
+                                v.y = D1;
+                                v.z = D2;
+                                *reinterpret_cast<Triple<T>*>(a.vec + 3 * o) = v;
+                            }
+                            if (want_d) {
+                                T d2 = O::mul(D0, D0);
+                                d2 = O::add(d2, O::mul(D1, D1));
+                                d2 = O::add(d2, O::mul(D2, D2));
+                                a.dist[o] = O::sqrt_(d2);
+                            }
+                        }
+                    }
+                    w = w_n;
+                    tg = tg_n;
+                    rec = rec_n;
+                    k = k_n;
+                }
+            }
+        }
+    }
+}
+
+// Static XCD-aware split of W work items over the workgroups of a grid:
+// workgroup b runs on XCD b % 8 (the hardware deals workgroups round-robin),
+// items are cut into 8 contiguous ranges and the workgroups of XCD x stride
+// over range x, so neighbouring bins share one L2.
+struct ItemRange {
     int64_t first, end, step;
 };
-__device__ __forceinline__ WaveRange xcd_range(int64_t W, int wv) {
+__device__ __forceinline__ ItemRange xcd_block_range(int64_t W) {
     const unsigned nblk = gridDim.x;
-    WaveRange r;
+    ItemRange r;
     if ((nblk & 7u) != 0) {
-        r.first = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+        r.first = blockIdx.x;
         r.end = W;
-        r.step = (int64_t)nblk * kWavesPerBlock;
+        r.step = nblk;
         return r;
     }
     const int64_t per = (W + 7) / 8;
     const int64_t x = blockIdx.x & 7u;
-    r.first = x * per + (int64_t)(blockIdx.x >> 3) * kWavesPerBlock + wv;
+    r.first = x * per + (int64_t)(blockIdx.x >> 3);
     r.end = min(W, (x + 1) * per);
-    r.step = (int64_t)(nblk >> 3) * kWavesPerBlock;
+    r.step = (int64_t)(nblk >> 3);
     return r;
 }
 
-// Counting pass, persistent grid: every wave walks its share of the
-// counting tasks (bin parts) of the cell-list structures, then of the source atoms of the
-// brute-force structures, and writes counts[s] for each source s.  The
-// status word is read once: abort bits only come from earlier kernels.
+// Counting pass, persistent grid: every workgroup walks its share of the
+// bins of the cell-list structures (one bin at a time, stencil built and
+// staged once, sources split over the four waves), then every wave its
+// share of the source atoms of the brute-force structures; writes counts[s]
+// for each source s.  The status word is read once: abort bits only come
+// from earlier kernels.
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? 4 : 1))) void
 k_cell_count(
     QueryArgs<T> a) {
-    __shared__ StencilLds s_st[kWavesPerBlock];
-    __shared__ T s_tr[kWavesPerBlock][3][kPieceCap];
+    __shared__ StencilLds s_st;
+    __shared__ T s_tr[3][kPieceCap];
+    __shared__ Vec4<T> s_cand[StageCap<T>::value];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
     const unsigned long long plan = load_status(a.status + SS_PLAN);
-    const int wv = uniform(threadIdx.x / kWave);
-    StencilLds& st = s_st[wv];
-    T(*tr)[kPieceCap] = s_tr[wv];
 
     if (plan & 2) {
-        const WaveRange wr = xcd_range(a.struct_ctask_off[a.nb], wv);
+        const ItemRange br = xcd_block_range(a.struct_bin_off[a.nb]);
         StructCache sc{0, 0, 0};
-        for (int64_t t = wr.first; t < wr.end; t += wr.step) {
+        for (int64_t g = br.first; g < br.end; g += br.step) {
             CellBin<T> cb;
-            if (!cell_bin<T>(a, t, sc, cb, st, tr)) continue;
-            if (cb.C > kMapCap)
-                cell_slow<T, MODE, false>(a, st, cb);
-            else
-                count_bin_any<T, MODE>(a, st, tr, cb);
+            if (block_bin<T>(a, g, sc, cb, s_st, s_tr)) {
+                const bool staged = cb.C <= StageCap<T>::value;
+                if (staged) stage_candidates<T>(a, s_st, cb.C, s_cand);
+                wave_sources(cb);
+                if (cb.C <= kMapCap)
+                    count_bin_any<T, MODE>(a, s_st, s_cand, staged, s_tr, cb);
+                else
+                    cell_slow<T, MODE, false>(a, s_st, cb);
+            }
+            __syncthreads();  // the bin's LDS is free
         }
     }
     if (plan & 1) {
+        const int wv = uniform(threadIdx.x / kWave);
         const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
         for (int64_t s = (int64_t)blockIdx.x * kWavesPerBlock + wv; s < a.n_atoms; s += nwaves) {
             const int b = a.atom_struct[s];
@@ -697,30 +999,48 @@ k_cell_count(
 }
 
 static_assert(kMapCap == kMaskWords * kWave, "one mask word per chunk of the piece map");
+static_assert(StageCap<float>::value % kBlock == 0 && StageCap<double>::value % kBlock == 0,
+              "staging copies whole workgroup strides");
+static_assert(StageCap<float>::value <= kMapCap && StageCap<double>::value <= kMapCap,
+              "staged stencils have a piece map");
 
-// Emitting pass: one wave per (source bin, part) task, blocks mapped
-// XCD-aware (block b runs on XCD b % 8; XCD x takes the x-th eighth of the
-// tasks).  The grid covers the tasks of the count (out->n_tasks), so the
-// kernel can run again on the same workspace.
+// Emitting pass: one workgroup per bin, mapped XCD-aware (workgroup b runs
+// on XCD b % 8; XCD x takes the x-th eighth of the bins).  The grid covers
+// the bins of the count (out->n_tasks), so the kernel can run again on the
+// same workspace.
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) void k_cell_emit(
     QueryArgs<T> a) {
-    __shared__ StencilLds s_st[kWavesPerBlock];
+    __shared__ StencilLds s_st;
+    __shared__ EmitTables<T> s_et;
+    __shared__ Vec4<T> s_cand[StageCap<T>::value];
     __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
-    const int wv = uniform(threadIdx.x / kWave);
-    const WaveRange wr = xcd_range(a.struct_task_off[a.nb], wv);
-    const int64_t t = wr.first;
-    if (t >= wr.end) return;
-    StencilLds& st = s_st[wv];
+    const ItemRange br = xcd_block_range(a.struct_bin_off[a.nb]);
+    const int64_t g = br.first;
+    if (g >= br.end) return;
     StructCache sc{0, 0, 0};
     CellBin<T> cb;
-    if (!cell_bin<T>(a, t, sc, cb, st)) return;
-    if (cb.C > kMapCap)
-        cell_slow<T, MODE, true>(a, st, cb);
-    else
-        emit_bin<T>(a, st, cb, s_list[wv]);
+    if (!block_bin<T>(a, g, sc, cb, s_st, nullptr, &s_et)) return;
+    const int wv = uniform(threadIdx.x / kWave);
+    if (cb.C <= StageCap<T>::value && !cb.wrapped) {
+        stage_candidates<T>(a, s_st, cb.C, s_cand);
+        wave_sources(cb);
+        if (!s_et.kbig)
+            emit_fast<T>(a, s_st, s_cand, s_et, cb, s_list[wv]);
+        else
+            emit_bin<T, true, false>(a, s_st, s_cand, cb, s_list[wv]);
+    } else if (cb.C <= kMapCap) {
+        wave_sources(cb);
+        if (cb.wrapped)
+            emit_bin<T, false, true>(a, s_st, s_cand, cb, s_list[wv]);
+        else
+            emit_bin<T, false, false>(a, s_st, s_cand, cb, s_list[wv]);
+    } else {
+        wave_sources(cb);
+        cell_slow<T, MODE, true>(a, s_st, cb);
+    }
 }
 
 }  // namespace tnr

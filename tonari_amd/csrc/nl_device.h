@@ -9,6 +9,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 namespace tnr {
 
@@ -16,9 +17,6 @@ constexpr int kWave = 64;
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kPieceCap = 192;            // stencil pieces per source bin
-// Sources of a cell-list bin per wave of the query kernels (a bin's sources
-// are split over up to 4 waves).
-constexpr double kSourcesPerPart = 6.0;
 
 // Automatic stencil reach: the smallest reach whose estimated stencil holds
 // at most this many candidates (one register pass of the counting kernel
@@ -205,6 +203,25 @@ __device__ __forceinline__ long long read_lane(long long v, int l) {
     const int lo = __builtin_amdgcn_readlane((int)(v & 0xffffffffll), l);
     const int hi = __builtin_amdgcn_readlane((int)(v >> 32), l);
     return ((long long)hi << 32) | (unsigned int)lo;
+}
+
+// Copy of `old` whose lane L holds the wave-uniform value `v`
+// (v_writelane_b32 with an immediate lane: one VALU instruction).
+template <int L>
+__device__ __forceinline__ int write_lane(int old, int v) {
+    int r;
+    asm("v_writelane_b32 %0, %1, %2" : "=v"(r) : "s"(v), "n"(L), "0"(old));
+    return r;
+}
+
+// f(std::integral_constant<int, j>) for j = 0 .. N - 1, unrolled at compile
+// time (lane indices and register array indices become immediates).
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
 }
 
 // Ordered 64-bit key of a double: key order == numeric order.

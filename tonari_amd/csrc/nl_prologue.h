@@ -704,17 +704,14 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
             r.reach[a] = reach[a];
         }
         r.zseg = zs;
-        // waves that share a bin's sources: one per kSourcesPerPart, at most 4
-        r.parts = (int32_t)fmin(fmax(floor(per_bin / kSourcesPerPart), 1.0), 4.0);
         if (cand <= kAutoCandidates<T>::value) break;
         }
     }
     r.algo = algo;
     r.nbins = nbins;
-    if (algo != ALGO_CELL) r.parts = 1;
-    // the counting pass tests more candidates per source than the emitting
-    // pass writes pairs, so it splits a bin over at most two waves
-    r.cparts = r.parts >= 2 ? 2 : 1;
+    // one workgroup per bin in both query passes
+    r.parts = 1;
+    r.cparts = 1;
     struct_bins[b] = nbins;
     struct_tasks[b] = nbins * r.parts;
     struct_ctasks[b] = nbins * r.cparts;

@@ -18,8 +18,7 @@ struct QueryArgs {
     const T* pos;
     const T* cells;
     const StructRec* recs;
-    const int64_t* struct_task_off;   // B + 1: first emitting task of each structure
-    const int64_t* struct_ctask_off;  // B + 1: first counting task of each structure
+    const int64_t* struct_bin_off;    // B + 1: first cell-list bin of each structure
     const int* atom_struct;
     const int4* atom_wrap;
     const Vec4<T>* atom_q;

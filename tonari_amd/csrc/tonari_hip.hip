@@ -141,11 +141,10 @@ static unsigned count_blocks(int64_t work_waves) {
     return (unsigned)(b > 0 ? b : 8);
 }
 
-// Blocks of the emitting cell-list kernel: one wave per task, 8 equal
-// XCD ranges of ceil(tasks / 8) tasks.
-static unsigned emit_blocks(int64_t tasks) {
-    const int64_t per = (tasks + 7) / 8;
-    const int64_t b = 8 * ((per + kWavesPerBlock - 1) / kWavesPerBlock);
+// Workgroups of the emitting cell-list kernel: one per bin, 8 equal XCD
+// ranges of ceil(bins / 8) bins.
+static unsigned emit_blocks(int64_t bins) {
+    const int64_t b = 8 * ((bins + 7) / 8);
     return (unsigned)(b > 0 ? b : 8);
 }
 
@@ -161,8 +160,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.pos = (const T*)req->positions;
     q.cells = (const T*)req->cell;
     q.recs = v.recs;
-    q.struct_task_off = (const int64_t*)v.struct_task_off;
-    q.struct_ctask_off = (const int64_t*)v.struct_ctask_off;
+    q.struct_bin_off = (const int64_t*)v.struct_bin_off;
     q.atom_struct = v.atom_struct;
     q.atom_wrap = v.atom_wrap;
     q.atom_q = (const Vec4<T>*)v.atom_q;
