@@ -14,7 +14,9 @@ Torch expression so autograd works as in the reference.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import threading
 from math import isfinite
 
 import torch
@@ -99,6 +101,28 @@ def _differentiable_geometry(
     return values
 
 
+_HOST = threading.local()
+
+
+def _host_result(device: torch.device):
+    """Pinned status buffer of this thread for `device`, with a ctypes view.
+
+    tnr_count copies the status words into it and synchronises the stream
+    before returning, so one buffer per thread and device is reused across
+    calls (a fresh pinned allocation per call costs more than the search of
+    a small structure).
+    """
+    cache = getattr(_HOST, "buffers", None)
+    if cache is None:
+        cache = _HOST.buffers = {}
+    entry = cache.get(device)
+    if entry is None:
+        host = torch.empty(HOST_RESULT_SLOTS, dtype=torch.int64, pin_memory=True)
+        view = (ctypes.c_int64 * HOST_RESULT_SLOTS).from_address(host.data_ptr())
+        entry = cache[device] = (host, view)
+    return entry
+
+
 def _raise(code: int, message: str) -> None:
     if code == TNR_INPUT_ERROR:
         raise ValueError(message)
@@ -152,11 +176,12 @@ def neighbor_list_hip(
         stencil_reach=0,
     )
     err = ctypes.create_string_buffer(512)
-    with torch.cuda.device(device):
+    switch = device.index is not None and device.index != torch.cuda.current_device()
+    with torch.cuda.device(device) if switch else contextlib.nullcontext():
         stream = torch.cuda.current_stream(device).cuda_stream
         ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-        host = torch.empty(HOST_RESULT_SLOTS, dtype=torch.int64, pin_memory=True)
+        host, host_view = _host_result(device)
         n_pairs = ctypes.c_int64(0)
         code = lib.tnr_count(
             ctypes.byref(req), workspace.data_ptr(), ws_bytes, host.data_ptr(), stream,
@@ -186,8 +211,8 @@ def neighbor_list_hip(
         if count > 0 and out:
             ptrs = Outputs(
                 n_pairs=count,
-                plan=int(host[3]),
-                n_tasks=int(host[7]),
+                plan=host_view[3],
+                n_tasks=host_view[7],
                 pairs=out["P"].data_ptr() if "P" in out else None,
                 shifts=out["S"].data_ptr() if "S" in out else None,
                 distances=out["d"].data_ptr() if "d" in out else None,

@@ -48,7 +48,7 @@ struct RegChunks<float> {
 };
 template <>
 struct RegChunks<double> {
-    static constexpr int value = 8;
+    static constexpr int value = 4;
 };
 
 // Candidates of a stencil staged in LDS (at most); a multiple of kBlock.
@@ -94,6 +94,13 @@ __device__ __forceinline__ void unpack_k(int v, int& kx, int& ky, int& kz) {
     ky = ((v >> 10) & 1023) - 512;
     kz = ((v >> 20) & 1023) - 512;
 }
+
+// Candidate held by lane l of chunk j of a stencil with nch chunks: the
+// chunks interleave the flattened stencil (chunk j takes candidates j,
+// j + nch, j + 2 nch, ...), so every chunk samples all pieces alike and
+// the hits of a source spread evenly over its mask words.  Both passes map
+// mask bits to candidates through this function.
+__device__ __forceinline__ int chunk_cand(int j, int l, int nch) { return l * nch + j; }
 
 // Broad-phase translation k . cell of image k; every pass that needs it
 // evaluates this same expression, so the broad-phase decisions agree.
@@ -533,7 +540,7 @@ __device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const Stencil
         cd.x[j] = cd.y[j] = cd.z[j] = far;
         cd.key[j] = MODE == 0 ? ~0u : 0u;
         if (c0 + j < cb.nch) {
-            const int v = (c0 + j) * kWave + lane;
+            const int v = chunk_cand(c0 + j, lane, cb.nch);
             if (v < cb.C) {
                 const int p = st.piece[v];
                 const Vec4<T> rec = staged ? cand[v] : a.binned[v + st.delta[p]];
@@ -555,7 +562,7 @@ __device__ __forceinline__ unsigned long long band_chunk(const QueryArgs<T>& a,
                                                          const StencilLds& st,
                                                          const CellBin<T>& cb, int jc, T sx,
                                                          T sy, T sz, int si) {
-    const int v = jc * kWave + lane_id();
+    const int v = chunk_cand(jc, lane_id(), cb.nch);
     bool ok = false;
     if (v < cb.C) {
         int tid, kk;
@@ -633,7 +640,7 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
                     for (int j = 0; j < NC && c0 + j < cb.nch; ++j) {
                         const unsigned long long m = (unsigned long long)read_lane((long long)mv, j);
                         if ((m >> lane) & 1ull) {
-                            const int v = (c0 + j) * kWave + lane;
+                            const int v = chunk_cand(c0 + j, lane, cb.nch);
                             const int p = st.piece[v];
                             shift_check(a, as_idx(a.binned[v + st.delta[p]].w), st.kid[p], si);
                         }
@@ -733,7 +740,7 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                     e_ = r < L ? (int)list[r] : 0;
                     tg_ = __shfl(tag, e_ >> 6);
                     if (r < L) {
-                        const int v = (tg_ & 63) * kWave + (e_ & 63);
+                        const int v = chunk_cand(tg_ & 63, e_ & 63, nch);
                         const int p = st.piece[v];
                         kk_ = st.kid[p];
                         rec_ = cand_record<T, STAGED>(a, st, cand, p, v);
@@ -782,20 +789,19 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
     const int j = lane - sl * nch;
     const bool want_d = a.dist != nullptr;
     const bool want_vec = a.vec != nullptr || want_d;
-    for (int sg = cb.sb; sg < cb.se; sg += kWave) {
-        const int ns = min(kWave, cb.se - sg);
+    // groups of S sources of the bin, dealt round-robin to the waves
+    const int wv = uniform(threadIdx.x / kWave);
+    const int nsrc = cb.se - cb.sb;
+    for (int s0g = wv * S; s0g < nsrc; s0g += kWavesPerBlock * S) {
+        const int ns = min(S, nsrc - s0g);
+        const int sg = cb.sb + s0g;
         const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
         const int sidx = as_idx(sq.w);
         const long long cur = lane < ns ? a.offsets[sidx] : 0;  // lane gi: first output of gi
-        auto mask_of = [&](int s0_) -> unsigned long long {
-            const int gi_ = s0_ + sl;
-            return sl < S && gi_ < ns ? a.masks[(int64_t)(sg + gi_) * kMaskWords + j] : 0ull;
-        };
-        unsigned long long m_next = mask_of(0);
-        for (int s0 = 0; s0 < ns; s0 += S) {
-            const int gi = min(s0 + sl, kWave - 1);
-            unsigned long long m = m_next;
-            if (s0 + S < ns) m_next = mask_of(s0 + S);
+        {
+            const int s0 = 0;
+            const int gi = min(sl, kWave - 1);
+            unsigned long long m = sl < ns ? a.masks[(int64_t)(sg + sl) * kMaskWords + j] : 0ull;
             int c = __popcll(m);
             int incl = wave_inclusive_scan_i32(c);
             // output range check of each source of the group (lane sl * nch)
@@ -856,7 +862,7 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                     const int e_ = list[min(r, L - 1)];
                     w_ = e_ >> 6;
                     tg_ = __shfl(tag, w_);
-                    const int v = ((tg_ & 63) << 6) | (e_ & 63);
+                    const int v = chunk_cand(tg_ & 63, e_ & 63, nch);
                     rec_ = cand[v];
                     k_ = et.pk[st.piece[v]];
                 };
@@ -960,7 +966,7 @@ __device__ __forceinline__ ItemRange xcd_block_range(int64_t W) {
 // for each source s.  The status word is read once: abort bits only come
 // from earlier kernels.
 template <typename T, int MODE>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? 4 : 1))) void
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void
 k_cell_count(
     QueryArgs<T> a) {
     __shared__ StencilLds s_st;
@@ -1026,11 +1032,12 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     const int wv = uniform(threadIdx.x / kWave);
     if (cb.C <= StageCap<T>::value && !cb.wrapped) {
         stage_candidates<T>(a, s_st, cb.C, s_cand);
-        wave_sources(cb);
-        if (!s_et.kbig)
-            emit_fast<T>(a, s_st, s_cand, s_et, cb, s_list[wv]);
-        else
+        if (!s_et.kbig) {
+            emit_fast<T>(a, s_st, s_cand, s_et, cb, s_list[wv]);  // deals its own groups
+        } else {
+            wave_sources(cb);
             emit_bin<T, true, false>(a, s_st, s_cand, cb, s_list[wv]);
+        }
     } else if (cb.C <= kMapCap) {
         wave_sources(cb);
         if (cb.wrapped)

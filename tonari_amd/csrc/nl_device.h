@@ -18,17 +18,9 @@ constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kPieceCap = 192;            // stencil pieces per source bin
 
-// Automatic stencil reach: the smallest reach whose estimated stencil holds
-// at most this many candidates (one register pass of the counting kernel
-// holds 1024 float or 512 double candidates).
-template <typename T>
-struct kAutoCandidates {
-    static constexpr double value = 768.0;
-};
-template <>
-struct kAutoCandidates<double> {
-    static constexpr double value = 512.0;
-};
+// Automatic stencil reach: weight of the per-bin work (stencil build,
+// staging, register gather) against the per-source distance tests.
+constexpr double kBinOverhead = 6.0;
 constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
 constexpr int64_t kAutoBruteCandidates = 4096;     // N_b * images at or below: brute force
 
@@ -92,9 +84,8 @@ struct alignas(16) StructRec {
     double inner2;       // broad d2 below this: inside for sure
     double outer2;       // broad d2 at or above this: outside for sure
     double cut2;         // (T)(cutoff * cutoff) as double
-    unsigned long long umin[3], umax[3];   // ordered keys of grid-coordinate bounds
-    unsigned long long cmin[3], cmax[3];   // ordered keys of Cartesian wrapped bounds
-    unsigned long long maxp;               // bits of max_c |p_c| (non-negative double)
+    unsigned long long red[14];  // max-keys of the atom reductions of shared blocks (kRed*)
+    unsigned long long maxp;     // bits of max_c |p_c| (non-negative double), set by k_plan
     unsigned long long flags;   // input-error bits found by k_setup for this structure
     int64_t img_total;   // images this structure adds to the batch total (0 if invalid)
     uint32_t maxw;       // max_a |wrap_a| (2^31 fits)
@@ -108,12 +99,21 @@ struct alignas(16) StructRec {
     int32_t diagonal;    // every off-diagonal cell entry is zero
 };
 
+// The 14 per-structure reductions over atoms, all kept as maxima of
+// "max-keys": kRedUlo + a / kRedUhi + a are the lower / upper bounds of the
+// grid coordinate on axis a, kRedClo + c / kRedChi + c those of the wrapped
+// Cartesian coordinate c, kRedP is max_c |p_c| and kRedW max_a |wrap_a|.
+// Lower bounds are stored complemented so that every reduction is a
+// maximum and 0 is the identity.  For float inputs the keys are 32-bit
+// (bounds rounded outward, Cartesian bounds exact, |p| rounded up); for
+// double inputs they are 64-bit and exact.
+enum RedSlot : int { kRedUlo = 0, kRedUhi = 3, kRedClo = 6, kRedChi = 9, kRedP = 12, kRedW = 13,
+                     kRedCount = 14 };
+
 // Per-block reduction record written by k_atoms for blocks whose atoms all
 // lie in one structure (k_plan combines them without atomics).
 struct alignas(16) BlockPartial {
-    unsigned long long umin[3], umax[3], cmin[3], cmax[3];
-    unsigned long long maxp;
-    unsigned long long maxw;
+    unsigned long long red[kRedCount];
 };
 
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte

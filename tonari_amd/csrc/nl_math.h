@@ -57,8 +57,11 @@ __device__ __forceinline__ double idx_as(int i, double) { return (double)i; }
 __device__ __forceinline__ int as_idx(float v) { return __float_as_int(v); }
 __device__ __forceinline__ int as_idx(double v) { return (int)v; }
 
+// Status word as left by the earlier kernels of the request: a plain load
+// (a kernel boundary makes their writes visible; bits raised meanwhile by
+// other workgroups of the running kernel may or may not be seen).
 __device__ __forceinline__ unsigned long long load_status(const unsigned long long* s) {
-    return __atomic_load_n(s, __ATOMIC_RELAXED);
+    return *s;
 }
 
 __device__ __forceinline__ int floor_div(int a, int b) {
@@ -169,5 +172,74 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x)
     }
     return x;
 }
+
+// Unsigned maximum over the wave, every lane receives it (DPP row shifts
+// and broadcasts; lanes whose source is outside the row read 0, the
+// identity).
+__device__ __forceinline__ unsigned wave_max_u32(unsigned x) {
+    x = max(x, (unsigned)dpp_move<0x111, 0xf>((int)x));
+    x = max(x, (unsigned)dpp_move<0x112, 0xf>((int)x));
+    x = max(x, (unsigned)dpp_move<0x114, 0xf>((int)x));
+    x = max(x, (unsigned)dpp_move<0x118, 0xf>((int)x));
+    x = max(x, (unsigned)dpp_move<0x142, 0xa>((int)x));
+    x = max(x, (unsigned)dpp_move<0x143, 0xc>((int)x));
+    return (unsigned)__builtin_amdgcn_readlane((int)x, kWave - 1);
+}
+
+// Maximum of x over the lanes [head, lane] of a contiguous segment that
+// starts at lane `head` (segmented inclusive scan with lane shuffles).
+__device__ __forceinline__ unsigned long long segment_max_u64(unsigned long long x, int head) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const unsigned long long y = __shfl_up(x, d);
+        if (lane - d >= head) x = y > x ? y : x;
+    }
+    return x;
+}
+
+// ------------------------------------------------- reduction key encodings
+// Max-keys of the atom reductions (see RedSlot): 32-bit keys for float
+// inputs, 64-bit for double.  ord32 / order_key map numeric order to
+// unsigned order.
+__device__ __forceinline__ unsigned ord32(float x) {
+    const unsigned b = __float_as_uint(x);
+    return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float ord32_value(unsigned k) {
+    const unsigned b = (k >> 31) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(b);
+}
+
+template <typename T>
+struct RedKeys;
+
+template <>
+struct RedKeys<float> {
+    // bounds rounded outward to float: the bins still cover every atom
+    __device__ static unsigned long long lower(double x) { return (unsigned long long)~ord32(Ops<float>::down(x)); }
+    __device__ static unsigned long long upper(double x) { return ord32(Ops<float>::up(x)); }
+    __device__ static unsigned long long lower_exact(float x) { return (unsigned long long)~ord32(x); }
+    __device__ static unsigned long long upper_exact(float x) { return ord32(x); }
+    // non-negative, rounded up: only enlarges the margin
+    __device__ static unsigned long long magnitude(double x) { return __float_as_uint(Ops<float>::up(x)); }
+    __device__ static double lower_value(unsigned long long k) { return (double)ord32_value(~(unsigned)k); }
+    __device__ static double upper_value(unsigned long long k) { return (double)ord32_value((unsigned)k); }
+    __device__ static double magnitude_value(unsigned long long k) { return (double)__uint_as_float((unsigned)k); }
+    __device__ static unsigned long long wave_max(unsigned long long x) { return wave_max_u32((unsigned)x); }
+};
+
+template <>
+struct RedKeys<double> {
+    __device__ static unsigned long long lower(double x) { return ~order_key(x); }
+    __device__ static unsigned long long upper(double x) { return order_key(x); }
+    __device__ static unsigned long long lower_exact(double x) { return ~order_key(x); }
+    __device__ static unsigned long long upper_exact(double x) { return order_key(x); }
+    __device__ static unsigned long long magnitude(double x) { return (unsigned long long)__double_as_longlong(x); }
+    __device__ static double lower_value(unsigned long long k) { return key_value(~k); }
+    __device__ static double upper_value(unsigned long long k) { return key_value(k); }
+    __device__ static double magnitude_value(unsigned long long k) { return __longlong_as_double((long long)k); }
+    __device__ static unsigned long long wave_max(unsigned long long x) { return wave_max_u64(x); }
+};
 
 }  // namespace tnr

@@ -5,6 +5,7 @@
 #pragma once
 
 #include "nl_math.h"
+#include "nl_scan.h"
 
 namespace tnr {
 
@@ -134,14 +135,14 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
     r.cparts = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
-        r.umin[a] = r.cmin[a] = ~0ull;
-        r.umax[a] = r.cmax[a] = 0ull;
         r.lo[a] = 0.0;
         r.inv_w[a] = 1.0;
         r.reps[a] = 0;
         r.nb[a] = 1;
         r.reach[a] = 1;
     }
+#pragma unroll
+    for (int e = 0; e < kRedCount; ++e) r.red[e] = 0;
     r.maxp = 0;
     r.maxw = 0;
     r.algo = ALGO_NONE;
@@ -367,7 +368,7 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
                                                    Vec4<T>* atom_q, unsigned long long* status,
                                                    int* bin_count, int64_t n_bin_count,
                                                    unsigned long long* tiles, int64_t n_tiles) {
-    __shared__ unsigned long long s_red[kWavesPerBlock][14];
+    __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
     __shared__ unsigned long long s_flags;
     {
         const int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -440,118 +441,68 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
     }
     if (st) atomicOr(status + SS_FLAGS, st);
 
-    unsigned long long v[14];
+    // the 14 reductions as max-keys (0 = identity for atoms that contribute nothing)
+    using K = RedKeys<T>;
+    unsigned long long v[kRedCount];
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
-        v[a] = good ? order_key(u[a]) : ~0ull;
-        v[3 + a] = good ? order_key(u[a]) : 0ull;
-        v[6 + a] = good ? order_key((double)q[a]) : ~0ull;
-        v[9 + a] = good ? order_key((double)q[a]) : 0ull;
+        v[kRedUlo + a] = good ? K::lower(u[a]) : 0ull;
+        v[kRedUhi + a] = good ? K::upper(u[a]) : 0ull;
+        v[kRedClo + a] = good ? K::lower_exact(q[a]) : 0ull;
+        v[kRedChi + a] = good ? K::upper_exact(q[a]) : 0ull;
     }
-    v[12] = good ? (unsigned long long)__double_as_longlong(pmax) : 0ull;
-    v[13] = good ? max(max((unsigned long long)llabs((long long)w[0]),
-                           (unsigned long long)llabs((long long)w[1])),
-                       (unsigned long long)llabs((long long)w[2]))
-                 : 0ull;
+    v[kRedP] = good ? K::magnitude(pmax) : 0ull;
+    v[kRedW] = good ? (unsigned long long)max(max(abs(w[0]), abs(w[1])), abs(w[2])) : 0ull;
     if (uniform) {
         const int wv = threadIdx.x / kWave;
 #pragma unroll
-        for (int e = 0; e < 14; ++e) {
-            const bool is_min = (e < 3) || (e >= 6 && e < 9);
-            v[e] = is_min ? wave_min_u64(v[e]) : wave_max_u64(v[e]);
-        }
+        for (int e = 0; e < kRedCount; ++e) v[e] = K::wave_max(v[e]);
         if (lane_id() == 0)
 #pragma unroll
-            for (int e = 0; e < 14; ++e) s_red[wv][e] = v[e];
+            for (int e = 0; e < kRedCount; ++e) s_red[wv][e] = v[e];
         __syncthreads();
-        if (threadIdx.x < 14) {
+        if (threadIdx.x < kRedCount) {
             const int e = threadIdx.x;
-            const bool is_min = (e < 3) || (e >= 6 && e < 9);
             unsigned long long x = s_red[0][e];
 #pragma unroll
-            for (int k = 1; k < kWavesPerBlock; ++k)
-                x = is_min ? min(x, s_red[k][e]) : max(x, s_red[k][e]);
-            unsigned long long* out = reinterpret_cast<unsigned long long*>(&partials[blockIdx.x]);
-            out[e] = x;
+            for (int k = 1; k < kWavesPerBlock; ++k) x = s_red[k][e] > x ? s_red[k][e] : x;
+            partials[blockIdx.x].red[e] = x;
         }
-    } else if (good) {
-        StructRec& r = recs[b];
+    } else {
+        // several structures: a segmented maximum per wave, then one atomic
+        // per (wave, structure, reduction) from the segment's last lane
+        const int lane = lane_id();
+        const int bprev = __shfl_up(b, 1);
+        const unsigned long long heads = __builtin_amdgcn_ballot_w64(lane == 0 || bprev != b);
+        const unsigned long long below = heads & (lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1));
+        const int head = kWave - 1 - __builtin_clzll(below);
+        const unsigned long long next_head = heads >> 1;  // bit l: lane l + 1 starts a segment
+        const bool tail = lane == kWave - 1 || ((next_head >> lane) & 1ull);
 #pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            atomicMin(&r.umin[a], v[a]);
-            atomicMax(&r.umax[a], v[3 + a]);
-            atomicMin(&r.cmin[a], v[6 + a]);
-            atomicMax(&r.cmax[a], v[9 + a]);
+        for (int e = 0; e < kRedCount; ++e) v[e] = segment_max_u64(v[e], head);
+        if (tail && valid) {
+            StructRec& r = recs[b];
+#pragma unroll
+            for (int e = 0; e < kRedCount; ++e)
+                if (v[e]) atomicMax(&r.red[e], v[e]);
         }
-        atomicMax(&r.maxp, v[12]);
-        atomicMax(&r.maxw, (unsigned)v[13]);
     }
 }
 
-// One wave per structure: combine the block partials and atomics, then (lane
-// 0) the broad-phase margin, the algorithm and the bin grid.  The margin
-// pad = 64 eps_T max(scale, rc) bounds the difference between the fused
-// broad-phase distance and the public predicate, with scale = 2 max|p| +
+
+// Planner of one structure (one thread): from the reduced bounds v (see
+// k_plan) the broad-phase margin, the algorithm and the bin grid.  The
+// margin pad = 64 eps_T max(scale, rc) bounds the difference between the
+// fused broad-phase distance and the public predicate, with scale = 2 max|p| +
 // sum_a (R_a + 2 max|w|) max_c |cell_ac|, the operation scale of
 // neighbors_cpu.cpp:156-219.
 template <typename T>
-__global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int64_t n_atoms,
-                                                double cutoff, int requested, int reach_target,
-                                                StructRec* recs, const BlockPartial* partials,
-                                                long long* struct_bins, long long* struct_tasks,
-                                                long long* struct_ctasks,
-                                                unsigned long long* status) {
-    const int64_t b = blockIdx.x;
-    const int lane = lane_id();
-    if (b >= nb) return;
-    StructRec& r = recs[b];
-    // fold the structure's own input errors and images into the status words
-    if (lane == 0) {
-        if (r.flags) atomicOr(status + SS_FLAGS, r.flags);
-        if (r.img_total > 0)
-            atomicAdd((unsigned long long*)(status + SS_TOTAL_IMAGES),
-                      (unsigned long long)r.img_total);
-    }
-    if ((r.flags & kAbortBits) || (load_status(status + SS_FLAGS) & kAbortBits)) {
-        if (lane == 0) {
-            struct_bins[b] = 0;
-            struct_tasks[b] = 0;
-            struct_ctasks[b] = 0;
-        }
-        return;
-    }
+__device__ void plan_structure(const T* cells, int64_t b, StructRec& r,
+                               const unsigned long long red[kRedCount], double cutoff,
+                               int requested, int reach_target, long long* struct_bins,
+                               long long* struct_tasks, long long* struct_ctasks) {
+    using K = RedKeys<T>;
     const int64_t n = r.natoms;
-    // reduce the partials of uniform blocks inside this structure
-    unsigned long long v[14];
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        v[a] = r.umin[a];
-        v[3 + a] = r.umax[a];
-        v[6 + a] = r.cmin[a];
-        v[9 + a] = r.cmax[a];
-    }
-    v[12] = r.maxp;
-    v[13] = r.maxw;
-    if (n > 0) {
-        const int64_t k0 = r.atom0 / kBlock, k1 = (r.atom0 + n - 1) / kBlock;
-        for (int64_t kb = k0 + lane; kb <= k1; kb += kWave) {
-            const int64_t first = kb * kBlock;
-            const int64_t last = (first + kBlock < n_atoms ? first + kBlock : n_atoms) - 1;
-            if (first < r.atom0 || last >= r.atom0 + n) continue;  // shared block: atomics
-            const unsigned long long* p = reinterpret_cast<const unsigned long long*>(&partials[kb]);
-#pragma unroll
-            for (int e = 0; e < 14; ++e) {
-                const bool is_min = (e < 3) || (e >= 6 && e < 9);
-                v[e] = is_min ? min(v[e], p[e]) : max(v[e], p[e]);
-            }
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 14; ++e) {
-        const bool is_min = (e < 3) || (e >= 6 && e < 9);
-        v[e] = is_min ? wave_min_u64(v[e]) : wave_max_u64(v[e]);
-    }
-    if (lane != 0) return;
     if (n == 0) {
         r.algo = ALGO_NONE;
         r.nbins = 0;
@@ -565,8 +516,9 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
     double cell[9];
 #pragma unroll
     for (int e = 0; e < 9; ++e) cell[e] = (double)cells[9 * b + e];
-    const double maxp = __longlong_as_double((long long)v[12]);
-    const double maxw = (double)v[13];
+    const double maxp = K::magnitude_value(red[kRedP]);
+    const unsigned maxw_u = (unsigned)red[kRedW];
+    const double maxw = (double)maxw_u;
     const int active = r.active;
     const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
     double scale = 0;
@@ -580,9 +532,9 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
     const double rc = cutoff;
     const double pad = 64.0 * Ops<T>::eps * fmax(scale, rc);
     r.pad = pad;
-    r.maxp = v[12];
-    r.maxw = (uint32_t)v[13];
-    r.any_wrap = v[13] != 0;
+    r.maxp = (unsigned long long)__double_as_longlong(maxp);
+    r.maxw = maxw_u;
+    r.any_wrap = maxw_u != 0;
     const double inner = rc - pad;
     r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
     r.outer2 = (double)Ops<T>::up((rc + pad) * (rc + pad));
@@ -601,7 +553,8 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
         bool ok = safe;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            const double span = key_value(v[9 + c]) - key_value(v[6 + c]) + 2 * size;
+            const double span = K::upper_value(red[kRedChi + c]) -
+                                K::lower_value(red[kRedClo + c]) + 2 * size;
             const double dim = span / size;
             if (!isfinite(dim) || dim > 67108864.0) ok = false;
             count *= fmax(1.0, ceil(dim));
@@ -614,10 +567,11 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
     int64_t nbins = 0;
     if (want_cell) {
         // Bin grid for a stencil reach of kt bins per padded cutoff.  With
-        // reach_target 0 the reach is chosen per structure: the smallest
-        // kt whose estimated stencil (bins in reach times atoms per bin)
-        // holds at most kAutoCandidates<T> candidates, else the one with
-        // the fewest candidates.
+        // reach_target 0 the reach is chosen per structure by an estimated
+        // cost per source: the stencil candidates (distance tests) times
+        // 1 + kBinOverhead / (sources per bin), since every bin builds and
+        // stages its stencil once for all of its sources; stencils beyond
+        // the mask capacity take the slow path and count four times.
         const double rcu0 = rc + 2 * pad;
         double best_c = INFINITY;
         int k_lo = reach_target > 0 ? reach_target : 1;
@@ -638,8 +592,8 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
                 nbf[a] = fmin(fmax(ceil(kt / rcu[a]) - 1.0, 1.0), 1048576.0);
                 wdt[a] = 1.0 / nbf[a];
             } else {
-                lo[a] = key_value(v[a]);
-                const double hi = key_value(v[3 + a]);
+                lo[a] = K::lower_value(red[kRedUlo + a]);
+                const double hi = K::upper_value(red[kRedUhi + a]);
                 ext[a] = fmax(hi - lo[a], 0.0);
                 if (!isfinite(ext[a]) || !isfinite(lo[a])) ok = false;
                 wdt[a] = rcu[a] / kt * (1.0 + 1e-9);
@@ -691,9 +645,11 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
             span_bins *= (active >> a & 1) ? w : fmin(w, nbf[a]);
         }
         const double cand = span_bins * per_bin;
-        const bool take = best_c == INFINITY || (best_c > kAutoCandidates<T>::value && cand < best_c);
+        const double cost = cand * (1.0 + kBinOverhead / fmax(per_bin, 1e-9)) *
+                            (cand > (double)(kMaskWords * kWave) ? 4.0 : 1.0);
+        const bool take = best_c == INFINITY || cost < best_c;
         if (!take) continue;
-        best_c = cand;
+        best_c = cost;
         algo = ALGO_CELL;
         nbins = (int64_t)bins_f;
 #pragma unroll
@@ -704,7 +660,6 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
             r.reach[a] = reach[a];
         }
         r.zseg = zs;
-        if (cand <= kAutoCandidates<T>::value) break;
         }
     }
     r.algo = algo;
@@ -715,8 +670,91 @@ __global__ __launch_bounds__(kWave) void k_plan(const T* cells, int64_t nb, int6
     struct_bins[b] = nbins;
     struct_tasks[b] = nbins * r.parts;
     struct_ctasks[b] = nbins * r.cparts;
-    atomicOr(status + SS_PLAN, algo == ALGO_CELL ? 2ull : 1ull);
-    if (st) atomicOr(status + SS_FLAGS, st);
+    r.flags |= st;
+}
+
+// One workgroup per structure: combines the block partials of k_atoms (all
+// loads in flight at once) with the atomics of shared blocks, and plans the
+// structure (plan_structure).  Results stay in the structure's record and
+// the per-structure arrays; k_struct_scan combines them for the batch (for a
+// single structure, with `fused_scan`, this workgroup does it itself).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int64_t n_atoms,
+                                                  double cutoff, int requested, int reach_target,
+                                                  StructRec* recs, const BlockPartial* partials,
+                                                  long long* struct_bins, long long* struct_tasks,
+                                                  long long* struct_ctasks, long long* bin_off,
+                                                  long long* task_off, long long* ctask_off,
+                                                  int64_t cap_bins, unsigned long long* status,
+                                                  int fused_scan) {
+    using K = RedKeys<T>;
+    __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
+    const int64_t b = blockIdx.x;
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
+    if (b < nb) {
+        StructRec& r = recs[b];
+        const unsigned long long flags = r.flags;
+        if ((flags & kAbortBits) || (load_status(status + SS_FLAGS) & kAbortBits)) {
+            if (tid == 0) {
+                struct_bins[b] = 0;
+                struct_tasks[b] = 0;
+                struct_ctasks[b] = 0;
+            }
+        } else {
+            const int64_t n = r.natoms;
+            unsigned long long v[kRedCount];
+#pragma unroll
+            for (int e = 0; e < kRedCount; ++e) v[e] = r.red[e];
+            if (n > 0) {
+                // partials of the k_atoms blocks that lie inside this structure
+                const int64_t k0 = r.atom0 / kBlock, k1 = (r.atom0 + n - 1) / kBlock;
+#pragma unroll 4
+                for (int64_t kb = k0 + tid; kb <= k1; kb += kBlock) {
+                    const int64_t first = kb * kBlock;
+                    const int64_t last = (first + kBlock < n_atoms ? first + kBlock : n_atoms) - 1;
+                    const bool inside = first >= r.atom0 && last < r.atom0 + n;
+#pragma unroll
+                    for (int e = 0; e < kRedCount; ++e) {
+                        const unsigned long long x = partials[kb].red[e];
+                        if (inside) v[e] = x > v[e] ? x : v[e];
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < kRedCount; ++e) v[e] = K::wave_max(v[e]);
+            if (lane == 0)
+#pragma unroll
+                for (int e = 0; e < kRedCount; ++e) s_red[wv][e] = v[e];
+            __syncthreads();
+            if (tid == 0) {
+#pragma unroll
+                for (int e = 0; e < kRedCount; ++e)
+#pragma unroll
+                    for (int w = 1; w < kWavesPerBlock; ++w)
+                        v[e] = s_red[w][e] > v[e] ? s_red[w][e] : v[e];
+                plan_structure<T>(cells, b, r, v, cutoff, requested, reach_target, struct_bins,
+                                  struct_tasks, struct_ctasks);
+            }
+        }
+    }
+    if (fused_scan) {
+        __syncthreads();
+        struct_scan_block(struct_bins, struct_tasks, struct_ctasks, nb, bin_off, task_off,
+                          ctask_off, recs, status, cap_bins);
+    }
+}
+
+// The batch-wide step of the planner (one workgroup, after k_plan).
+__global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
+                                                         const long long* struct_tasks,
+                                                         const long long* struct_ctasks,
+                                                         int64_t nb, long long* bin_off,
+                                                         long long* task_off,
+                                                         long long* ctask_off, StructRec* recs,
+                                                         unsigned long long* status,
+                                                         int64_t cap_bins) {
+    struct_scan_block(struct_bins, struct_tasks, struct_ctasks, nb, bin_off, task_off, ctask_off,
+                      recs, status, cap_bins);
 }
 
 template <typename T>
@@ -739,17 +777,22 @@ __global__ __launch_bounds__(kBlock) void k_bin(int64_t n_atoms, const StructRec
                                                  const int* atom_struct, const Vec4<T>* atom_q,
                                                  int* atom_bin, int* atom_rank, int* bin_count,
                                                  const unsigned long long* status) {
-    if (load_status(status + SS_FLAGS) & kAbortBits) return;
+    // the status, the structure index and the position in one round trip;
+    // the record (indexed by the structure) only once the status is clean
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n_atoms) return;
-    const StructRec& r = recs[atom_struct[i]];
-    if (r.algo != ALGO_CELL) {
+    const int64_t ic = i < n_atoms ? i : n_atoms - 1;
+    const unsigned long long st = load_status(status + SS_FLAGS);
+    const int b = atom_struct[ic];
+    const Vec4<T> v = atom_q[ic];
+    if ((st & kAbortBits) || i >= n_atoms) return;
+    const StructRec& r = recs[b];
+    const int algo = r.algo;
+    const T q[3] = {v.x, v.y, v.z};
+    const int64_t g = r.bin0 + local_bin(r, q);
+    if (algo != ALGO_CELL) {
         atom_bin[i] = -1;
         return;
     }
-    const Vec4<T> v = atom_q[i];
-    const T q[3] = {v.x, v.y, v.z};
-    const int64_t g = r.bin0 + local_bin(r, q);
     atom_bin[i] = (int)g;
     atom_rank[i] = atomicAdd(bin_count + g, 1);
 }

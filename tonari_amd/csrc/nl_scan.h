@@ -1,6 +1,6 @@
 // Device-wide exclusive scans: a single-pass scan with decoupled look-back
 // (k_scan_lookback), the one-block scan of the bins per structure
-// (k_struct_scan), the three-kernel scan (reduce, scan of block totals,
+// (struct_scan_block, run by the last workgroup of k_plan), the three-kernel scan (reduce, scan of block totals,
 // apply) and small fill kernels.
 #pragma once
 
@@ -122,11 +122,12 @@ __device__ __forceinline__ unsigned long long tile_read(const unsigned long long
 // `in` into out[0..n], out[n] = total, in one launch.  Blocks take tiles of
 // kScanTile items in the order they start (an atomic ticket), so every
 // earlier tile belongs to a block that is already running; a block publishes
-// its tile aggregate, then walks back over the earlier tiles until it meets
-// an inclusive prefix (decoupled look-back).  The wait on an earlier tile is
-// bounded (kLookbackSpins polls); on expiry the block raises ST_SCAN_STALL
-// and finishes, so every wave exits.  `tiles` must hold zeros and `ticket`
-// zero.  When total_slot is given the total is also stored there.
+// its tile aggregate, then its first wave looks back over the 64 preceding
+// tiles at a time (one read per lane) and adds the aggregates down to the
+// nearest inclusive prefix (decoupled look-back).  The wait on an earlier
+// tile is bounded (kLookbackSpins polls); on expiry the block raises
+// ST_SCAN_STALL and finishes, so every wave exits.  `tiles` must hold zeros
+// and `ticket` zero.  When total_slot is given the total is also stored there.
 template <typename In, typename Out>
 __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t n,
                                                            const unsigned long long* n_dev,
@@ -152,26 +153,38 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     }
     long long total;
     const long long ex = block_exclusive_scan(s, &total);
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < kWave) {
+        const int lane = lane_id();
         long long excl = 0;
         if (tile > 0) {
-            tile_publish(tiles + tile, kTileAggregate | (unsigned long long)total);
-            for (int64_t t = tile - 1; t >= 0; --t) {
-                unsigned long long w = tile_read(tiles + t);
-                for (int spin = 0; (w >> 62) == 0 && spin < kLookbackSpins; ++spin) {
+            if (lane == 0) tile_publish(tiles + tile, kTileAggregate | (unsigned long long)total);
+            for (int64_t hi = tile - 1;; hi -= kWave) {
+                const int64_t t = hi - lane;
+                // tiles before the first count as an inclusive prefix of 0
+                unsigned long long w = t >= 0 ? tile_read(tiles + t) : kTilePrefix;
+                for (int spin = 0; spin < kLookbackSpins; ++spin) {
+                    if (!__builtin_amdgcn_ballot_w64((w >> 62) == 0)) break;
                     __builtin_amdgcn_s_sleep(1);
-                    w = tile_read(tiles + t);
+                    if ((w >> 62) == 0) w = tile_read(tiles + t);
                 }
-                if ((w >> 62) == 0) {
-                    atomicOr(status + SS_FLAGS, ST_SCAN_STALL);
+                if (__builtin_amdgcn_ballot_w64((w >> 62) == 0)) {
+                    if (lane == 0) atomicOr(status + SS_FLAGS, ST_SCAN_STALL);
                     break;
                 }
-                excl += (long long)(w & kTileValue);
-                if ((w & ~kTileValue) == kTilePrefix) break;
+                const unsigned long long pm =
+                    __builtin_amdgcn_ballot_w64((w & ~kTileValue) == kTilePrefix);
+                const int stop = pm ? __builtin_ctzll(pm) : kWave - 1;
+                long long part = lane <= stop ? (long long)(w & kTileValue) : 0;
+#pragma unroll
+                for (int d = kWave / 2; d > 0; d >>= 1) part += __shfl_xor(part, d);
+                excl += part;
+                if (pm) break;
             }
         }
-        tile_publish(tiles + tile, kTilePrefix | (unsigned long long)(excl + total));
-        s_excl = excl;
+        if (lane == 0) {
+            tile_publish(tiles + tile, kTilePrefix | (unsigned long long)(excl + total));
+            s_excl = excl;
+        }
     }
     __syncthreads();
     long long run = s_excl + ex;
@@ -187,61 +200,78 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     }
 }
 
-// One block: exclusive scans of the bins, the emitting tasks and the
+// One workgroup: exclusive scans of the bins, the emitting tasks and the
 // counting tasks per structure into bin_off, task_off and ctask_off
 // ([0..nb]; each structure's first bin and tasks go to its record), their
 // totals, and the batch checks that need every structure's plan: total
 // periodic images and bin capacity.
-__global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
-                                                         const long long* struct_tasks,
-                                                         const long long* struct_ctasks,
-                                                         int64_t nb, long long* bin_off,
-                                                         long long* task_off,
-                                                         long long* ctask_off, StructRec* recs,
-                                                         unsigned long long* status,
-                                                         int64_t cap_bins) {
-    __shared__ long long carry[3];
-    if (threadIdx.x < 3) carry[threadIdx.x] = 0;
+__device__ void struct_scan_block(const long long* struct_bins, const long long* struct_tasks,
+                                  const long long* struct_ctasks, int64_t nb, long long* bin_off,
+                                  long long* task_off, long long* ctask_off, StructRec* recs,
+                                  unsigned long long* status, int64_t cap_bins) {
+    // every bin is one task of both query passes: one scan fills the three offsets
+    (void)struct_tasks;
+    (void)struct_ctasks;
+    __shared__ long long s_carry;
+    __shared__ unsigned long long s_flags, s_plan, s_images;
+    if (threadIdx.x == 0) {
+        s_carry = 0;
+        s_flags = 0;
+        s_plan = 0;
+        s_images = 0;
+    }
     __syncthreads();
-    const long long* in[3] = {struct_bins, struct_tasks, struct_ctasks};
-    long long* out[3] = {bin_off, task_off, ctask_off};
+    unsigned long long flags = 0, plan = 0, images = 0;
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
+        long long v[kScanItems];
+        long long sum = 0;
 #pragma unroll
-        for (int q = 0; q < 3; ++q) {
-            long long v[kScanItems];
-            long long sum = 0;
-#pragma unroll
-            for (int k = 0; k < kScanItems; ++k) {
-                v[k] = i0 + k < nb ? in[q][i0 + k] : 0;
-                sum += v[k];
+        for (int k = 0; k < kScanItems; ++k) {
+            const int64_t i = i0 + k;
+            v[k] = i < nb ? struct_bins[i] : 0;
+            sum += v[k];
+            if (i < nb) {
+                const StructRec& r = recs[i];
+                flags |= r.flags;
+                plan |= r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
+                images += (unsigned long long)r.img_total;
             }
-            long long tot;
-            long long run = block_exclusive_scan(sum, &tot) + carry[q];
-#pragma unroll
-            for (int k = 0; k < kScanItems; ++k) {
-                if (i0 + k < nb) {
-                    out[q][i0 + k] = run;
-                    if (q == 0) recs[i0 + k].bin0 = run;
-                    if (q == 1) recs[i0 + k].task0 = run;
-                    if (q == 2) recs[i0 + k].ctask0 = run;
-                }
-                run += v[k];
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) carry[q] += tot;
-            __syncthreads();
         }
-    }
-    if (threadIdx.x == 0) {
+        long long tot;
+        long long run = block_exclusive_scan(sum, &tot) + s_carry;
 #pragma unroll
-        for (int q = 0; q < 3; ++q) out[q][nb] = carry[q];
-        status[SS_TOTAL_BINS] = (unsigned long long)carry[0];
-        status[SS_TOTAL_TASKS] = (unsigned long long)carry[1];
-        status[SS_TOTAL_CTASKS] = (unsigned long long)carry[2];
-        unsigned long long st = 0;
-        if (carry[0] > cap_bins) st |= ST_CAPACITY;
-        if (status[SS_TOTAL_IMAGES] > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+        for (int k = 0; k < kScanItems; ++k) {
+            const int64_t i = i0 + k;
+            if (i < nb) {
+                bin_off[i] = run;
+                task_off[i] = run;
+                ctask_off[i] = run;
+                recs[i].bin0 = run;
+                recs[i].task0 = run;
+                recs[i].ctask0 = run;
+            }
+            run += v[k];
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) s_carry += tot;
+        __syncthreads();
+    }
+    if (flags) atomicOr(&s_flags, flags);
+    if (plan) atomicOr(&s_plan, plan);
+    if (images) atomicAdd(&s_images, images);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const long long total = s_carry;
+        bin_off[nb] = task_off[nb] = ctask_off[nb] = total;
+        status[SS_TOTAL_BINS] = (unsigned long long)total;
+        status[SS_TOTAL_TASKS] = (unsigned long long)total;
+        status[SS_TOTAL_CTASKS] = (unsigned long long)total;
+        status[SS_PLAN] = s_plan;
+        status[SS_TOTAL_IMAGES] = s_images;
+        unsigned long long st = s_flags;
+        if (total > cap_bins) st |= ST_CAPACITY;
+        if (s_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
         if (st) atomicOr(status + SS_FLAGS, st);
     }
 }

@@ -7,9 +7,10 @@
 //   tnr_count: k_setup (zeroes the status words; per structure: batch_ptr
 //              checks, active pseudo-inverse, image repeats, grid frame) ->
 //              k_atoms (per atom: wraps, wrapped position, block reductions;
-//              zeroes the bin counters and scan tiles) -> k_plan (one wave per
-//              structure: margins, algorithm, bin grid) -> k_struct_scan (bins
-//              per structure) -> k_bin -> k_scan_lookback(bin counts) -> k_scatter ->
+//              zeroes the bin counters and scan tiles) -> k_plan (one
+//              workgroup per structure: margins, algorithm, bin grid) ->
+//              k_struct_scan (bins per structure, batch status; folded into
+//              k_plan for a single structure) -> k_bin -> k_scan_lookback(bin counts) -> k_scatter ->
 //              k_cell_count (persistent: cell-list bins, then brute-force
 //              sources) -> k_scan_lookback(pairs per source; E) -> one
 //              8-word device-to-host copy (status, E, plan, bins).
@@ -226,12 +227,16 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
             v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
     }
     const int reach = req->stencil_reach;  // 0: chosen per structure
-    k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kWave, 0, stream>>>(
+    // a single structure is planned and scanned by one workgroup
+    const int fused_scan = nb <= 1 ? 1 : 0;
+    k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
         (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
-        v.block_partials, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.status);
-    k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks, v.struct_ctasks, nb,
-                                            v.struct_bin_off, v.struct_task_off,
-                                            v.struct_ctask_off, v.recs, v.status, L.cap_bins);
+        v.block_partials, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.struct_bin_off,
+        v.struct_task_off, v.struct_ctask_off, L.cap_bins, v.status, fused_scan);
+    if (!fused_scan)
+        k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks, v.struct_ctasks,
+                                                nb, v.struct_bin_off, v.struct_task_off,
+                                                v.struct_ctask_off, v.recs, v.status, L.cap_bins);
     if (n > 0 && req->algorithm != TNR_BRUTE_FORCE) {
         k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
                                                        (const Vec4<T>*)v.atom_q, v.atom_bin,
