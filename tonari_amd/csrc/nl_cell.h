@@ -138,6 +138,7 @@ struct StructCache {
 
 __device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb, int64_t g,
                                                  StructCache& sc) {
+    if (nb == 1) return 0;  // every bin belongs to the only structure
     if (g >= sc.lo && g < sc.hi) return sc.b;
     int64_t lo = 0, hi = nb;
     while (hi - lo > 1) {
@@ -163,16 +164,16 @@ template <typename T>
 __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, StructCache& sc,
                                           CellBin<T>& cb, StencilLds& st,
                                           T (*tr)[kPieceCap] = nullptr,
-                                          EmitTables<T>* et = nullptr) {
+                                          EmitTables<T>* et = nullptr,
+                                          Vec4<T>* src_pre = nullptr) {
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wv = tid / kWave;
     cb.b = structure_of_item(a.struct_bin_off, a.nb, g, sc);
     const StructRec& r = a.recs[cb.b];
     const unsigned lbin = (unsigned)(g - r.bin0);  // bins of a structure fit in 32 bits
-    cb.sb = uniform(a.bin_start[g]);
-    cb.se = uniform(a.bin_start[g + 1]);
-    if (cb.sb >= cb.se) return false;
+    // the bin's sources and the piece bounds below load in one round trip
+    const int sb_raw = a.bin_start[g], se_raw = a.bin_start[g + 1];
     const T* cell = a.cells + 9 * cb.b;
 #pragma unroll
     for (int e = 0; e < 9; ++e) cb.c[e] = cell[e];
@@ -198,20 +199,6 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     int kz0 = 0;  // image of the lowest stencil z-bin (zlo < nz)
     if (perz)
         for (int zz = zlo; zz < 0; zz += nz) --kz0;
-    // clear the piece marks (the previous bin's users passed a barrier)
-    reinterpret_cast<unsigned long long*>(st.piece)[tid] = 0ull;
-    static_assert(kMapCap == 8 * kBlock, "one 8-byte word of piece marks per thread");
-    if (et) {
-        if (tid == 0) et->kbig = 0;
-        constexpr int NP = 3 * (2 * kProdK + 1) * 3;
-        static_assert(NP <= kBlock, "one product per thread");
-        if (tid < NP) {
-            const int ax = tid / (3 * (2 * kProdK + 1));
-            const int rest_ = tid - ax * 3 * (2 * kProdK + 1);
-            const int kv = rest_ / 3 - kProdK, c = rest_ % 3;
-            et->prod[ax][kv + kProdK][c] = Ops<T>::mul((T)kv, cell[3 * ax + c]);
-        }
-    }
 
     const int p = tid;
     int len = 0, start = 0, kx = 0, ky = 0, kz = 0;
@@ -258,8 +245,35 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
             len = bstart[rowbase + z1 + 1] - start;
         }
     }
+    cb.sb = uniform(sb_raw);
+    cb.se = uniform(se_raw);
+    if (cb.sb >= cb.se) return false;
+    // clear the piece marks (the previous bin's users passed a barrier)
+    reinterpret_cast<unsigned long long*>(st.piece)[tid] = 0ull;
+    static_assert(kMapCap == 8 * kBlock, "one 8-byte word of piece marks per thread");
+    if (et) {
+        if (tid == 0) et->kbig = 0;
+        constexpr int NP = 3 * (2 * kProdK + 1) * 3;
+        static_assert(NP <= kBlock, "one product per thread");
+        if (tid < NP) {
+            const int ax = tid / (3 * (2 * kProdK + 1));
+            const int rest_ = tid - ax * 3 * (2 * kProdK + 1);
+            const int kv = rest_ / 3 - kProdK, c = rest_ % 3;
+            const int e = 3 * ax + c;
+            T cv = cb.c[0];
+#pragma unroll
+            for (int q = 1; q < 9; ++q) cv = e == q ? cb.c[q] : cv;
+            et->prod[ax][kv + kProdK][c] = Ops<T>::mul((T)kv, cv);
+        }
+    }
     // workgroup exclusive scan of the piece lengths
     const int inc = wave_inclusive_scan_i32(len);
+    if (src_pre) {
+        // lane l: record of the bin's source l (l < 64), in flight during the
+        // rest of the stencil build (issued after the piece bounds were used)
+        const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
+        *src_pre = lane < cb.se - cb.sb ? a.binned[cb.sb + lane] : zero4;
+    }
     if (lane == kWave - 1) st.wtot[wv] = inc;
     __syncthreads();  // also orders the mark clearing before the marks
     int before = 0, total = 0;
@@ -779,7 +793,9 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
 template <typename T>
 __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLds& st,
                                           const Vec4<T>* cand, const EmitTables<T>& et,
-                                          const CellBin<T>& cb, unsigned short* list) {
+                                          const CellBin<T>& cb, unsigned short* list,
+                                          const Vec4<T>& src_all, long long cur_all,
+                                          unsigned long long m_pre0, unsigned long long m_pre1) {
     using O = Ops<T>;
     const int lane = lane_id();
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
@@ -791,17 +807,27 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
     const bool want_vec = a.vec != nullptr || want_d;
     // groups of S sources of the bin, dealt round-robin to the waves
     const int wv = uniform(threadIdx.x / kWave);
-    const int nsrc = cb.se - cb.sb;
-    for (int s0g = wv * S; s0g < nsrc; s0g += kWavesPerBlock * S) {
+    const int nsrc = cb.se - cb.sb;  // at most kWave: sources and offsets come preloaded
+    int it = 0;
+    for (int s0g = wv * S; s0g < nsrc; s0g += kWavesPerBlock * S, ++it) {
         const int ns = min(S, nsrc - s0g);
         const int sg = cb.sb + s0g;
-        const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
+        // lane gi: the group's source gi and its first output
+        const int from = min(s0g + lane, kWave - 1);
+        Vec4<T> sq;
+        sq.x = __shfl(src_all.x, from);
+        sq.y = __shfl(src_all.y, from);
+        sq.z = __shfl(src_all.z, from);
+        sq.w = __shfl(src_all.w, from);
         const int sidx = as_idx(sq.w);
-        const long long cur = lane < ns ? a.offsets[sidx] : 0;  // lane gi: first output of gi
+        const long long cur = __shfl(cur_all, from);
         {
             const int s0 = 0;
             const int gi = min(sl, kWave - 1);
-            unsigned long long m = sl < ns ? a.masks[(int64_t)(sg + sl) * kMaskWords + j] : 0ull;
+            unsigned long long m =
+                it == 0 ? m_pre0
+                        : it == 1 ? m_pre1
+                                  : (sl < ns ? a.masks[(int64_t)(sg + sl) * kMaskWords + j] : 0ull);
             int c = __popcll(m);
             int incl = wave_inclusive_scan_i32(c);
             // output range check of each source of the group (lane sl * nch)
@@ -977,20 +1003,31 @@ k_cell_count(
     const unsigned long long plan = load_status(a.status + SS_PLAN);
 
     if (plan & 2) {
-        const ItemRange br = xcd_block_range(a.struct_bin_off[a.nb]);
+        // Static interleaved split: bins come in chunks of 8 consecutive
+        // bins, chunk c belongs to XCD c % 8 (workgroups with blockIdx % 8 ==
+        // x run on XCD x), and the workgroups of an XCD take its bins round
+        // robin.  Every XCD and workgroup thus sees a mix of the batch's
+        // structures (balanced load) while neighbouring bins share an L2.
+        const int64_t W = a.struct_bin_off[a.nb];
+        const int64_t nxb = (int64_t)(gridDim.x / 8);  // workgroups per XCD (grid is a multiple of 8)
+        const int64_t x = (int64_t)(blockIdx.x & 7u);
         StructCache sc{0, 0, 0};
-        for (int64_t g = br.first; g < br.end; g += br.step) {
-            CellBin<T> cb;
-            if (block_bin<T>(a, g, sc, cb, s_st, s_tr)) {
-                const bool staged = cb.C <= StageCap<T>::value;
-                if (staged) stage_candidates<T>(a, s_st, cb.C, s_cand);
-                wave_sources(cb);
-                if (cb.C <= kMapCap)
-                    count_bin_any<T, MODE>(a, s_st, s_cand, staged, s_tr, cb);
-                else
-                    cell_slow<T, MODE, false>(a, s_st, cb);
+        for (int64_t j = (int64_t)(blockIdx.x >> 3);; j += nxb) {
+            const int64_t g = ((j >> 3) * 8 + x) * 8 + (j & 7);
+            if ((j >> 3) * 64 >= W) break;  // uniform: this XCD has no bins from here on
+            if (g < W) {
+                CellBin<T> cb;
+                if (block_bin<T>(a, g, sc, cb, s_st, s_tr)) {
+                    const bool staged = cb.C <= StageCap<T>::value;
+                    if (staged) stage_candidates<T>(a, s_st, cb.C, s_cand);
+                    wave_sources(cb);
+                    if (cb.C <= kMapCap)
+                        count_bin_any<T, MODE>(a, s_st, s_cand, staged, s_tr, cb);
+                    else
+                        cell_slow<T, MODE, false>(a, s_st, cb);
+                }
+                __syncthreads();  // the bin's LDS is free
             }
-            __syncthreads();  // the bin's LDS is free
         }
     }
     if (plan & 1) {
@@ -1023,17 +1060,35 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
-    const ItemRange br = xcd_block_range(a.struct_bin_off[a.nb]);
+    const ItemRange br = xcd_block_range(a.n_bins);
     const int64_t g = br.first;
     if (g >= br.end) return;
     StructCache sc{0, 0, 0};
     CellBin<T> cb;
-    if (!block_bin<T>(a, g, sc, cb, s_st, nullptr, &s_et)) return;
+    Vec4<T> src_all;
+    if (!block_bin<T>(a, g, sc, cb, s_st, nullptr, &s_et, &src_all)) return;
     const int wv = uniform(threadIdx.x / kWave);
+    const int lane = lane_id();
     if (cb.C <= StageCap<T>::value && !cb.wrapped) {
+        const int nsrc = cb.se - cb.sb;
+        const bool fast = !s_et.kbig && nsrc <= kWave;
+        long long cur_all = 0;
+        unsigned long long m0 = 0, m1 = 0;
+        if (fast) {
+            // offsets and the masks of the wave's first two groups load with the staging
+            cur_all = lane < nsrc ? a.offsets[as_idx(src_all.w)] : 0;
+            const int S = kWave / cb.nch;
+            const int sl = (int)(((float)lane + 0.5f) / (float)cb.nch);
+            const int j = lane - sl * cb.nch;
+            const int s0 = wv * S + sl, s1 = (wv + kWavesPerBlock) * S + sl;
+            if (sl < S && s0 < min(nsrc, wv * S + S))
+                m0 = a.masks[(int64_t)(cb.sb + s0) * kMaskWords + j];
+            if (sl < S && s1 < min(nsrc, (wv + kWavesPerBlock) * S + S))
+                m1 = a.masks[(int64_t)(cb.sb + s1) * kMaskWords + j];
+        }
         stage_candidates<T>(a, s_st, cb.C, s_cand);
-        if (!s_et.kbig) {
-            emit_fast<T>(a, s_st, s_cand, s_et, cb, s_list[wv]);  // deals its own groups
+        if (fast) {
+            emit_fast<T>(a, s_st, s_cand, s_et, cb, s_list[wv], src_all, cur_all, m0, m1);
         } else {
             wave_sources(cb);
             emit_bin<T, true, false>(a, s_st, s_cand, cb, s_list[wv]);

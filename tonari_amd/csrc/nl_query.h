@@ -31,6 +31,7 @@ struct QueryArgs {
     int64_t n_atoms;
     int64_t nb;
     int64_t limit;  // E: emit never writes at or beyond it
+    int64_t n_bins; // emit: cell-list bins of the batch (from the count's status words)
     // outputs (emit)
     int64_t* pairs;
     int32_t* shifts;

@@ -271,6 +271,7 @@ static hipError_t run_emit(const tnr_request* req, void* ws, const Layout& L,
     q.src = out->sources;
     q.dst = out->targets;
     q.limit = out->n_pairs;
+    q.n_bins = out->n_tasks;
     dispatch_queries<T, true>(req, L, q, out->plan, out->n_tasks, stream);
     return hipGetLastError();
 }
