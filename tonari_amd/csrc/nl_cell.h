@@ -74,16 +74,18 @@ struct StencilLds {
     int wmax[kWavesPerBlock];           // block running maximum: wave maxima
 };
 
-// Tables of the emitting fast path: the image shift of every piece, and the
-// products fl(k * cell[a][c]) of the public formula for |k| <= kProdK per
-// axis a and component c (the output shift S equals the image shift k when
-// no representative is wrapped).
-constexpr int kProdK = 8;
+// Candidates of a stencil staged in LDS by the emitting pass (at most); a
+// multiple of kBlock.  Smaller than the counting pass's so that more
+// emitting workgroups fit on a CU.
 template <typename T>
-struct EmitTables {
-    int4 pk[kPieceCap];                  // (kx, ky, kz, 0)
-    T prod[3][2 * kProdK + 1][4];        // [axis][k + kProdK][component]
-    int kbig;                            // some piece has |k_a| > kProdK
+struct EmitStageCap;
+template <>
+struct EmitStageCap<float> {
+    static constexpr int value = 768;
+};
+template <>
+struct EmitStageCap<double> {
+    static constexpr int value = 768;
 };
 
 __device__ __forceinline__ int pack_k(int kx, int ky, int kz) {
@@ -151,11 +153,100 @@ __device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb,
     return sc.b;
 }
 
+// Geometry of the stencil of one bin, decoded from its structure record.
+struct BinGeom {
+    int ix, iy, iz;         // the bin
+    int nx, ny, nz;         // bins per axis (each at least 1)
+    int Kx, Kz, RY, zs;     // reach in x and z, rows per x step, z segments per row
+    int R0, R1, R2;         // image repeats
+    bool perx, pery, perz;
+    int kz0;                // image of the lowest stencil z-bin
+    int npieces;            // (2 Kx + 1) * RY * zs, at most kPieceCap
+};
+
+__device__ __forceinline__ BinGeom bin_geom(const StructRec& r, unsigned lbin) {
+    BinGeom G;
+    G.nx = r.nb[0];
+    G.ny = r.nb[1];
+    G.nz = r.nb[2];
+    G.Kx = r.reach[0];
+    const int Ky = r.reach[1];
+    G.Kz = r.reach[2];
+    G.R0 = r.reps[0];
+    G.R1 = r.reps[1];
+    G.R2 = r.reps[2];
+    G.perx = r.active & 1;
+    G.pery = r.active >> 1 & 1;
+    G.perz = r.active >> 2 & 1;
+    G.zs = r.zseg;
+    G.iz = (int)(lbin % (unsigned)G.nz);
+    const unsigned rest = lbin / (unsigned)G.nz;
+    G.iy = (int)(rest % (unsigned)G.ny);
+    G.ix = (int)(rest / (unsigned)G.ny);
+    G.RY = 2 * Ky + 1;
+    G.npieces = (2 * G.Kx + 1) * G.RY * G.zs;
+    G.kz0 = 0;
+    if (G.perz)
+        for (int zz = G.iz - G.Kz; zz < 0; zz += G.nz) --G.kz0;
+    return G;
+}
+
+// Piece p < npieces of the stencil: a run of consecutive z-bins of one (x, y)
+// row with one periodic image k.  Pieces with |k_a| > R_a are dropped, which
+// keeps exactly the reference's image box.  Returns whether the piece is
+// kept and writes the image shift and the indices i0, i1 (relative to the
+// structure's first bin) whose bin starts bound the run; dropped pieces get
+// i0 = i1 = 0, so callers may load both unconditionally (every load of a
+// thread in flight at once) and take len = ok ? start(i1) - start(i0) : 0.
+__device__ __forceinline__ bool stencil_piece_rows(const BinGeom& G, int p, int& i0, int& i1,
+                                                   int& kx, int& ky, int& kz) {
+    kx = ky = kz = 0;
+    // p / zs and row / RY through a float reciprocal: p < 2^8 and divisors
+    // below 2^8, so (p + 1/2) / d lies at least 1/512 from an integer while
+    // the float error stays below 2^-15.
+    const float rzs = 1.0f / (float)G.zs, rry = 1.0f / (float)G.RY;
+    const int row = (int)(((float)p + 0.5f) * rzs);
+    const int seg = p - row * G.zs;
+    const int rx = (int)(((float)row + 0.5f) * rry);
+    int jx = G.ix + rx - G.Kx, jy = G.iy + (row - rx * G.RY) - (G.RY >> 1);
+    bool ok;
+    if (G.perx) {
+        while (jx < 0) { jx += G.nx; --kx; }
+        while (jx >= G.nx) { jx -= G.nx; ++kx; }
+        ok = abs(kx) <= G.R0;
+    } else {
+        ok = jx >= 0 && jx < G.nx;
+    }
+    if (G.pery) {
+        while (jy < 0) { jy += G.ny; --ky; }
+        while (jy >= G.ny) { jy -= G.ny; ++ky; }
+        ok = ok && abs(ky) <= G.R1;
+    } else {
+        ok = ok && jy >= 0 && jy < G.ny;
+    }
+    const int zlo = G.iz - G.Kz, zhi = G.iz + G.Kz;
+    int z0, z1;
+    if (G.perz) {
+        kz = G.kz0 + seg;
+        const int zbeg = seg == 0 ? zlo : kz * G.nz;
+        const int zend = min(zhi, (kz + 1) * G.nz - 1);
+        ok = ok && zbeg <= zhi && abs(kz) <= G.R2;
+        z0 = zbeg - kz * G.nz;
+        z1 = zend - kz * G.nz;
+    } else {
+        z0 = max(0, zlo);
+        z1 = min(G.nz - 1, zhi);
+        ok = ok && seg == 0 && z0 <= z1;
+    }
+    const int rowbase = (jx * G.ny + jy) * G.nz;
+    i0 = ok ? rowbase + z0 : 0;
+    i1 = ok ? rowbase + z1 + 1 : 0;
+    return ok;
+}
+
 // Builds the stencil of global bin g with the whole workgroup (every thread
-// calls it; it holds workgroup barriers).  Pieces are runs of consecutive
-// z-bins of one (x, y) row with one periodic image k, one thread per piece;
-// pieces with |k_a| > R_a are dropped, which keeps exactly the reference's
-// image box.  Fills the piece tables of st (and, when tr is given, the
+// calls it; it holds workgroup barriers), one thread per piece
+// (stencil_piece_rows).  Fills the piece tables of st (and, when tr is given, the
 // broad-phase translation of every piece) and, when C <= kMapCap, the piece
 // of every candidate in st.piece (a workgroup running maximum of the marks
 // left at every piece start).  Returns false, before any barrier, when the
@@ -164,7 +255,6 @@ template <typename T>
 __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, StructCache& sc,
                                           CellBin<T>& cb, StencilLds& st,
                                           T (*tr)[kPieceCap] = nullptr,
-                                          EmitTables<T>* et = nullptr,
                                           Vec4<T>* src_pre = nullptr) {
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -182,90 +272,21 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     cb.cut2 = (T)r.cut2;
     cb.wrapped = r.any_wrap != 0;
     cb.diagonal = r.diagonal != 0;
-    const int nx = r.nb[0], ny = r.nb[1], nz = r.nb[2];  // each at least 1
-    const int Kx = r.reach[0], Ky = r.reach[1], Kz = r.reach[2];
-    const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
-    const bool perx = r.active & 1, pery = r.active >> 1 & 1, perz = r.active >> 2 & 1;
-    const int zs = r.zseg;
-    const int iz = (int)(lbin % (unsigned)nz);
-    const unsigned rest = lbin / (unsigned)nz;
-    const int iy = (int)(rest % (unsigned)ny);
-    const int ix = (int)(rest / (unsigned)ny);
-    const int RY = 2 * Ky + 1;
-    const int npieces = (2 * Kx + 1) * RY * zs;  // at most kPieceCap < kBlock
+    const BinGeom G = bin_geom(r, lbin);
+    const int npieces = G.npieces;  // at most kPieceCap < kBlock
     cb.npieces = npieces;
-    const int* bstart = a.bin_start + r.bin0;
-    const int zlo = iz - Kz, zhi = iz + Kz;
-    int kz0 = 0;  // image of the lowest stencil z-bin (zlo < nz)
-    if (perz)
-        for (int zz = zlo; zz < 0; zz += nz) --kz0;
-
     const int p = tid;
-    int len = 0, start = 0, kx = 0, ky = 0, kz = 0;
-    if (p < npieces) {
-        // p / zs and row / RY through a float reciprocal: p < 2^8 and divisors
-        // below 2^8, so (p + 1/2) / d lies at least 1/512 from an integer while
-        // the float error stays below 2^-15.
-        const float rzs = 1.0f / (float)zs, rry = 1.0f / (float)RY;
-        const int row = (int)(((float)p + 0.5f) * rzs);
-        const int seg = p - row * zs;
-        const int rx = (int)(((float)row + 0.5f) * rry);
-        int jx = ix + rx - Kx, jy = iy + (row - rx * RY) - Ky;
-        bool ok;
-        if (perx) {
-            while (jx < 0) { jx += nx; --kx; }
-            while (jx >= nx) { jx -= nx; ++kx; }
-            ok = abs(kx) <= R0;
-        } else {
-            ok = jx >= 0 && jx < nx;
-        }
-        if (pery) {
-            while (jy < 0) { jy += ny; --ky; }
-            while (jy >= ny) { jy -= ny; ++ky; }
-            ok = ok && abs(ky) <= R1;
-        } else {
-            ok = ok && jy >= 0 && jy < ny;
-        }
-        int z0, z1;
-        if (perz) {
-            kz = kz0 + seg;
-            const int zbeg = seg == 0 ? zlo : kz * nz;
-            const int zend = min(zhi, (kz + 1) * nz - 1);
-            ok = ok && zbeg <= zhi && abs(kz) <= R2;
-            z0 = zbeg - kz * nz;
-            z1 = zend - kz * nz;
-        } else {
-            z0 = max(0, zlo);
-            z1 = min(nz - 1, zhi);
-            ok = ok && seg == 0 && z0 <= z1;
-        }
-        if (ok) {
-            const int rowbase = (jx * ny + jy) * nz;
-            start = bstart[rowbase + z0];
-            len = bstart[rowbase + z1 + 1] - start;
-        }
-    }
+    int kx = 0, ky = 0, kz = 0, i0 = 0, i1 = 0;
+    const bool pok = p < npieces && stencil_piece_rows(G, p, i0, i1, kx, ky, kz);
+    const int* bstart = a.bin_start + r.bin0;
+    const int start = bstart[i0];
+    const int len = pok ? bstart[i1] - start : 0;
     cb.sb = uniform(sb_raw);
     cb.se = uniform(se_raw);
     if (cb.sb >= cb.se) return false;
     // clear the piece marks (the previous bin's users passed a barrier)
     reinterpret_cast<unsigned long long*>(st.piece)[tid] = 0ull;
     static_assert(kMapCap == 8 * kBlock, "one 8-byte word of piece marks per thread");
-    if (et) {
-        if (tid == 0) et->kbig = 0;
-        constexpr int NP = 3 * (2 * kProdK + 1) * 3;
-        static_assert(NP <= kBlock, "one product per thread");
-        if (tid < NP) {
-            const int ax = tid / (3 * (2 * kProdK + 1));
-            const int rest_ = tid - ax * 3 * (2 * kProdK + 1);
-            const int kv = rest_ / 3 - kProdK, c = rest_ % 3;
-            const int e = 3 * ax + c;
-            T cv = cb.c[0];
-#pragma unroll
-            for (int q = 1; q < 9; ++q) cv = e == q ? cb.c[q] : cv;
-            et->prod[ax][kv + kProdK][c] = Ops<T>::mul((T)kv, cv);
-        }
-    }
     // workgroup exclusive scan of the piece lengths
     const int inc = wave_inclusive_scan_i32(len);
     if (src_pre) {
@@ -293,10 +314,6 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
                                     (lex_negative(kx, ky, kz) ? 2 : 0));
         if (len > 0 && ex < kMapCap) st.piece[ex] = (unsigned char)p;
         if (tr) image_translation(kk, cb.c, tr[0][p], tr[1][p], tr[2][p]);
-        if (et) {
-            et->pk[p] = make_int4(kx, ky, kz, 0);
-            if (abs(kx) > kProdK || abs(ky) > kProdK || abs(kz) > kProdK) et->kbig = 1;
-        }
     }
     if (tid == 0) st.pre[npieces] = total;
     cb.C = uniform(total);
@@ -331,12 +348,12 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     return true;
 }
 
-// Copies the records of the C <= StageCap<T> candidates into LDS (every
+// Copies the records of the C <= CAP candidates into LDS (every
 // thread calls it; ends with a workgroup barrier).
-template <typename T>
+template <typename T, int CAP>
 __device__ __forceinline__ void stage_candidates(const QueryArgs<T>& a, const StencilLds& st,
                                                  int C, Vec4<T>* cand) {
-    constexpr int NS = StageCap<T>::value / kBlock;
+    constexpr int NS = CAP / kBlock;
     const int tid = threadIdx.x;
     Vec4<T> rec[NS];
     // every load is issued before the first is needed: slots past C re-read
@@ -782,17 +799,27 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
     }
 }
 
+// Sources per decode group of the emitting fast path: at most 64 / nch (one
+// mask word per lane), and so many groups (a multiple of the wave count,
+// dealt round-robin) that every wave of the workgroup gets an equal share
+// of the bin's sources.
+__device__ __forceinline__ int emit_group_size(int nsrc, int nch) {
+    const int S = kWave / nch;
+    const int per_pass = kWavesPerBlock * S;
+    const int groups = kWavesPerBlock * ((nsrc + per_pass - 1) / per_pass);
+    return (nsrc + groups - 1) / groups;
+}
+
 // Emitting fast path: staged candidates, no wrapped representative (the
-// output shift is the image shift k and positions are the records), every
-// |k_a| <= kProdK.  The same decode as emit_bin; a round reads only LDS:
-// the list entry, the owner lane's tag, the candidate record and piece, the
-// piece's shift and the products fl(k_a * cell[a][c]), and evaluates D with
-// the public formula's operation order.  Each source's output range
+// output shift is the image shift k and positions are the records).  The
+// same decode as emit_bin; a round reads only LDS (the list entry, the owner
+// lane's tag, the candidate record, its piece and the piece's shift) and
+// evaluates D with the public formula's operation order.  Each source's output range
 // [offsets[s], offsets[s] + hits) is checked against E once; a source that
 // does not fit raises ST_CAPACITY and writes nothing.
 template <typename T>
 __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLds& st,
-                                          const Vec4<T>* cand, const EmitTables<T>& et,
+                                          const Vec4<T>* cand,
                                           const CellBin<T>& cb, unsigned short* list,
                                           const Vec4<T>& src_all, long long cur_all,
                                           unsigned long long m_pre0, unsigned long long m_pre1) {
@@ -800,12 +827,12 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
     const int lane = lane_id();
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
     const int nch = cb.nch;
-    const int S = kWave / nch;
+    const int S = emit_group_size(cb.se - cb.sb, nch);
     const int sl = (int)(((float)lane + 0.5f) / (float)nch);  // lane = sl * nch + j
     const int j = lane - sl * nch;
     const bool want_d = a.dist != nullptr;
     const bool want_vec = a.vec != nullptr || want_d;
-    // groups of S sources of the bin, dealt round-robin to the waves
+    // groups of S sources of the bin (emit_group_size), dealt round-robin to the waves
     const int wv = uniform(threadIdx.x / kWave);
     const int nsrc = cb.se - cb.sb;  // at most kWave: sources and offsets come preloaded
     int it = 0;
@@ -890,7 +917,7 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                     tg_ = __shfl(tag, w_);
                     const int v = chunk_cand(tg_ & 63, e_ & 63, nch);
                     rec_ = cand[v];
-                    k_ = et.pk[st.piece[v]];
+                    unpack_k(st.kid[st.piece[v]], k_.x, k_.y, k_.z);
                 };
                 int w, tg;
                 Vec4<T> rec;
@@ -923,18 +950,21 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                             *reinterpret_cast<Triple<int32_t>*>(a.shifts + 3 * o) = v;
                         }
                         if (want_vec) {
+                            // D = (p_t - p_s) + S0 c0 + S1 c1 + S2 c2, rounded in T
+                            // after every operation (public_vector)
+                            const T f0 = (T)k.x, f1 = (T)k.y, f2 = (T)k.z;
                             T D0 = O::sub(rec.x, sx), D1 = O::sub(rec.y, sy), D2 = O::sub(rec.z, sz);
                             if (cb.diagonal) {
-                                D0 = O::add(D0, et.prod[0][k.x + kProdK][0]);
-                                D1 = O::add(D1, et.prod[1][k.y + kProdK][1]);
-                                D2 = O::add(D2, et.prod[2][k.z + kProdK][2]);
+                                D0 = O::add(D0, O::mul(f0, cb.c[0]));
+                                D1 = O::add(D1, O::mul(f1, cb.c[4]));
+                                D2 = O::add(D2, O::mul(f2, cb.c[8]));
                             } else {
-                                const T* px = et.prod[0][k.x + kProdK];
-                                const T* py = et.prod[1][k.y + kProdK];
-                                const T* pz = et.prod[2][k.z + kProdK];
-                                D0 = O::add(O::add(O::add(D0, px[0]), py[0]), pz[0]);
-                                D1 = O::add(O::add(O::add(D1, px[1]), py[1]), pz[1]);
-                                D2 = O::add(O::add(O::add(D2, px[2]), py[2]), pz[2]);
+                                D0 = O::add(O::add(O::add(D0, O::mul(f0, cb.c[0])), O::mul(f1, cb.c[3])),
+                                            O::mul(f2, cb.c[6]));
+                                D1 = O::add(O::add(O::add(D1, O::mul(f0, cb.c[1])), O::mul(f1, cb.c[4])),
+                                            O::mul(f2, cb.c[7]));
+                                D2 = O::add(O::add(O::add(D2, O::mul(f0, cb.c[2])), O::mul(f1, cb.c[5])),
+                                            O::mul(f2, cb.c[8]));
                             }
                             if (a.vec) {
                                 Triple<T> v;
@@ -1019,7 +1049,7 @@ k_cell_count(
                 CellBin<T> cb;
                 if (block_bin<T>(a, g, sc, cb, s_st, s_tr)) {
                     const bool staged = cb.C <= StageCap<T>::value;
-                    if (staged) stage_candidates<T>(a, s_st, cb.C, s_cand);
+                    if (staged) stage_candidates<T, StageCap<T>::value>(a, s_st, cb.C, s_cand);
                     wave_sources(cb);
                     if (cb.C <= kMapCap)
                         count_bin_any<T, MODE>(a, s_st, s_cand, staged, s_tr, cb);
@@ -1055,8 +1085,7 @@ template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) void k_cell_emit(
     QueryArgs<T> a) {
     __shared__ StencilLds s_st;
-    __shared__ EmitTables<T> s_et;
-    __shared__ Vec4<T> s_cand[StageCap<T>::value];
+    __shared__ Vec4<T> s_cand[EmitStageCap<T>::value];
     __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
@@ -1066,18 +1095,18 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     StructCache sc{0, 0, 0};
     CellBin<T> cb;
     Vec4<T> src_all;
-    if (!block_bin<T>(a, g, sc, cb, s_st, nullptr, &s_et, &src_all)) return;
+    if (!block_bin<T>(a, g, sc, cb, s_st, nullptr, &src_all)) return;
     const int wv = uniform(threadIdx.x / kWave);
     const int lane = lane_id();
-    if (cb.C <= StageCap<T>::value && !cb.wrapped) {
+    if (cb.C <= EmitStageCap<T>::value && !cb.wrapped) {
         const int nsrc = cb.se - cb.sb;
-        const bool fast = !s_et.kbig && nsrc <= kWave;
+        const bool fast = nsrc <= kWave;
         long long cur_all = 0;
         unsigned long long m0 = 0, m1 = 0;
         if (fast) {
             // offsets and the masks of the wave's first two groups load with the staging
             cur_all = lane < nsrc ? a.offsets[as_idx(src_all.w)] : 0;
-            const int S = kWave / cb.nch;
+            const int S = emit_group_size(nsrc, cb.nch);
             const int sl = (int)(((float)lane + 0.5f) / (float)cb.nch);
             const int j = lane - sl * cb.nch;
             const int s0 = wv * S + sl, s1 = (wv + kWavesPerBlock) * S + sl;
@@ -1086,9 +1115,9 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
             if (sl < S && s1 < min(nsrc, (wv + kWavesPerBlock) * S + S))
                 m1 = a.masks[(int64_t)(cb.sb + s1) * kMaskWords + j];
         }
-        stage_candidates<T>(a, s_st, cb.C, s_cand);
+        stage_candidates<T, EmitStageCap<T>::value>(a, s_st, cb.C, s_cand);
         if (fast) {
-            emit_fast<T>(a, s_st, s_cand, s_et, cb, s_list[wv], src_all, cur_all, m0, m1);
+            emit_fast<T>(a, s_st, s_cand, cb, s_list[wv], src_all, cur_all, m0, m1);
         } else {
             wave_sources(cb);
             emit_bin<T, true, false>(a, s_st, s_cand, cb, s_list[wv]);
