@@ -105,12 +105,12 @@ _HOST = threading.local()
 
 
 def _host_result(device: torch.device):
-    """Pinned status buffer of this thread for `device`, with a ctypes view.
+    """Pinned status buffer of this thread for `device`, its ctypes view and an event.
 
-    tnr_count copies the status words into it and synchronises the stream
-    before returning, so one buffer per thread and device is reused across
-    calls (a fresh pinned allocation per call costs more than the search of
-    a small structure).
+    tnr_count_async copies the status words into the buffer on the stream;
+    the event, recorded right after, tells when they have arrived.  One
+    buffer per thread and device is reused across calls (a fresh pinned
+    allocation per call costs more than the search of a small structure).
     """
     cache = getattr(_HOST, "buffers", None)
     if cache is None:
@@ -119,8 +119,64 @@ def _host_result(device: torch.device):
     if entry is None:
         host = torch.empty(HOST_RESULT_SLOTS, dtype=torch.int64, pin_memory=True)
         view = (ctypes.c_int64 * HOST_RESULT_SLOTS).from_address(host.data_ptr())
-        entry = cache[device] = (host, view)
+        entry = cache[device] = (host, view, torch.cuda.Event())
     return entry
+
+
+def _speculation() -> dict:
+    """This thread's last (output capacity, plan, bins) per request shape."""
+    table = getattr(_HOST, "speculation", None)
+    if table is None:
+        table = _HOST.speculation = {}
+    return table
+
+
+# Output capacity of the next call of a shape: the last pair count plus
+# 1/32 and a constant, which covers the drift of a molecular-dynamics step.
+def _capacity(n_pairs: int) -> int:
+    return n_pairs + (n_pairs >> 5) + 4096
+
+
+_ROWS = {
+    "P": ((2,), torch.int64),
+    "S": ((3,), torch.int32),
+    "i": ((), torch.int64),
+    "j": ((), torch.int64),
+}
+
+
+def _allocate(want: set, rows: int, dtype: torch.dtype, device: torch.device) -> dict:
+    out = {}
+    for q in ("P", "S", "i", "j", "d", "D"):
+        if q not in want:
+            continue
+        if q in _ROWS:
+            tail, qdtype = _ROWS[q]
+        else:
+            tail, qdtype = ((3,) if q == "D" else ()), dtype
+        out[q] = torch.empty((rows, *tail), dtype=qdtype, device=device)
+    return out
+
+
+def _emit(lib, req, workspace: Tensor, ws_bytes: int, out: dict, rows: int, plan: int,
+          bins: int, stream: int, err) -> None:
+    ptrs = Outputs(
+        n_pairs=rows,
+        plan=plan,
+        n_tasks=bins,
+        pairs=out["P"].data_ptr() if "P" in out else None,
+        shifts=out["S"].data_ptr() if "S" in out else None,
+        distances=out["d"].data_ptr() if "d" in out else None,
+        vectors=out["D"].data_ptr() if "D" in out else None,
+        sources=out["i"].data_ptr() if "i" in out else None,
+        targets=out["j"].data_ptr() if "j" in out else None,
+    )
+    code = lib.tnr_emit(
+        ctypes.byref(req), workspace.data_ptr(), ws_bytes, ctypes.byref(ptrs), stream, err,
+        len(err),
+    )
+    if code != TNR_OK:
+        _raise(code, err.value.decode())
 
 
 def _raise(code: int, message: str) -> None:
@@ -144,7 +200,19 @@ def neighbor_list_hip(
     grad_positions: Tensor | None = None,
     grad_cell: Tensor | None = None,
 ) -> tuple[Tensor, ...]:
-    """Run count + emit on the tensors' HIP device; returns one tensor per quantity."""
+    """Run count + emit on the tensors' HIP device; returns one tensor per quantity.
+
+    The first call of a request shape (device, dtype, sizes, pair policy,
+    algorithm, quantities) counts, waits for the pair count E and writes
+    outputs of exactly E rows, as the reference does.  A repeated call of
+    the same shape launches the writing pass right behind the count, into
+    outputs sized from the previous call's count plus a margin, and waits
+    only for the count: when E fits (and the plan and bins match the
+    launch) the results are the first E rows of those outputs; otherwise
+    the writing pass runs again with exact sizes.  Either way the returned
+    values are the same; a repeated call's tensors may be views of slightly
+    larger allocations.
+    """
     try:
         lib = load_torch_hip()
     except ImportError as error:
@@ -175,57 +243,58 @@ def neighbor_list_hip(
         sorted=int(sorted),
         stencil_reach=0,
     )
+    dtype = positions.dtype
+    want = set(quantities)
+    if need_grad:
+        want |= {"P", "S"}
+        want -= {"d", "D"}
     err = ctypes.create_string_buffer(512)
     switch = device.index is not None and device.index != torch.cuda.current_device()
     with torch.cuda.device(device) if switch else contextlib.nullcontext():
-        stream = torch.cuda.current_stream(device).cuda_stream
+        torch_stream = torch.cuda.current_stream(device)
+        stream = torch_stream.cuda_stream
         ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-        host, host_view = _host_result(device)
-        n_pairs = ctypes.c_int64(0)
-        code = lib.tnr_count(
-            ctypes.byref(req), workspace.data_ptr(), ws_bytes, host.data_ptr(), stream,
-            ctypes.byref(n_pairs), err, len(err),
+        host, host_view, arrived = _host_result(device)
+        code = lib.tnr_count_async(
+            ctypes.byref(req), workspace.data_ptr(), ws_bytes, host.data_ptr(), stream, err,
+            len(err),
         )
         if code != TNR_OK:
             _raise(code, err.value.decode())
-        count = int(n_pairs.value)
-        dtype = positions.dtype
-        want = set(quantities)
-        if need_grad:
-            want |= {"P", "S"}
-            want -= {"d", "D"}
+        arrived.record(torch_stream)
+        key = (device, req.dtype, req.n_atoms, req.n_structures, req.half_list,
+               req.include_self, req.algorithm, frozenset(want))
+        table = _speculation()
+        guess = table.get(key)
         out: dict[str, Tensor] = {}
-        if "P" in want:
-            out["P"] = torch.empty((count, 2), dtype=torch.int64, device=device)
-        if "S" in want:
-            out["S"] = torch.empty((count, 3), dtype=torch.int32, device=device)
-        if "i" in want:
-            out["i"] = torch.empty((count,), dtype=torch.int64, device=device)
-        if "j" in want:
-            out["j"] = torch.empty((count,), dtype=torch.int64, device=device)
-        if "d" in want:
-            out["d"] = torch.empty((count,), dtype=dtype, device=device)
-        if "D" in want:
-            out["D"] = torch.empty((count, 3), dtype=dtype, device=device)
-        if count > 0 and out:
-            ptrs = Outputs(
-                n_pairs=count,
-                plan=host_view[3],
-                n_tasks=host_view[7],
-                pairs=out["P"].data_ptr() if "P" in out else None,
-                shifts=out["S"].data_ptr() if "S" in out else None,
-                distances=out["d"].data_ptr() if "d" in out else None,
-                vectors=out["D"].data_ptr() if "D" in out else None,
-                sources=out["i"].data_ptr() if "i" in out else None,
-                targets=out["j"].data_ptr() if "j" in out else None,
+        if guess is not None and want:
+            capacity, plan_guess, bins_guess = guess
+            out = _allocate(want, capacity, dtype, device)
+            _emit(lib, req, workspace, ws_bytes, out, capacity, plan_guess, bins_guess, stream, err)
+        arrived.synchronize()
+        n_pairs = ctypes.c_int64(0)
+        code = lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n_pairs), err, len(err))
+        if code != TNR_OK:
+            _raise(code, err.value.decode())
+        count = int(n_pairs.value)
+        plan, bins = int(host_view[3]), int(host_view[7])
+        if guess is not None and want:
+            fits = (
+                count <= capacity
+                and (plan & ~plan_guess) == 0
+                and (not plan & 2 or bins <= bins_guess)
             )
-            code = lib.tnr_emit(
-                ctypes.byref(req), workspace.data_ptr(), ws_bytes, ctypes.byref(ptrs), stream,
-                err, len(err),
-            )
-            if code != TNR_OK:
-                _raise(code, err.value.decode())
+            if count > capacity:
+                out = _allocate(want, count, dtype, device)
+            if not fits and count > 0:
+                _emit(lib, req, workspace, ws_bytes, out, count, plan, bins, stream, err)
+            out = {q: t[:count] for q, t in out.items()}
+        else:
+            out = _allocate(want, count, dtype, device)
+            if count > 0 and out:
+                _emit(lib, req, workspace, ws_bytes, out, count, plan, bins, stream, err)
+        table[key] = (_capacity(count), plan, bins)
         if need_grad:
             out.update(
                 _differentiable_geometry(

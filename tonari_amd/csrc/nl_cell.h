@@ -816,7 +816,7 @@ __device__ __forceinline__ int emit_group_size(int nsrc, int nch) {
 // lane's tag, the candidate record, its piece and the piece's shift) and
 // evaluates D with the public formula's operation order.  Each source's output range
 // [offsets[s], offsets[s] + hits) is checked against E once; a source that
-// does not fit raises ST_CAPACITY and writes nothing.
+// does not fit raises ST_OUTPUT_RANGE and writes nothing.
 template <typename T>
 __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLds& st,
                                           const Vec4<T>* cand,
@@ -867,7 +867,7 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                 if (__builtin_amdgcn_ballot_w64(bad)) {
                     if (bad) {
                         m = 0;
-                        atomicOr(a.status + SS_FLAGS, ST_CAPACITY);
+                        atomicOr(a.status + SS_FLAGS, ST_OUTPUT_RANGE);
                     }
                     c = __popcll(m);
                     incl = wave_inclusive_scan_i32(c);
@@ -1078,9 +1078,10 @@ static_assert(StageCap<float>::value <= kMapCap && StageCap<double>::value <= kM
               "staged stencils have a piece map");
 
 // Emitting pass: one workgroup per bin, mapped XCD-aware (workgroup b runs
-// on XCD b % 8; XCD x takes the x-th eighth of the bins).  The grid covers
-// the bins of the count (out->n_tasks), so the kernel can run again on the
-// same workspace.
+// on XCD b % 8; XCD x takes the x-th eighth of the bins).  The grid is sized
+// for out->n_tasks bins; the kernel reads the batch's bin count from the
+// status words and only trusts the smaller of the two, and it can run again
+// on the same workspace.
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) void k_cell_emit(
     QueryArgs<T> a) {
@@ -1089,7 +1090,10 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
-    const ItemRange br = xcd_block_range(a.n_bins);
+    // the batch's bins from the count's status words; the grid may cover
+    // more (a launch sized before the count finished)
+    const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_TASKS);
+    const ItemRange br = xcd_block_range(min(a.n_bins, bins));
     const int64_t g = br.first;
     if (g >= br.end) return;
     StructCache sc{0, 0, 0};

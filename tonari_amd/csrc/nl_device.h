@@ -41,6 +41,10 @@ enum StatusBit : unsigned long long {
     ST_CELL_UNSAFE = 1ull << 12,
     ST_CAPACITY = 1ull << 13,
     ST_SCAN_STALL = 1ull << 14,
+    // emitting pass: a pair index at or beyond the caller's output length
+    // (outputs sized for another pair count); not an abort bit, so the pass
+    // can run again on the same workspace with larger outputs
+    ST_OUTPUT_RANGE = 1ull << 15,
 };
 // Bits that make every later kernel skip its work (inputs are unusable).
 constexpr unsigned long long kAbortBits =

@@ -31,7 +31,7 @@ struct QueryArgs {
     int64_t n_atoms;
     int64_t nb;
     int64_t limit;  // E: emit never writes at or beyond it
-    int64_t n_bins; // emit: cell-list bins of the batch (from the count's status words)
+    int64_t n_bins; // emit: cell-list bins covered by the grid (at least the batch's)
     // outputs (emit)
     int64_t* pairs;
     int32_t* shifts;
@@ -56,7 +56,7 @@ __device__ __forceinline__ void write_hit(const QueryArgs<T>& a, long long o, in
                                           int S0, int S1, int S2, const T ps[3], const T pt[3],
                                           const T* cell, bool diagonal) {
     if (o < 0 || o >= a.limit) {
-        atomicOr(a.status + SS_FLAGS, ST_CAPACITY);
+        atomicOr(a.status + SS_FLAGS, ST_OUTPUT_RANGE);
         return;
     }
     if (a.pairs) {
