@@ -115,9 +115,11 @@ enum RedSlot : int { kRedUlo = 0, kRedUhi = 3, kRedClo = 6, kRedChi = 9, kRedP =
                      kRedCount = 14 };
 
 // Per-block reduction record written by k_atoms for blocks whose atoms all
-// lie in one structure (k_plan combines them without atomics).
+// lie in one structure (k_plan combines them without atomics); for a
+// single-structure request also the block's atom error bits.
 struct alignas(16) BlockPartial {
     unsigned long long red[kRedCount];
+    unsigned long long flags;
 };
 
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte

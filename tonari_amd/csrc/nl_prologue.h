@@ -16,7 +16,7 @@ namespace tnr {
 // geometry.cpp:15-118, carried out in double instead of long double.  Loops
 // run over all three columns with guards so every index is static (no
 // scratch memory).  Returns false when the active rows are linearly dependent.
-__device__ bool active_pinv(double w[3][3], int k, double dual[3][3]) {
+__device__ __forceinline__ bool active_pinv(double w[3][3], int k, double dual[3][3]) {
     double v[3][3] = {{1, 0, 0}, {0, 1, 0}, {0, 0, 1}};
     const double eps = 2.220446049250313e-16;
     for (int sweep = 0; sweep < 64; ++sweep) {
@@ -95,30 +95,15 @@ __device__ inline void normalize3(double v[3]) {
     }
 }
 
-// One thread per structure: batch_ptr checks, periodic metadata
-// (geometry.cpp:123-219) and the grid frame used for binning.  Grid rows:
+// Structure b (one thread): batch_ptr checks, periodic metadata
+// (geometry.cpp:123-219) and the grid frame used for binning, into r.  Grid rows:
 // dual columns on periodic axes (the grid coordinate is the fractional
 // coordinate) and orthonormal complements of the periodic rows elsewhere.
-// Block 0 first zeroes the status block of the request (every later kernel
-// reads it).  Per-structure errors go to the record (k_plan folds them into
-// the status words), so no thread races the zeroing.
+// Per-structure errors go to the record's flags.
 template <typename T>
-__global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb,
-                        int64_t n_atoms, double cutoff, StructRec* recs,
-                        unsigned long long* status) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (blockIdx.x == 0) {
-        for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
-        __syncthreads();
-        if (nb == 0 && threadIdx.x == 0) {
-            unsigned long long st = 0;
-            if (bp[0] != 0) st |= ST_BP_START;
-            if (bp[0] != n_atoms) st |= ST_BP_END;
-            status[SS_FLAGS] = st;
-        }
-    }
-    if (b >= nb) return;
-    StructRec& r = recs[b];
+__device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cells,
+                                                const uint8_t* pbc, int64_t nb, int64_t n_atoms,
+                                                double cutoff, int64_t b, StructRec& r) {
     unsigned long long st = 0;
     const int64_t lo = bp[b], hi = bp[b + 1];
     if (b == 0 && lo != 0) st |= ST_BP_START;
@@ -182,7 +167,9 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
         for (int j = 0; j < 3; ++j)
 #pragma unroll
             for (int c = 0; c < 3; ++c)
-                w[c][j] = j < k ? cell[slot_axis[j] == 0 ? 0 : (slot_axis[j] == 1 ? 1 : 2)][c] : 0.0;
+                w[c][j] = j >= k ? 0.0
+                                 : (slot_axis[j] == 0 ? cell[0][c]
+                                                      : (slot_axis[j] == 1 ? cell[1][c] : cell[2][c]));
         if (k > 0 && !active_pinv(w, k, dual_slot)) st |= ST_CELL_RANK;
         int64_t reps[3] = {0, 0, 0};
         if (!(st & ST_CELL_RANK)) {
@@ -302,6 +289,29 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
     r.flags = st;
 }
 
+// One thread per structure (setup_structure).  Block 0 first zeroes the
+// status block of the request (every later kernel reads it).  Per-structure
+// errors go to the record (k_plan folds them into the status words), so no
+// thread races the zeroing.
+template <typename T>
+__global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb,
+                        int64_t n_atoms, double cutoff, StructRec* recs,
+                        unsigned long long* status) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
+        __syncthreads();
+        if (nb == 0 && threadIdx.x == 0) {
+            unsigned long long st = 0;
+            if (bp[0] != 0) st |= ST_BP_START;
+            if (bp[0] != n_atoms) st |= ST_BP_END;
+            status[SS_FLAGS] = st;
+        }
+    }
+    if (b >= nb) return;
+    setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, recs[b]);
+}
+
 // Structure of atom i: the b with bp[b] <= i < bp[b + 1] (batch_ptr valid).
 __device__ __forceinline__ int structure_of(const int64_t* bp, int64_t nb, int64_t i) {
     int64_t lo = 0, hi = nb;  // answer in [lo, hi)
@@ -360,16 +370,23 @@ __device__ __forceinline__ void grid_coords(const StructRec& r, const T q[3], do
 // structure records (each such structure is small, so contention is low).
 // The grid also zeroes the bin counters and the tile states of the two
 // single-pass scans, which later kernels of the request use.
-template <typename T>
+//
+// SINGLE (a request of one structure with atoms): the grid also does the
+// work of k_setup.  Every block derives the structure's record in LDS
+// (thread 0) and block 0 stores it; the atoms' error bits go to the block's
+// partial instead of the status words, which k_single_bin writes.
+template <typename T, bool SINGLE>
 __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* bp,
-                                                   const T* cells, int64_t nb, int64_t n_atoms,
+                                                   const T* cells, const uint8_t* pbc,
+                                                   double cutoff, int64_t nb, int64_t n_atoms,
                                                    StructRec* recs, BlockPartial* partials,
                                                    int* atom_struct, int4* atom_wrap,
                                                    Vec4<T>* atom_q, unsigned long long* status,
                                                    int* bin_count, int64_t n_bin_count,
                                                    unsigned long long* tiles, int64_t n_tiles) {
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
-    __shared__ unsigned long long s_flags;
+    __shared__ unsigned long long s_flags, s_atom_flags;
+    __shared__ StructRec s_rec;
     {
         const int64_t stride = (int64_t)gridDim.x * kBlock;
         for (int64_t k = (int64_t)blockIdx.x * kBlock + threadIdx.x; k < n_bin_count; k += stride)
@@ -377,16 +394,35 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
         for (int64_t k = (int64_t)blockIdx.x * kBlock + threadIdx.x; k < n_tiles; k += stride)
             tiles[k] = 0;
     }
+    // the atom's position loads while thread 0 derives the record
+    const int64_t ia = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t ic = ia < n_atoms ? ia : (n_atoms > 0 ? n_atoms - 1 : 0);
+    T p_pre[3] = {T(0), T(0), T(0)};
+    if (n_atoms > 0)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) p_pre[c] = pos[3 * ic + c];
     // Block-uniform early exit (the barrier below needs every thread).
-    if (threadIdx.x == 0) s_flags = load_status(status + SS_FLAGS);
+    if (threadIdx.x == 0) {
+        if constexpr (SINGLE) {
+            setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, 0, s_rec);
+            if (blockIdx.x == 0) recs[0] = s_rec;
+            s_flags = s_rec.flags;
+            s_atom_flags = 0;
+        } else {
+            s_flags = load_status(status + SS_FLAGS);
+        }
+    }
     __syncthreads();
-    if (s_flags & kAbortBits) return;
+    if (s_flags & kAbortBits) {
+        if (SINGLE && threadIdx.x == 0) partials[blockIdx.x].flags = 0;
+        return;
+    }
     const int64_t first = (int64_t)blockIdx.x * kBlock;
     const int64_t last = (first + kBlock < n_atoms ? first + kBlock : n_atoms) - 1;
     const int64_t i = first + threadIdx.x;
     const bool valid = i < n_atoms;
-    const int bfirst = structure_of(bp, nb, first);
-    const int blast = structure_of(bp, nb, last);
+    const int bfirst = SINGLE ? 0 : structure_of(bp, nb, first);
+    const int blast = SINGLE ? 0 : structure_of(bp, nb, last);
     const bool uniform = bfirst == blast;
     int b = bfirst;
     bool good = false;
@@ -398,12 +434,12 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
     if (valid) {
         b = uniform ? bfirst : structure_of(bp, nb, i);
         atom_struct[i] = b;
-        const StructRec& r = recs[b];
+        const StructRec& r = SINGLE ? s_rec : recs[b];
         T p[3];
         bool finite = true;
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
-            p[c] = pos[3 * i + c];
+            p[c] = p_pre[c];
             finite = finite && isfinite((double)p[c]);
         }
         if (r.flags & kAbortBits) {
@@ -439,7 +475,12 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
         atom_wrap[i] = make_int4(w[0], w[1], w[2], 0);
         atom_q[i] = Vec4<T>{q[0], q[1], q[2], idx_as((int)i, T(0))};
     }
-    if (st) atomicOr(status + SS_FLAGS, st);
+    if (st) {
+        if constexpr (SINGLE)
+            atomicOr(&s_atom_flags, st);
+        else
+            atomicOr(status + SS_FLAGS, st);
+    }
 
     // the 14 reductions as max-keys (0 = identity for atoms that contribute nothing)
     using K = RedKeys<T>;
@@ -468,6 +509,7 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
             for (int k = 1; k < kWavesPerBlock; ++k) x = s_red[k][e] > x ? s_red[k][e] : x;
             partials[blockIdx.x].red[e] = x;
         }
+        if (threadIdx.x == kRedCount) partials[blockIdx.x].flags = SINGLE ? s_atom_flags : 0ull;
     } else {
         // several structures: a segmented maximum per wave, then one atomic
         // per (wave, structure, reduction) from the segment's last lane
@@ -490,27 +532,33 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
 }
 
 
-// Planner of one structure (one thread): from the reduced bounds v (see
+// Planner of one structure, run by all lanes of one wave (lane 0 writes the
+// record and the per-structure arrays): from the reduced bounds red (see
 // k_plan) the broad-phase margin, the algorithm and the bin grid.  The
 // margin pad = 64 eps_T max(scale, rc) bounds the difference between the
 // fused broad-phase distance and the public predicate, with scale = 2 max|p| +
 // sum_a (R_a + 2 max|w|) max_c |cell_ac|, the operation scale of
-// neighbors_cpu.cpp:156-219.
+// neighbors_cpu.cpp:156-219.  The candidate stencil reaches are evaluated one
+// per lane.
 template <typename T>
-__device__ void plan_structure(const T* cells, int64_t b, StructRec& r,
-                               const unsigned long long red[kRedCount], double cutoff,
-                               int requested, int reach_target, long long* struct_bins,
-                               long long* struct_tasks, long long* struct_ctasks) {
+__device__ __forceinline__ void plan_structure(const T* cells, int64_t b, StructRec& r,
+                                               const unsigned long long red[kRedCount],
+                                               double cutoff, int requested, int reach_target,
+                                               long long* struct_bins, long long* struct_tasks,
+                                               long long* struct_ctasks) {
     using K = RedKeys<T>;
+    const bool writer = lane_id() == 0;
     const int64_t n = r.natoms;
     if (n == 0) {
-        r.algo = ALGO_NONE;
-        r.nbins = 0;
-        r.parts = 1;
-        r.cparts = 1;
-        struct_bins[b] = 0;
-        struct_tasks[b] = 0;
-        struct_ctasks[b] = 0;
+        if (writer) {
+            r.algo = ALGO_NONE;
+            r.nbins = 0;
+            r.parts = 1;
+            r.cparts = 1;
+            struct_bins[b] = 0;
+            struct_tasks[b] = 0;
+            struct_ctasks[b] = 0;
+        }
         return;
     }
     double cell[9];
@@ -531,14 +579,16 @@ __device__ void plan_structure(const T* cells, int64_t b, StructRec& r,
     }
     const double rc = cutoff;
     const double pad = 64.0 * Ops<T>::eps * fmax(scale, rc);
-    r.pad = pad;
-    r.maxp = (unsigned long long)__double_as_longlong(maxp);
-    r.maxw = maxw_u;
-    r.any_wrap = maxw_u != 0;
     const double inner = rc - pad;
-    r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
-    r.outer2 = (double)Ops<T>::up((rc + pad) * (rc + pad));
-    r.cut2 = (double)(T)(cutoff * cutoff);
+    if (writer) {
+        r.pad = pad;
+        r.maxp = (unsigned long long)__double_as_longlong(maxp);
+        r.maxw = maxw_u;
+        r.any_wrap = maxw_u != 0;
+        r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
+        r.outer2 = (double)Ops<T>::up((rc + pad) * (rc + pad));
+        r.cut2 = (double)(T)(cutoff * cutoff);
+    }
     const bool safe = isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Ops<T>::max;
 
     const int64_t nimages = r.nimages;
@@ -573,13 +623,13 @@ __device__ void plan_structure(const T* cells, int64_t b, StructRec& r,
         // stages its stencil once for all of its sources; stencils beyond
         // the mask capacity take the slow path and count four times.
         const double rcu0 = rc + 2 * pad;
-        double best_c = INFINITY;
-        int k_lo = reach_target > 0 ? reach_target : 1;
-        int k_hi = reach_target > 0 ? reach_target : 4;
-        for (int kt_i = k_lo; kt_i <= k_hi; ++kt_i) {
+        const int k_lo = reach_target > 0 ? reach_target : 1;
+        const int k_hi = reach_target > 0 ? reach_target : 4;
+        const int lane = lane_id();
+        const int kt_i = min(k_lo + lane, k_hi);
         const double kt = (double)kt_i;
         double ext[3], wdt[3], nbf[3], rcu[3], lo[3];
-        bool ok = true;
+        bool ok = k_lo + lane <= k_hi;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
             const double gn = sqrt(r.grid[3 * a] * r.grid[3 * a] +
@@ -634,7 +684,6 @@ __device__ void plan_structure(const T* cells, int64_t b, StructRec& r,
         const bool fits = ok && reach_ok && nbf[0] * nbf[1] * nbf[2] <= capb &&
                           (long long)rows * zs <= kPieceCap &&
                           (double)n * (double)(rows * zs) < 2147483647.0;
-        if (!fits) continue;
         // estimated candidates of a stencil and sources of a bin
         const double bins_f = nbf[0] * nbf[1] * nbf[2];
         const double per_bin = (double)n / bins_f;
@@ -645,32 +694,57 @@ __device__ void plan_structure(const T* cells, int64_t b, StructRec& r,
             span_bins *= (active >> a & 1) ? w : fmin(w, nbf[a]);
         }
         const double cand = span_bins * per_bin;
-        const double cost = cand * (1.0 + kBinOverhead / fmax(per_bin, 1e-9)) *
-                            (cand > (double)(kMaskWords * kWave) ? 4.0 : 1.0);
-        const bool take = best_c == INFINITY || cost < best_c;
-        if (!take) continue;
-        best_c = cost;
-        algo = ALGO_CELL;
-        nbins = (int64_t)bins_f;
+        double cost = cand * (1.0 + kBinOverhead / fmax(per_bin, 1e-9)) *
+                      (cand > (double)(kMaskWords * kWave) ? 4.0 : 1.0);
+        // the cheapest fitting reach, the smallest on ties
+        cost = fits ? fmin(cost, 1.7976931348623157e308) : INFINITY;
+        int best = lane;
 #pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            r.nb[a] = (int32_t)nbf[a];
-            r.inv_w[a] = (active >> a & 1) ? nbf[a] : 1.0 / wdt[a];
-            r.lo[a] = lo[a];
-            r.reach[a] = reach[a];
+        for (int d = kWave / 2; d > 0; d >>= 1) {
+            const double oc = __shfl_xor(cost, d);
+            const int ob = __shfl_xor(best, d);
+            if (oc < cost || (oc == cost && ob < best)) {
+                cost = oc;
+                best = ob;
+            }
         }
-        r.zseg = zs;
+        best = __builtin_amdgcn_readfirstlane(best);
+        if (cost < INFINITY) {
+            algo = ALGO_CELL;
+            nbins = (int64_t)__shfl(bins_f, best);
+            double nbw[3], invw[3], low[3];
+            int rch[3];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                nbw[a] = __shfl(nbf[a], best);
+                invw[a] = __shfl((active >> a & 1) ? nbf[a] : 1.0 / wdt[a], best);
+                low[a] = __shfl(lo[a], best);
+                rch[a] = __shfl(reach[a], best);
+            }
+            const int zsb = __shfl(zs, best);
+            if (writer) {
+#pragma unroll
+                for (int a = 0; a < 3; ++a) {
+                    r.nb[a] = (int32_t)nbw[a];
+                    r.inv_w[a] = invw[a];
+                    r.lo[a] = low[a];
+                    r.reach[a] = rch[a];
+                }
+                r.zseg = zsb;
+            }
         }
     }
-    r.algo = algo;
-    r.nbins = nbins;
-    // one workgroup per bin in both query passes
-    r.parts = 1;
-    r.cparts = 1;
-    struct_bins[b] = nbins;
-    struct_tasks[b] = nbins * r.parts;
-    struct_ctasks[b] = nbins * r.cparts;
-    r.flags |= st;
+    if (writer) {
+        r.algo = algo;
+        r.nbins = nbins;
+        // one workgroup per bin in both query passes
+        r.parts = 1;
+        r.cparts = 1;
+        struct_bins[b] = nbins;
+        struct_tasks[b] = nbins;
+        struct_ctasks[b] = nbins;
+        r.flags |= st;
+    }
 }
 
 // One workgroup per structure: combines the block partials of k_atoms (all
@@ -726,12 +800,14 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
 #pragma unroll
                 for (int e = 0; e < kRedCount; ++e) s_red[wv][e] = v[e];
             __syncthreads();
-            if (tid == 0) {
+            if (wv == 0) {
 #pragma unroll
-                for (int e = 0; e < kRedCount; ++e)
+                for (int e = 0; e < kRedCount; ++e) {
+                    v[e] = s_red[0][e];
 #pragma unroll
                     for (int w = 1; w < kWavesPerBlock; ++w)
                         v[e] = s_red[w][e] > v[e] ? s_red[w][e] : v[e];
+                }
                 plan_structure<T>(cells, b, r, v, cutoff, requested, reach_target, struct_bins,
                                   struct_tasks, struct_ctasks);
             }
@@ -793,6 +869,114 @@ __global__ __launch_bounds__(kBlock) void k_bin(int64_t n_atoms, const StructRec
         atom_bin[i] = -1;
         return;
     }
+    atom_bin[i] = (int)g;
+    atom_rank[i] = atomicAdd(bin_count + g, 1);
+}
+
+// Single-structure request: k_plan, the planner's batch step and k_bin in
+// one kernel.  Every block combines the partials of k_atoms<T, true> (the
+// reductions and the atoms' error bits, all loads in flight at once) and
+// plans the structure itself (thread 0, into an LDS copy of the record), so
+// no block waits for another; block 0 stores the plan and writes the status
+// words (all zero first: nothing has written them yet in this request).
+// Then every block bins its atoms as k_bin does.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_single_bin(
+    const T* cells, int64_t n_atoms, double cutoff, int requested, int reach_target,
+    StructRec* recs, const BlockPartial* partials, int64_t n_partials, const Vec4<T>* atom_q,
+    int* atom_bin, int* atom_rank, int* bin_count, long long* struct_bins,
+    long long* struct_tasks, long long* struct_ctasks, long long* bin_off, long long* task_off,
+    long long* ctask_off, int64_t cap_bins, unsigned long long* status) {
+    using K = RedKeys<T>;
+    __shared__ StructRec s_rec;
+    __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
+    __shared__ long long s_bins, s_tasks, s_ctasks;
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
+    // the record (16-byte words) and this thread's partials in one round trip
+    constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(int4));
+    static_assert(sizeof(StructRec) % sizeof(int4) == 0 && kRecWords <= kBlock, "record copy");
+    if (tid < kRecWords)
+        reinterpret_cast<int4*>(&s_rec)[tid] = reinterpret_cast<const int4*>(recs)[tid];
+    const int64_t i = (int64_t)blockIdx.x * kBlock + tid;
+    const Vec4<T> qv = atom_q[i < n_atoms ? i : n_atoms - 1];
+    unsigned long long v[kRedCount + 1];
+#pragma unroll
+    for (int e = 0; e <= kRedCount; ++e) v[e] = 0;
+    static_assert(kRedCount % 2 == 0 && sizeof(BlockPartial) == 8 * (kRedCount + 2),
+                  "partials load as 16-byte words");
+#pragma unroll 2
+    for (int64_t kb = tid; kb < n_partials; kb += kBlock) {
+        const ulonglong2* w = reinterpret_cast<const ulonglong2*>(partials + kb);
+        ulonglong2 x[kRedCount / 2 + 1];
+#pragma unroll
+        for (int e = 0; e <= kRedCount / 2; ++e) x[e] = w[e];
+#pragma unroll
+        for (int e = 0; e < kRedCount / 2; ++e) {
+            v[2 * e] = x[e].x > v[2 * e] ? x[e].x : v[2 * e];
+            v[2 * e + 1] = x[e].y > v[2 * e + 1] ? x[e].y : v[2 * e + 1];
+        }
+        v[kRedCount] |= x[kRedCount / 2].x;
+    }
+#pragma unroll
+    for (int e = 0; e < kRedCount; ++e) v[e] = K::wave_max(v[e]);
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) v[kRedCount] |= __shfl_xor(v[kRedCount], d);
+    if (lane == 0)
+#pragma unroll
+        for (int e = 0; e <= kRedCount; ++e) s_red[wv][e] = v[e];
+    __syncthreads();
+    if (wv == 0) {
+#pragma unroll
+        for (int e = 0; e <= kRedCount; ++e) v[e] = s_red[0][e];
+#pragma unroll
+        for (int w = 1; w < kWavesPerBlock; ++w) {
+#pragma unroll
+            for (int e = 0; e < kRedCount; ++e) v[e] = s_red[w][e] > v[e] ? s_red[w][e] : v[e];
+            v[kRedCount] |= s_red[w][kRedCount];
+        }
+        StructRec& r = s_rec;
+        const unsigned long long flags = r.flags | v[kRedCount];
+        if (lane == 0) {
+            r.flags = flags;
+            s_bins = s_tasks = s_ctasks = 0;
+            r.algo = ALGO_NONE;
+        }
+        if (!(flags & kAbortBits))
+            plan_structure<T>(cells, 0, r, v, cutoff, requested, reach_target, &s_bins, &s_tasks,
+                              &s_ctasks);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        StructRec& r = s_rec;
+        r.bin0 = r.task0 = r.ctask0 = 0;
+        if (blockIdx.x == 0) {
+            recs[0] = r;
+            struct_bins[0] = s_bins;
+            struct_tasks[0] = s_tasks;
+            struct_ctasks[0] = s_ctasks;
+            bin_off[0] = task_off[0] = ctask_off[0] = 0;
+            bin_off[1] = task_off[1] = ctask_off[1] = s_bins;
+            for (int k = 0; k < SS_SLOTS; ++k) status[k] = 0;
+            const unsigned long long images = (unsigned long long)r.img_total;
+            unsigned long long st = r.flags;
+            if (s_bins > cap_bins) st |= ST_CAPACITY;
+            if (images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+            status[SS_TOTAL_BINS] = status[SS_TOTAL_TASKS] = status[SS_TOTAL_CTASKS] =
+                (unsigned long long)s_bins;
+            status[SS_PLAN] = r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
+            status[SS_TOTAL_IMAGES] = images;
+            status[SS_FLAGS] = st;
+        }
+    }
+    __syncthreads();
+    const StructRec& r = s_rec;
+    if ((r.flags & kAbortBits) || s_bins > cap_bins || i >= n_atoms) return;
+    if (r.algo != ALGO_CELL) {
+        atom_bin[i] = -1;
+        return;
+    }
+    const T q[3] = {qv.x, qv.y, qv.z};
+    const int64_t g = local_bin(r, q);
     atom_bin[i] = (int)g;
     atom_rank[i] = atomicAdd(bin_count + g, 1);
 }

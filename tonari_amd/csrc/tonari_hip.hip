@@ -213,34 +213,48 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                             hipStream_t stream) {
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
-    // k_setup zeroes the status words; k_atoms zeroes the bin counters and
-    // the tile states of both single-pass scans.
-    k_setup<T><<<blocks_for(nb > 0 ? nb : 1, 64), 64, 0, stream>>>(
-        req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, v.recs, v.status);
-    if (n > 0) {
-        const int64_t n_tiles =
-            (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) +
-            L.n_tiles_pairs;
-        k_atoms<T><<<blocks_for(n), kBlock, 0, stream>>>(
-            (const T*)req->positions, req->batch_ptr, (const T*)req->cell, nb, n, v.recs,
-            v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q, v.status,
-            v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
-    }
     const int reach = req->stencil_reach;  // 0: chosen per structure
-    // a single structure is planned and scanned by one workgroup
-    const int fused_scan = nb <= 1 ? 1 : 0;
-    k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
-        (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
-        v.block_partials, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.struct_bin_off,
-        v.struct_task_off, v.struct_ctask_off, L.cap_bins, v.status, fused_scan);
-    if (!fused_scan)
-        k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks, v.struct_ctasks,
-                                                nb, v.struct_bin_off, v.struct_task_off,
-                                                v.struct_ctask_off, v.recs, v.status, L.cap_bins);
+    const int64_t n_tiles =
+        (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) + L.n_tiles_pairs;
+    if (nb == 1 && n > 0) {
+        // one structure: set-up and atoms, then plan and binning, in two
+        // launches; k_single_bin writes the status words
+        k_atoms<T, true><<<blocks_for(n), kBlock, 0, stream>>>(
+            (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc, req->cutoff,
+            nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q,
+            v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
+        k_single_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(
+            (const T*)req->cell, n, req->cutoff, req->algorithm, reach, v.recs, v.block_partials,
+            (int64_t)blocks_for(n), (const Vec4<T>*)v.atom_q, v.atom_bin, v.atom_rank,
+            v.bin_count, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.struct_bin_off,
+            v.struct_task_off, v.struct_ctask_off, L.cap_bins, v.status);
+    } else {
+        // k_setup zeroes the status words; k_atoms zeroes the bin counters and
+        // the tile states of both single-pass scans.
+        k_setup<T><<<blocks_for(nb > 0 ? nb : 1, 64), 64, 0, stream>>>(
+            req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, v.recs, v.status);
+        if (n > 0)
+            k_atoms<T, false><<<blocks_for(n), kBlock, 0, stream>>>(
+                (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc,
+                req->cutoff, nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
+                (Vec4<T>*)v.atom_q, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
+        // a single structure is planned and scanned by one workgroup
+        const int fused_scan = nb <= 1 ? 1 : 0;
+        k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
+            (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
+            v.block_partials, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.struct_bin_off,
+            v.struct_task_off, v.struct_ctask_off, L.cap_bins, v.status, fused_scan);
+        if (!fused_scan)
+            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks,
+                                                    v.struct_ctasks, nb, v.struct_bin_off,
+                                                    v.struct_task_off, v.struct_ctask_off, v.recs,
+                                                    v.status, L.cap_bins);
+        if (n > 0 && req->algorithm != TNR_BRUTE_FORCE)
+            k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
+                                                           (const Vec4<T>*)v.atom_q, v.atom_bin,
+                                                           v.atom_rank, v.bin_count, v.status);
+    }
     if (n > 0 && req->algorithm != TNR_BRUTE_FORCE) {
-        k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
-                                                       (const Vec4<T>*)v.atom_q, v.atom_bin,
-                                                       v.atom_rank, v.bin_count, v.status);
         k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
             v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
             v.status + SS_TICKET_BINS, v.status, nullptr);
