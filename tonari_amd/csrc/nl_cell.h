@@ -126,6 +126,8 @@ struct CellBin {
     int C;            // flattened stencil candidates
     int nch;          // chunks of 64 candidates
     int npieces;
+    int dself;        // delta of the piece holding the bin itself with k = 0 (a source
+                      // s at binned index b is its own candidate b - dself)
     T c[9];           // cell (rows are cell vectors)
     T outer2, inner2, cut2;
     bool wrapped, diagonal;
@@ -319,6 +321,8 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     cb.C = uniform(total);
     cb.nch = (cb.C + kWave - 1) / kWave;
     __syncthreads();
+    // the bin itself with image 0: row (Kx, Ky), the z segment with kz = 0
+    cb.dself = st.delta[(G.Kx * G.RY + (G.RY >> 1)) * G.zs + (G.perz ? -G.kz0 : 0)];
     if (cb.C <= kMapCap) {
         // piece of candidate v: running maximum of the marks up to v, eight
         // candidates per thread
@@ -576,7 +580,8 @@ __device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const Stencil
                 const int p = st.piece[v];
                 const Vec4<T> rec = staged ? cand[v] : a.binned[v + st.delta[p]];
                 const int f = st.kfl[p];
-                cd.key[j] = identity_key<MODE>(as_idx(rec.w), (f & 1) != 0, (f & 2) != 0);
+                if constexpr (MODE >= 2)
+                    cd.key[j] = identity_key<MODE>(as_idx(rec.w), (f & 1) != 0, (f & 2) != 0);
                 cd.x[j] = O::add(rec.x, tr[0][p]);
                 cd.y[j] = O::add(rec.y, tr[1][p]);
                 cd.z[j] = O::add(rec.z, tr[2][p]);
@@ -621,7 +626,9 @@ __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLd
         const T dx = O::sub(cd.x[j], sx), dy = O::sub(cd.y[j], sy), dz = O::sub(cd.z[j], sz);
         const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
         unsigned long long mk = __builtin_amdgcn_ballot_w64(d2 < cb.outer2);
-        if constexpr (MODE != 1) mk &= __builtin_amdgcn_ballot_w64(identity_pass<MODE>(cd.key[j], si));
+        // the full list's only identity exclusion, the source itself with
+        // k = 0, is removed once per source afterwards (count_bin)
+        if constexpr (MODE >= 2) mk &= __builtin_amdgcn_ballot_w64(identity_pass<MODE>(cd.key[j], si));
         const unsigned long long mi = __builtin_amdgcn_ballot_w64(d2 < cb.inner2);
         const unsigned long long m = mk & mi;
         band |= (mk & ~mi) ? (1u << j) : 0u;
@@ -666,7 +673,19 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
                         sz = read_lane(sq.z, gi);
                 const int si = read_lane(sidx, gi);
                 unsigned long long mv;  // lane j: hit mask of chunk c0 + j
-                const int cnt = pass_masks<T, MODE, NC>(a, st, cb, cd, c0, sx, sy, sz, si, mv);
+                int cnt = pass_masks<T, MODE, NC>(a, st, cb, cd, c0, sx, sy, sz, si, mv);
+                if constexpr (MODE == 0) {
+                    // drop the source itself (candidate vs, at distance 0): lane
+                    // vs / nch of chunk vs % nch
+                    const int vs = sg + gi - cb.dself;
+                    const int ls = (int)(((float)vs + 0.5f) / (float)cb.nch);
+                    const int jc = vs - ls * cb.nch - c0;
+                    if (jc >= 0 && jc < NC) {
+                        const unsigned long long mj = (unsigned long long)read_lane((long long)mv, jc);
+                        cnt -= (int)((mj >> ls) & 1ull);
+                        if (lane == jc) mv &= ~(1ull << ls);
+                    }
+                }
                 if (cb.wrapped) {
                     for (int j = 0; j < NC && c0 + j < cb.nch; ++j) {
                         const unsigned long long m = (unsigned long long)read_lane((long long)mv, j);
