@@ -67,7 +67,7 @@ struct StageCap<double> {
 struct StencilLds {
     int pre[kPieceCap + 1];             // exclusive prefix of piece lengths
     int delta[kPieceCap];               // binned index = candidate index + delta
-    int kid[kPieceCap];                 // packed image shift (k + 512 per 10 bits)
+    int kid[kPieceCap];                 // packed image shift (pack_k)
     unsigned char kfl[kPieceCap];       // bit 0: k == 0, bit 1: k < 0 (lexicographic)
     unsigned char piece[kMapCap];       // piece of each candidate (when C <= kMapCap)
     int wtot[kWavesPerBlock];           // block scan: wave totals
@@ -88,13 +88,14 @@ struct EmitStageCap<double> {
     static constexpr int value = 768;
 };
 
+// Image shift k packed as three signed 10-bit fields (|k_a| <= 511).
 __device__ __forceinline__ int pack_k(int kx, int ky, int kz) {
-    return (kx + 512) | ((ky + 512) << 10) | ((kz + 512) << 20);
+    return (kx & 1023) | ((ky & 1023) << 10) | ((kz & 1023) << 20);
 }
 __device__ __forceinline__ void unpack_k(int v, int& kx, int& ky, int& kz) {
-    kx = (v & 1023) - 512;
-    ky = ((v >> 10) & 1023) - 512;
-    kz = ((v >> 20) & 1023) - 512;
+    kx = (int)__builtin_amdgcn_sbfe((unsigned)v, 0u, 10u);
+    ky = (int)__builtin_amdgcn_sbfe((unsigned)v, 10u, 10u);
+    kz = (int)__builtin_amdgcn_sbfe((unsigned)v, 20u, 10u);
 }
 
 // Candidate held by lane l of chunk j of a stencil with nch chunks: the
@@ -102,7 +103,9 @@ __device__ __forceinline__ void unpack_k(int v, int& kx, int& ky, int& kz) {
 // j + nch, j + 2 nch, ...), so every chunk samples all pieces alike and
 // the hits of a source spread evenly over its mask words.  Both passes map
 // mask bits to candidates through this function.
-__device__ __forceinline__ int chunk_cand(int j, int l, int nch) { return l * nch + j; }
+__device__ __forceinline__ int chunk_cand(int j, int l, int nch) {
+    return (int)__umul24((unsigned)l, (unsigned)nch) + j;
+}
 
 // Broad-phase translation k . cell of image k; every pass that needs it
 // evaluates this same expression, so the broad-phase decisions agree.
@@ -836,7 +839,7 @@ __device__ __forceinline__ int emit_group_size(int nsrc, int nch) {
 // evaluates D with the public formula's operation order.  Each source's output range
 // [offsets[s], offsets[s] + hits) is checked against E once; a source that
 // does not fit raises ST_OUTPUT_RANGE and writes nothing.
-template <typename T>
+template <typename T, bool OFF32>
 __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLds& st,
                                           const Vec4<T>* cand,
                                           const CellBin<T>& cb, unsigned short* list,
@@ -896,6 +899,7 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
             const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
             const int first = __shfl(pos, min(sl, S - 1) * nch);
             const long long ob = __shfl(cur, gi) - first;
+            const unsigned ob32 = (unsigned)ob;  // o = ob + list position (mod 2^32)
             const int tag = (gi << 6) | j;  // owner data: source lane, chunk
             for (int base = 0; base < total; base += kListCap) {
                 const int L = min(kListCap, total - base);
@@ -938,72 +942,92 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                     rec_ = cand[v];
                     unpack_k(st.kid[st.piece[v]], k_.x, k_.y, k_.z);
                 };
-                int w, tg;
-                Vec4<T> rec;
-                int4 k;
-                fetch(lane, w, tg, rec, k);
-                for (int r0 = 0; r0 < L; r0 += kWave) {
-                    int w_n, tg_n;
-                    Vec4<T> rec_n;
-                    int4 k_n;
-                    fetch(r0 + kWave + lane, w_n, tg_n, rec_n, k_n);
+                // pair r0 + lane of the list; byte offsets of output o in 32
+                // bits when OFF32 (every offset below 2^32)
+                auto put = [&](int r0, int w, int tg, const Vec4<T>& rec, const int4& k) {
                     const int g = tg >> 6;
-                    const long long o = __shfl(ob, w) + base + r0 + lane;
                     const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                     const int si = __shfl(sidx, g);
-                    if (r0 + lane < L) {
-                        const int t = as_idx(rec.w);
-                        if (a.pairs) {
-                            long2 v;
-                            v.x = si;
-                            v.y = t;
-                            *reinterpret_cast<long2*>(a.pairs + 2 * o) = v;
+                    long long o;
+                    if constexpr (OFF32)
+                        o = (long long)(unsigned)(__shfl(ob32, w) + (unsigned)(base + r0 + lane));
+                    else
+                        o = __shfl(ob, w) + base + r0 + lane;
+                    auto at = [&](auto* ptr, unsigned width) {
+                        using P = std::remove_pointer_t<decltype(ptr)>;
+                        // widths 12 and 24 by shifts (a full-rate add, not a
+                        // 32-bit multiply)
+                        const unsigned u = (unsigned)o;
+                        const unsigned off = width == 12u   ? (u << 3) + (u << 2)
+                                             : width == 24u ? (u << 4) + (u << 3)
+                                                            : u * width;
+                        if constexpr (OFF32)
+                            return reinterpret_cast<P*>(reinterpret_cast<char*>(ptr) + (size_t)off);
+                        else
+                            return reinterpret_cast<P*>(reinterpret_cast<char*>(ptr) +
+                                                        (size_t)o * width);
+                    };
+                    if (r0 + lane >= L) return;
+                    const int t = as_idx(rec.w);
+                    if (a.pairs) {
+                        long2 v;
+                        v.x = (long long)(unsigned)si;
+                        v.y = (long long)(unsigned)t;
+                        *reinterpret_cast<long2*>(at(a.pairs, 16u)) = v;
+                    }
+                    if (a.src) *at(a.src, 8u) = (long long)(unsigned)si;
+                    if (a.dst) *at(a.dst, 8u) = (long long)(unsigned)t;
+                    if (a.shifts) {
+                        Triple<int32_t> v;
+                        v.x = k.x;
+                        v.y = k.y;
+                        v.z = k.z;
+                        *reinterpret_cast<Triple<int32_t>*>(at(a.shifts, 12u)) = v;
+                    }
+                    if (want_vec) {
+                        // D = (p_t - p_s) + S0 c0 + S1 c1 + S2 c2, rounded in T
+                        // after every operation (public_vector)
+                        const T f0 = (T)k.x, f1 = (T)k.y, f2 = (T)k.z;
+                        T D0 = O::sub(rec.x, sx), D1 = O::sub(rec.y, sy), D2 = O::sub(rec.z, sz);
+                        if (cb.diagonal) {
+                            D0 = O::add(D0, O::mul(f0, cb.c[0]));
+                            D1 = O::add(D1, O::mul(f1, cb.c[4]));
+                            D2 = O::add(D2, O::mul(f2, cb.c[8]));
+                        } else {
+                            D0 = O::add(O::add(O::add(D0, O::mul(f0, cb.c[0])), O::mul(f1, cb.c[3])),
+                                        O::mul(f2, cb.c[6]));
+                            D1 = O::add(O::add(O::add(D1, O::mul(f0, cb.c[1])), O::mul(f1, cb.c[4])),
+                                        O::mul(f2, cb.c[7]));
+                            D2 = O::add(O::add(O::add(D2, O::mul(f0, cb.c[2])), O::mul(f1, cb.c[5])),
+                                        O::mul(f2, cb.c[8]));
                         }
-                        if (a.src) a.src[o] = si;
-                        if (a.dst) a.dst[o] = t;
-                        if (a.shifts) {
-                            Triple<int32_t> v;
-                            v.x = k.x;
-                            v.y = k.y;
-                            v.z = k.z;
-                            *reinterpret_cast<Triple<int32_t>*>(a.shifts + 3 * o) = v;
+                        if (a.vec) {
+                            Triple<T> v;
+                            v.x = D0;
+                            v.y = D1;
+                            v.z = D2;
+                            *reinterpret_cast<Triple<T>*>(at(a.vec, 3u * sizeof(T))) = v;
                         }
-                        if (want_vec) {
-                            // D = (p_t - p_s) + S0 c0 + S1 c1 + S2 c2, rounded in T
-                            // after every operation (public_vector)
-                            const T f0 = (T)k.x, f1 = (T)k.y, f2 = (T)k.z;
-                            T D0 = O::sub(rec.x, sx), D1 = O::sub(rec.y, sy), D2 = O::sub(rec.z, sz);
-                            if (cb.diagonal) {
-                                D0 = O::add(D0, O::mul(f0, cb.c[0]));
-                                D1 = O::add(D1, O::mul(f1, cb.c[4]));
-                                D2 = O::add(D2, O::mul(f2, cb.c[8]));
-                            } else {
-                                D0 = O::add(O::add(O::add(D0, O::mul(f0, cb.c[0])), O::mul(f1, cb.c[3])),
-                                            O::mul(f2, cb.c[6]));
-                                D1 = O::add(O::add(O::add(D1, O::mul(f0, cb.c[1])), O::mul(f1, cb.c[4])),
-                                            O::mul(f2, cb.c[7]));
-                                D2 = O::add(O::add(O::add(D2, O::mul(f0, cb.c[2])), O::mul(f1, cb.c[5])),
-                                            O::mul(f2, cb.c[8]));
-                            }
-                            if (a.vec) {
-                                Triple<T> v;
-                                v.x = D0;
-                                v.y = D1;
-                                v.z = D2;
-                                *reinterpret_cast<Triple<T>*>(a.vec + 3 * o) = v;
-                            }
-                            if (want_d) {
-                                T d2 = O::mul(D0, D0);
-                                d2 = O::add(d2, O::mul(D1, D1));
-                                d2 = O::add(d2, O::mul(D2, D2));
-                                a.dist[o] = O::sqrt_(d2);
-                            }
+                        if (want_d) {
+                            T d2 = O::mul(D0, D0);
+                            d2 = O::add(d2, O::mul(D1, D1));
+                            d2 = O::add(d2, O::mul(D2, D2));
+                            *at(a.dist, (unsigned)sizeof(T)) = O::sqrt_(d2);
                         }
                     }
-                    w = w_n;
-                    tg = tg_n;
-                    rec = rec_n;
-                    k = k_n;
+                };
+                // two register sets alternate: round r + 1's LDS reads are in
+                // flight while round r writes
+                int wA, tgA, wB, tgB;
+                Vec4<T> recA, recB;
+                int4 kA, kB;
+                fetch(lane, wA, tgA, recA, kA);
+                for (int r0 = 0; r0 < L; r0 += 2 * kWave) {
+                    fetch(r0 + kWave + lane, wB, tgB, recB, kB);
+                    put(r0, wA, tgA, recA, kA);
+                    if (r0 + kWave >= L) break;
+                    fetch(r0 + 2 * kWave + lane, wA, tgA, recA, kA);
+                    put(r0 + kWave, wB, tgB, recB, kB);
                 }
             }
         }
@@ -1140,7 +1164,11 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
         }
         stage_candidates<T, EmitStageCap<T>::value>(a, s_st, cb.C, s_cand);
         if (fast) {
-            emit_fast<T>(a, s_st, s_cand, cb, s_list[wv], src_all, cur_all, m0, m1);
+            // every output's byte offset below 2^32: 32-bit offsets
+            if (a.limit <= (int64_t)(0xffffffffll / 16))
+                emit_fast<T, true>(a, s_st, s_cand, cb, s_list[wv], src_all, cur_all, m0, m1);
+            else
+                emit_fast<T, false>(a, s_st, s_cand, cb, s_list[wv], src_all, cur_all, m0, m1);
         } else {
             wave_sources(cb);
             emit_bin<T, true, false>(a, s_st, s_cand, cb, s_list[wv]);
