@@ -834,8 +834,9 @@ __device__ __forceinline__ int emit_group_size(int nsrc, int nch) {
 
 // Emitting fast path: staged candidates, no wrapped representative (the
 // output shift is the image shift k and positions are the records).  The
-// same decode as emit_bin; a round reads only LDS (the list entry, the owner
-// lane's tag, the candidate record, its piece and the piece's shift) and
+// decode of emit_bin, except that a list entry holds the source's lane in
+// the group and the candidate index itself; a round reads only LDS (the
+// entry, the candidate record, its piece and the piece's shift) and
 // evaluates D with the public formula's operation order.  Each source's output range
 // [offsets[s], offsets[s] + hits) is checked against E once; a source that
 // does not fit raises ST_OUTPUT_RANGE and writes nothing.
@@ -898,9 +899,14 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
             const int pos = incl - c;  // list position of this lane's first hit
             const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
             const int first = __shfl(pos, min(sl, S - 1) * nch);
-            const long long ob = __shfl(cur, gi) - first;
+            // lane g: output base of the group's source g (its first output
+            // minus the list position of its first hit)
+            const long long ob = __shfl(__shfl(cur, gi) - first, min(lane, S - 1) * nch);
             const unsigned ob32 = (unsigned)ob;  // o = ob + list position (mod 2^32)
-            const int tag = (gi << 6) | j;  // owner data: source lane, chunk
+            // list entry: source lane g << 10 | candidate v (v < C <= 1024)
+            static_assert(EmitStageCap<float>::value <= 1024 && EmitStageCap<double>::value <= 1024,
+                          "candidate index in 10 bits");
+            const unsigned ebase = ((unsigned)gi << 10) + (unsigned)j;  // + bit * nch
             for (int base = 0; base < total; base += kListCap) {
                 const int L = min(kListCap, total - base);
                 __builtin_amdgcn_wave_barrier();
@@ -910,49 +916,46 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                     unsigned lo = (unsigned)m, hi = (unsigned)(m >> 32);
                     int r = pos;
                     while (lo) {
-                        const int bit = __builtin_ctz(lo);
+                        const unsigned bit = __builtin_ctz(lo);
                         lo &= lo - 1;
-                        list[r++] = (unsigned short)((lane << 6) | bit);
+                        list[r++] = (unsigned short)(ebase + __umul24(bit, (unsigned)nch));
                     }
                     while (hi) {
-                        const int bit = __builtin_ctz(hi) + 32;
+                        const unsigned bit = __builtin_ctz(hi) + 32;
                         hi &= hi - 1;
-                        list[r++] = (unsigned short)((lane << 6) | bit);
+                        list[r++] = (unsigned short)(ebase + __umul24(bit, (unsigned)nch));
                     }
                 } else {
                     unsigned long long mm = m;
                     int r = pos - base;
                     while (mm) {
-                        const int bit = __builtin_ctzll(mm);
+                        const unsigned bit = __builtin_ctzll(mm);
                         mm &= mm - 1;
-                        if (r >= 0 && r < L) list[r] = (unsigned short)((lane << 6) | bit);
+                        if (r >= 0 && r < L)
+                            list[r] = (unsigned short)(ebase + __umul24(bit, (unsigned)nch));
                         ++r;
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 // rounds of 64 entries; the next round's LDS reads are issued ahead
-                // entry e = owner lane w << 6 | bit; the owner lane holds the
-                // tag (source lane, chunk) and the output base of its word
-                auto fetch = [&](int r, int& w_, int& tg_, Vec4<T>& rec_, int4& k_) {
-                    const int e_ = list[min(r, L - 1)];
-                    w_ = e_ >> 6;
-                    tg_ = __shfl(tag, w_);
-                    const int v = chunk_cand(tg_ & 63, e_ & 63, nch);
+                auto fetch = [&](int r, int& g_, Vec4<T>& rec_, int4& k_) {
+                    const unsigned e_ = list[min(r, L - 1)];
+                    g_ = (int)(e_ >> 10);
+                    const int v = (int)(e_ & 1023u);
                     rec_ = cand[v];
                     unpack_k(st.kid[st.piece[v]], k_.x, k_.y, k_.z);
                 };
                 // pair r0 + lane of the list; byte offsets of output o in 32
                 // bits when OFF32 (every offset below 2^32)
-                auto put = [&](int r0, int w, int tg, const Vec4<T>& rec, const int4& k) {
-                    const int g = tg >> 6;
+                auto put = [&](int r0, int g, const Vec4<T>& rec, const int4& k) {
                     const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                     const int si = __shfl(sidx, g);
                     long long o;
                     if constexpr (OFF32)
-                        o = (long long)(unsigned)(__shfl(ob32, w) + (unsigned)(base + r0 + lane));
+                        o = (long long)(unsigned)(__shfl(ob32, g) + (unsigned)(base + r0 + lane));
                     else
-                        o = __shfl(ob, w) + base + r0 + lane;
+                        o = __shfl(ob, g) + base + r0 + lane;
                     auto at = [&](auto* ptr, unsigned width) {
                         using P = std::remove_pointer_t<decltype(ptr)>;
                         // widths 12 and 24 by shifts (a full-rate add, not a
@@ -1018,16 +1021,16 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                 };
                 // two register sets alternate: round r + 1's LDS reads are in
                 // flight while round r writes
-                int wA, tgA, wB, tgB;
+                int gA, gB;
                 Vec4<T> recA, recB;
                 int4 kA, kB;
-                fetch(lane, wA, tgA, recA, kA);
+                fetch(lane, gA, recA, kA);
                 for (int r0 = 0; r0 < L; r0 += 2 * kWave) {
-                    fetch(r0 + kWave + lane, wB, tgB, recB, kB);
-                    put(r0, wA, tgA, recA, kA);
+                    fetch(r0 + kWave + lane, gB, recB, kB);
+                    put(r0, gA, recA, kA);
                     if (r0 + kWave >= L) break;
-                    fetch(r0 + 2 * kWave + lane, wA, tgA, recA, kA);
-                    put(r0 + kWave, wB, tgB, recB, kB);
+                    fetch(r0 + 2 * kWave + lane, gA, recA, kA);
+                    put(r0 + kWave, gB, recB, kB);
                 }
             }
         }
