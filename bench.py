@@ -36,7 +36,6 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
-EMIT_BATCH = 8
 METRIC = "pairs/sec (M edges/s) + achieved HBM GB/s, 100k-atom box and batched crystals"
 
 
@@ -86,11 +85,11 @@ def time_public(cfg, t, steps: int, warmup: int):
 def time_phases(cfg, t, reps: int):
     """HIP-event durations of the count pipeline and of the emit kernel.
 
-    Drives the C ABI exactly as the frontend does, on torch's current stream,
-    recording events around tnr_count_async and around a batch of tnr_emit
-    calls.  For a cell-list workload tnr_emit launches one kernel (the
-    cell-list emit), so the second interval per call is that kernel's
-    duration.
+    Drives the C ABI as a repeated call of the frontend does, on torch's
+    current stream: events around tnr_count_async and around the tnr_emit
+    queued right behind it, one request per repetition.  For a cell-list
+    workload tnr_emit launches one kernel (the cell-list emit), so the second
+    interval is that kernel's duration in its place in the request.
     """
     import torch
 
@@ -116,41 +115,41 @@ def time_phases(cfg, t, reps: int):
     quantities = cfg["quantities"]
     n = ctypes.c_int64(0)
     outs = {}
+    o = None
     for rep in range(reps + 1):
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        # one request as the product runs it: the counting pipeline, then the
+        # emitting pass queued right behind it (no host wait in between; the
+        # inputs do not change, so E, the plan and the bins are the previous
+        # repetition's and are checked afterwards)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         ev[0].record()
         rc = lib.tnr_count_async(ctypes.byref(req), ws.data_ptr(), ws_bytes, host.data_ptr(),
                                  stream, err, len(err))
         ev[1].record()
+        if rc == 0 and o is not None:
+            rc = lib.tnr_emit(ctypes.byref(req), ws.data_ptr(), ws_bytes, ctypes.byref(o),
+                              stream, err, len(err))
+        ev[2].record()
         torch.cuda.synchronize()
         if rc != 0 or lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err)) != 0:
             raise RuntimeError(err.value.decode())
         E = int(n.value)
-        if not outs:
+        if o is None:  # the first repetition sizes the outputs and warms caches
             dt = pos.dtype
             shapes = {"P": ((E, 2), torch.int64), "S": ((E, 3), torch.int32),
                       "i": ((E,), torch.int64), "j": ((E,), torch.int64),
                       "d": ((E,), dt), "D": ((E, 3), dt)}
             outs = {q: torch.empty(shapes[q][0], dtype=shapes[q][1], device=dev)
                     for q in set(quantities)}
-        ptr = lambda q: outs[q].data_ptr() if q in outs else None  # noqa: E731
-        o = Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[7]), pairs=ptr("P"), shifts=ptr("S"),
-                    distances=ptr("d"), vectors=ptr("D"), sources=ptr("i"), targets=ptr("j"))
-        # EMIT_BATCH back-to-back launches keep the queue full, so the
-        # interval is kernel time rather than host submission latency.
-        ev[2].record()
-        for _ in range(EMIT_BATCH):
-            rc = lib.tnr_emit(ctypes.byref(req), ws.data_ptr(), ws_bytes, ctypes.byref(o),
-                              stream, err, len(err))
-            if rc != 0:
-                break
-        ev[3].record()
-        torch.cuda.synchronize()
-        if rc != 0:
-            raise RuntimeError(err.value.decode())
-        if rep > 0:  # the first repetition warms caches and code objects
-            count_ms.append(ev[0].elapsed_time(ev[1]))
-            emit_ms.append(ev[2].elapsed_time(ev[3]) / EMIT_BATCH)
+            ptr = lambda q: outs[q].data_ptr() if q in outs else None  # noqa: E731
+            o = Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[7]), pairs=ptr("P"),
+                        shifts=ptr("S"), distances=ptr("d"), vectors=ptr("D"),
+                        sources=ptr("i"), targets=ptr("j"))
+            continue
+        if (E, int(host[3]), int(host[7])) != (o.n_pairs, o.plan, o.n_tasks):
+            raise RuntimeError("the count changed between repetitions of the same input")
+        count_ms.append(ev[0].elapsed_time(ev[1]))
+        emit_ms.append(ev[1].elapsed_time(ev[2]))
     plan = int(host[3])
     del outs, ws
     return statistics.mean(count_ms), statistics.mean(emit_ms), E, plan

@@ -120,7 +120,10 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
 int tnr_count_finish(const int64_t* host_result, int64_t* n_pairs, char* err, size_t err_len);
 
 /* Writes every non-NULL output of `out` for the request last counted in
- * `workspace`; the pair order is source-major (sorted by source index). */
+ * `workspace`.  The pairs of one source are contiguous; with `sorted` the
+ * sources come in increasing index order, otherwise in an order of the
+ * library's choosing (the cell-list bin order when every structure of the
+ * request is searched with a cell list, index order otherwise). */
 int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
              const tnr_outputs* out, void* stream, char* err, size_t err_len);
 

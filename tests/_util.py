@@ -46,6 +46,18 @@ def assert_sorted_by_source(pairs) -> None:
     assert np.all(src[1:] >= src[:-1])
 
 
+def assert_grouped_by_source(pairs) -> None:
+    """The pairs of every source form one contiguous run."""
+    src = pairs[:, 0]
+    if hasattr(src, "detach"):
+        src = src.detach().cpu().numpy()
+    src = np.asarray(src)
+    if len(src) == 0:
+        return
+    runs = 1 + int(np.count_nonzero(src[1:] != src[:-1]))
+    assert runs == len(np.unique(src)), "pairs of a source are not contiguous"
+
+
 def oracle_call(cfg: dict, *, algorithm: str | None = None, threads: int = 8, kind: str = "port"):
     return oracle.neighbor_pairs(
         cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"],

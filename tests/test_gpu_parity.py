@@ -13,6 +13,7 @@ import torch
 
 from tests._util import (
     assert_geometry_close,
+    assert_grouped_by_source,
     assert_same_keys,
     assert_sorted_by_source,
     key_set,
@@ -331,11 +332,30 @@ def test_c4_small():
     P, S, D = gpu("PSD", cfg)
     assert_same_keys(keys_of(P, S), expected)
     assert_geometry_close(P, S, None, D, cfg)
-    # 'PD' (the benchmark's quantities) returns the same pairs; within-source
-    # order is unspecified, as in the reference.
+    # 'PD' (the benchmark's quantities) returns the same pairs; without
+    # `sorted` the order is unspecified, as in the reference.
     P2, D2 = gpu("PD", cfg)
-    assert torch.equal(P2[:, 0], P[:, 0])
+    n = len(cfg["positions"])
+    assert torch.equal(torch.sort(P2[:, 0] * n + P2[:, 1]).values,
+                       torch.sort(P[:, 0] * n + P[:, 1]).values)
     assert_geometry_close(P2, _shifts_for(P2, P, S), None, D2, cfg)
+
+
+def test_output_order_sorted_and_unsorted():
+    # sorted: sources in increasing index order; unsorted: the same pairs,
+    # every source's pairs contiguous (cell-list bin order for a cell-list
+    # batch, index order for a batch that also holds brute-force structures)
+    cfg = W.c4(n_atoms=20000)
+    P1, S1 = gpu("PS", cfg, sorted=True)
+    P0, S0 = gpu("PS", cfg, sorted=False)
+    assert_sorted_by_source(P1)
+    assert_grouped_by_source(P0)
+    assert_same_keys(keys_of(P0, S0), keys_of(P1, S1))
+    mixed = W.c2()
+    mixed["algorithm"] = "auto"
+    Pm, Sm = gpu("PS", mixed, sorted=False)
+    assert_grouped_by_source(Pm)
+    assert_same_keys(keys_of(Pm, Sm), keys_of(*gpu("PS", mixed, sorted=True)))
 
 
 def _shifts_for(pairs_new, pairs_old, shifts_old):
@@ -384,7 +404,10 @@ def test_full_size_matches_golden(name):
     P, S = gpu("PS", cfg)
     assert P.shape[0] == entry["pairs"]
     assert f"{multiset_hash_torch(P, S):016x}" == entry["multiset"]
-    assert_sorted_by_source(P)
+    if cfg.get("sorted", False):
+        assert_sorted_by_source(P)
+    else:
+        assert_grouped_by_source(P)
     if "sha256" in entry and entry["pairs"] <= 2_000_000:
         import oracle
 
