@@ -114,7 +114,7 @@ def time_phases(cfg, t, reps: int):
     count_ms, emit_ms = [], []
     quantities = cfg["quantities"]
     n = ctypes.c_int64(0)
-    outs = {}
+    outs = []
     o = None
     for rep in range(reps + 1):
         # one request as the product runs it: the counting pipeline, then the
@@ -127,8 +127,10 @@ def time_phases(cfg, t, reps: int):
                                  stream, err, len(err))
         ev[1].record()
         if rc == 0 and o is not None:
-            rc = lib.tnr_emit(ctypes.byref(req), ws.data_ptr(), ws_bytes, ctypes.byref(o),
-                              stream, err, len(err))
+            # two output sets in turn, as in the timed loop of the public call
+            # (the previous call's outputs are still held while the next runs)
+            rc = lib.tnr_emit(ctypes.byref(req), ws.data_ptr(), ws_bytes,
+                              ctypes.byref(o[rep % 2]), stream, err, len(err))
         ev[2].record()
         torch.cuda.synchronize()
         if rc != 0 or lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err)) != 0:
@@ -139,14 +141,17 @@ def time_phases(cfg, t, reps: int):
             shapes = {"P": ((E, 2), torch.int64), "S": ((E, 3), torch.int32),
                       "i": ((E,), torch.int64), "j": ((E,), torch.int64),
                       "d": ((E,), dt), "D": ((E, 3), dt)}
-            outs = {q: torch.empty(shapes[q][0], dtype=shapes[q][1], device=dev)
-                    for q in set(quantities)}
-            ptr = lambda q: outs[q].data_ptr() if q in outs else None  # noqa: E731
-            o = Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[7]), pairs=ptr("P"),
-                        shifts=ptr("S"), distances=ptr("d"), vectors=ptr("D"),
-                        sources=ptr("i"), targets=ptr("j"))
+            o = []
+            for _ in range(2):
+                out = {q: torch.empty(shapes[q][0], dtype=shapes[q][1], device=dev)
+                       for q in set(quantities)}
+                ptr = lambda q: out[q].data_ptr() if q in out else None  # noqa: E731
+                outs.append(out)
+                o.append(Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[7]),
+                                 pairs=ptr("P"), shifts=ptr("S"), distances=ptr("d"),
+                                 vectors=ptr("D"), sources=ptr("i"), targets=ptr("j")))
             continue
-        if (E, int(host[3]), int(host[7])) != (o.n_pairs, o.plan, o.n_tasks):
+        if (E, int(host[3]), int(host[7])) != (o[0].n_pairs, o[0].plan, o[0].n_tasks):
             raise RuntimeError("the count changed between repetitions of the same input")
         count_ms.append(ev[0].elapsed_time(ev[1]))
         emit_ms.append(ev[1].elapsed_time(ev[2]))

@@ -129,6 +129,7 @@ struct CellBin {
     int C;            // flattened stencil candidates
     int nch;          // chunks of 64 candidates
     int npieces;
+    bool by_bin;      // counts and offsets indexed by binned position (QueryArgs::by_bin)
     int dself;        // delta of the piece holding the bin itself with k = 0 (a source
                       // s at binned index b is its own candidate b - dself)
     T c[9];           // cell (rows are cell vectors)
@@ -277,6 +278,7 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     cb.cut2 = (T)r.cut2;
     cb.wrapped = r.any_wrap != 0;
     cb.diagonal = r.diagonal != 0;
+    cb.by_bin = a.by_bin && load_status(a.status + SS_PLAN) == 2ull;
     const BinGeom G = bin_geom(r, lbin);
     const int npieces = G.npieces;  // at most kPieceCap < kBlock
     cb.npieces = npieces;
@@ -521,7 +523,7 @@ __device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLd
             sidx = as_idx(sq.w);
         }
         long long acc = 0, cur = 0;
-        if (EMIT && lane < ns) cur = a.offsets[sidx];
+        if (EMIT && lane < ns) cur = a.offsets[cb.by_bin ? sg + lane : sidx];
         for (int j = 0; j < cb.nch; ++j) {
             const int v = j * kWave + lane;
             const bool valid = v < cb.C;
@@ -552,7 +554,7 @@ __device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLd
                 }
             }
         }
-        if (!EMIT && lane < ns) a.counts[sidx] = acc;
+        if (!EMIT && lane < ns) a.counts[cb.by_bin ? sg + lane : sidx] = acc;
     }
 }
 
@@ -703,7 +705,7 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
                 if (lane == gi) acc += cnt;
             }
         }
-        if (lane < ns) a.counts[sidx] = acc;
+        if (lane < ns) a.counts[cb.by_bin ? sg + lane : sidx] = acc;
     }
 }
 
@@ -751,7 +753,8 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
         const int ns = min(kWave, cb.se - sg);
         const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
         const int sidx = as_idx(sq.w);
-        const long long cur = lane < ns ? a.offsets[sidx] : 0;  // lane gi: first output of gi
+        // lane gi: first output of source gi
+        const long long cur = lane < ns ? a.offsets[cb.by_bin ? sg + lane : sidx] : 0;
         auto mask_of = [&](int s0_) -> unsigned long long {
             const int gi_ = s0_ + sl;
             return sl < S && gi_ < ns ? a.masks[(int64_t)(sg + gi_) * kMaskWords + j] : 0ull;
@@ -1155,7 +1158,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
         unsigned long long m0 = 0, m1 = 0;
         if (fast) {
             // offsets and the masks of the wave's first two groups load with the staging
-            cur_all = lane < nsrc ? a.offsets[as_idx(src_all.w)] : 0;
+            cur_all = lane < nsrc ? a.offsets[cb.by_bin ? cb.sb + lane : as_idx(src_all.w)] : 0;
             const int S = emit_group_size(nsrc, cb.nch);
             const int sl = (int)(((float)lane + 0.5f) / (float)cb.nch);
             const int j = lane - sl * cb.nch;

@@ -126,7 +126,7 @@ struct alignas(16) BlockPartial {
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
     size_t status, structs, struct_bins, struct_bin_off, struct_tasks, struct_task_off,
-        struct_ctasks, struct_ctask_off, atom_struct, atom_wrap, atom_q, perm,
+        struct_ctasks, struct_ctask_off, atom_struct, atom_wrap, atom_q,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials,
         block_partials, masks, tiles_bins, tiles_pairs, total;
     int64_t cap_bins, n_partials, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
@@ -169,7 +169,6 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.bin_count = take(sizeof(int32_t) * (size_t)(L.cap_bins + 1));
     L.bin_start = take(sizeof(int32_t) * (size_t)(L.cap_bins + 2));
     L.binned = take(tsize * 4 * (size_t)(n + 1));
-    L.perm = take(sizeof(int32_t) * (size_t)(n + 1));
     L.counts = take(sizeof(int64_t) * (size_t)(n + 1));
     L.offsets = take(sizeof(int64_t) * (size_t)(n + 2));
     L.partials = take(sizeof(int64_t) * (size_t)(L.n_partials + 1));

@@ -982,21 +982,18 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
 }
 
 // Counting sort, last step: atom i goes to binned position
-// bin_start[bin] + rank, and perm records the atom of every position.
+// bin_start[bin] + rank.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<T>* atom_q,
                                                      const int* atom_bin, const int* atom_rank,
                                                      const int* bin_start, Vec4<T>* binned,
-                                                     int* perm,
                                                      const unsigned long long* status) {
     if (load_status(status + SS_FLAGS) & kAbortBits) return;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_atoms) return;
     const int g = atom_bin[i];
     if (g < 0) return;
-    const int at = bin_start[g] + atom_rank[i];
-    binned[at] = atom_q[i];
-    perm[at] = (int)i;
+    binned[bin_start[g] + atom_rank[i]] = atom_q[i];
 }
 
 }  // namespace tnr

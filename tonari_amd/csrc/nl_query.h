@@ -30,6 +30,11 @@ struct QueryArgs {
     unsigned long long* masks;      // kMaskWords hit masks per binned cell-list source
     int64_t n_atoms;
     int64_t nb;
+    // without `sorted`: when every structure is searched with a cell list
+    // (status plan 2), pair counts and output offsets are indexed by binned
+    // position, so sources take the outputs in binned order and every
+    // emitting workgroup writes one contiguous range; otherwise by atom index
+    int by_bin;
     int64_t limit;  // E: emit never writes at or beyond it
     int64_t n_bins; // emit: cell-list bins covered by the grid (at least the batch's)
     // outputs (emit)

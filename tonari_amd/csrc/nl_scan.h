@@ -128,19 +128,13 @@ __device__ __forceinline__ unsigned long long tile_read(const unsigned long long
 // tile is bounded (kLookbackSpins polls); on expiry the block raises
 // ST_SCAN_STALL and finishes, so every wave exits.  `tiles` must hold zeros
 // and `ticket` zero.  When total_slot is given the total is also stored there.
-// When perm is given, every structure of the request is searched with a
-// cell list (status plan 2: every atom has a binned position) and no abort
-// bit is set (binning ran), item k of the scan is in[perm[k]] and its result
-// goes to out[perm[k]]: the scan runs in the binned order instead of the
-// index order.
 template <typename In, typename Out>
 __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t n,
                                                            const unsigned long long* n_dev,
                                                            Out* out, unsigned long long* tiles,
                                                            unsigned long long* ticket,
                                                            unsigned long long* status,
-                                                           unsigned long long* total_slot,
-                                                           const int* perm = nullptr) {
+                                                           unsigned long long* total_slot) {
     __shared__ long long s_tile, s_excl;
     if (threadIdx.x == 0) s_tile = (long long)atomicAdd(ticket, 1ull);
     __syncthreads();
@@ -149,27 +143,12 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     const int64_t ntiles = n > 0 ? (n + kScanTile - 1) / kScanTile : 1;
     if (tile >= ntiles) return;
     const int64_t base = tile * kScanTile + (int64_t)threadIdx.x * kScanItems;
-    // perm is complete only when binning ran: no abort bits (indices are
-    // clamped all the same, so no access leaves the arrays)
-    const bool permute = perm != nullptr && load_status(status + SS_PLAN) == 2ull &&
-                         !(load_status(status + SS_FLAGS) & kAbortBits);
-    int64_t at[kScanItems];
-#pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-        const int64_t i = base + k;
-        int64_t a = i;
-        if (permute && i < n) {
-            const int p = perm[i];
-            a = p >= 0 && (int64_t)p < n ? (int64_t)p : i;
-        }
-        at[k] = i < n ? a : 0;
-    }
     long long v[kScanItems];
     long long s = 0;
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
         const int64_t i = base + k;
-        v[k] = i < n ? (long long)in[at[k]] : 0;
+        v[k] = i < n ? (long long)in[i] : 0;
         s += v[k];
     }
     long long total;
@@ -212,7 +191,7 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
         const int64_t i = base + k;
-        if (i < n) out[at[k]] = (Out)run;
+        if (i < n) out[i] = (Out)run;
         run += v[k];
     }
     if (tile == ntiles - 1 && threadIdx.x == 0) {

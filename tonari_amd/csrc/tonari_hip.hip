@@ -70,7 +70,6 @@ struct Views {
     long long* partials;
     BlockPartial* block_partials;
     unsigned long long* masks;
-    int* perm;
     unsigned long long* tiles_bins;
     unsigned long long* tiles_pairs;
 };
@@ -99,7 +98,6 @@ static Views views(void* ws, const Layout& L) {
     v.partials = (long long*)(base + L.partials);
     v.block_partials = (BlockPartial*)(base + L.block_partials);
     v.masks = (unsigned long long*)(base + L.masks);
-    v.perm = (int*)(base + L.perm);
     v.tiles_bins = (unsigned long long*)(base + L.tiles_bins);
     v.tiles_pairs = (unsigned long long*)(base + L.tiles_pairs);
     return v;
@@ -175,6 +173,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.masks = v.masks;
     q.n_atoms = req->n_atoms;
     q.nb = req->n_structures;
+    q.by_bin = req->sorted ? 0 : 1;
     return q;
 }
 
@@ -263,19 +262,15 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_scatter<T><<<blocks_for(n), kBlock, 0, stream>>>(n, (const Vec4<T>*)v.atom_q,
                                                            v.atom_bin, v.atom_rank,
                                                            v.bin_start, (Vec4<T>*)v.binned,
-                                                           v.perm, v.status);
+                                                           v.status);
     }
     const QueryArgs<T> q = query_args<T>(req, v);
     dispatch_queries<T, false>(req, L, q, 0, 0, stream);
-    // pairs per source -> offsets; the total (E) goes to the status words.
-    // Without `sorted`, a batch searched entirely with cell lists takes its
-    // sources in binned order, so each emitting workgroup writes one
-    // contiguous range of the outputs; with `sorted`, in index order.
+    // pairs per source -> offsets; the total (E) goes to the status words
     k_scan_lookback<long long, long long>
         <<<(unsigned)((n + kScanTile - 1) / kScanTile > 0 ? (n + kScanTile - 1) / kScanTile : 1),
            kBlock, 0, stream>>>(v.counts, n, nullptr, v.offsets, v.tiles_pairs,
-                                v.status + SS_TICKET_PAIRS, v.status, v.status + SS_PAIRS,
-                                req->sorted ? nullptr : v.perm);
+                                v.status + SS_TICKET_PAIRS, v.status, v.status + SS_PAIRS);
     return hipGetLastError();
 }
 
