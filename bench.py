@@ -147,11 +147,11 @@ def time_phases(cfg, t, reps: int):
                        for q in set(quantities)}
                 ptr = lambda q: out[q].data_ptr() if q in out else None  # noqa: E731
                 outs.append(out)
-                o.append(Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[7]),
+                o.append(Outputs(n_pairs=E, plan=int(host[3]), n_tasks=int(host[4]),
                                  pairs=ptr("P"), shifts=ptr("S"), distances=ptr("d"),
                                  vectors=ptr("D"), sources=ptr("i"), targets=ptr("j")))
             continue
-        if (E, int(host[3]), int(host[7])) != (o[0].n_pairs, o[0].plan, o[0].n_tasks):
+        if (E, int(host[3]), int(host[4])) != (o[0].n_pairs, o[0].plan, o[0].n_tasks):
             raise RuntimeError("the count changed between repetitions of the same input")
         count_ms.append(ev[0].elapsed_time(ev[1]))
         emit_ms.append(ev[1].elapsed_time(ev[2]))

@@ -80,7 +80,7 @@ typedef struct tnr_request {
 typedef struct tnr_outputs {
     int64_t n_pairs;    /* E returned by tnr_count */
     int64_t plan;       /* host_result[3] of tnr_count (kernel families in use) */
-    int64_t n_tasks;    /* host_result[7] of tnr_count (cell-list tasks) */
+    int64_t n_tasks;    /* host_result[4] of tnr_count (cell-list bins of the batch) */
     int64_t* pairs;     /* P: int64[E][2] (source, target) */
     int32_t* shifts;    /* S: int32[E][3] */
     void* distances;    /* d: T[E] */

@@ -278,7 +278,7 @@ def neighbor_list_hip(
         if code != TNR_OK:
             _raise(code, err.value.decode())
         count = int(n_pairs.value)
-        plan, bins = int(host_view[3]), int(host_view[7])
+        plan, bins = int(host_view[3]), int(host_view[4])
         if guess is not None and want:
             fits = (
                 count <= capacity

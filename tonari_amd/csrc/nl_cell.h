@@ -1141,7 +1141,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
     // the batch's bins from the count's status words; the grid may cover
     // more (a launch sized before the count finished)
-    const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_TASKS);
+    const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_BINS);
     const ItemRange br = xcd_block_range(min(a.n_bins, bins));
     const int64_t g = br.first;
     if (g >= br.end) return;

@@ -60,8 +60,6 @@ enum StatusSlot : int {
     SS_TOTAL_BINS = 4,
     SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
-    SS_TOTAL_TASKS = 7,   // emitting cell-list tasks (bin parts) of the batch
-    SS_TOTAL_CTASKS = 8,  // counting cell-list tasks of the batch
     SS_SLOTS = 64,
 };
 
@@ -76,10 +74,6 @@ struct alignas(16) StructRec {
     int64_t nimages;
     int64_t bin0;
     int64_t nbins;
-    int64_t task0;       // first emitting task (bin part) of the structure
-    int64_t ctask0;      // first counting task of the structure
-    int32_t parts;       // emitting tasks per bin: waves that split a bin's sources
-    int32_t cparts;      // counting tasks per bin
     double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
     double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
     double lo[3];        // grid origin (inactive axes)
@@ -125,11 +119,10 @@ struct alignas(16) BlockPartial {
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
-    size_t status, structs, struct_bins, struct_bin_off, struct_tasks, struct_task_off,
-        struct_ctasks, struct_ctask_off, atom_struct, atom_wrap, atom_q,
-        atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets, partials,
+    size_t status, structs, struct_bins, struct_bin_off, atom_struct, atom_wrap, atom_q,
+        atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets,
         block_partials, masks, tiles_bins, tiles_pairs, total;
-    int64_t cap_bins, n_partials, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
+    int64_t cap_bins, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
 };
 
 // Hit masks stored per cell-list source: one 64-bit word per chunk of 64
@@ -145,8 +138,6 @@ inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     Layout L{};
     L.cap_bins = 2 * n + 64 * b + 64;
-    const int64_t longest = (L.cap_bins > n ? L.cap_bins : n) + 1;
-    L.n_partials = (longest + kScanChunk - 1) / kScanChunk + 1;
     size_t o = 0;
     auto take = [&](size_t bytes) {
         const size_t at = o;
@@ -157,10 +148,6 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.structs = take(sizeof(StructRec) * (size_t)(b > 0 ? b : 1));
     L.struct_bins = take(sizeof(int64_t) * (size_t)(b + 1));
     L.struct_bin_off = take(sizeof(int64_t) * (size_t)(b + 2));
-    L.struct_tasks = take(sizeof(int64_t) * (size_t)(b + 1));
-    L.struct_task_off = take(sizeof(int64_t) * (size_t)(b + 2));
-    L.struct_ctasks = take(sizeof(int64_t) * (size_t)(b + 1));
-    L.struct_ctask_off = take(sizeof(int64_t) * (size_t)(b + 2));
     L.atom_struct = take(sizeof(int32_t) * (size_t)(n + 1));
     L.atom_wrap = take(sizeof(int32_t) * 4 * (size_t)(n + 1));
     L.atom_q = take(tsize * 4 * (size_t)(n + 1));
@@ -171,7 +158,6 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.binned = take(tsize * 4 * (size_t)(n + 1));
     L.counts = take(sizeof(int64_t) * (size_t)(n + 1));
     L.offsets = take(sizeof(int64_t) * (size_t)(n + 2));
-    L.partials = take(sizeof(int64_t) * (size_t)(L.n_partials + 1));
     L.n_atom_blocks = (n + kBlock - 1) / kBlock;
     L.block_partials = take(sizeof(BlockPartial) * (size_t)(L.n_atom_blocks + 1));
     L.masks = take(sizeof(unsigned long long) * kMaskWords * (size_t)(n + 1));

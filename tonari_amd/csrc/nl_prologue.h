@@ -114,10 +114,6 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     r.natoms = natoms;
     r.bin0 = 0;
     r.nbins = 0;
-    r.task0 = 0;
-    r.ctask0 = 0;
-    r.parts = 1;
-    r.cparts = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         r.lo[a] = 0.0;
@@ -544,8 +540,7 @@ template <typename T>
 __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, StructRec& r,
                                                const unsigned long long red[kRedCount],
                                                double cutoff, int requested, int reach_target,
-                                               long long* struct_bins, long long* struct_tasks,
-                                               long long* struct_ctasks) {
+                                               long long* struct_bins) {
     using K = RedKeys<T>;
     const bool writer = lane_id() == 0;
     const int64_t n = r.natoms;
@@ -553,11 +548,7 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
         if (writer) {
             r.algo = ALGO_NONE;
             r.nbins = 0;
-            r.parts = 1;
-            r.cparts = 1;
             struct_bins[b] = 0;
-            struct_tasks[b] = 0;
-            struct_ctasks[b] = 0;
         }
         return;
     }
@@ -737,12 +728,7 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
     if (writer) {
         r.algo = algo;
         r.nbins = nbins;
-        // one workgroup per bin in both query passes
-        r.parts = 1;
-        r.cparts = 1;
         struct_bins[b] = nbins;
-        struct_tasks[b] = nbins;
-        struct_ctasks[b] = nbins;
         r.flags |= st;
     }
 }
@@ -756,9 +742,7 @@ template <typename T>
 __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int64_t n_atoms,
                                                   double cutoff, int requested, int reach_target,
                                                   StructRec* recs, const BlockPartial* partials,
-                                                  long long* struct_bins, long long* struct_tasks,
-                                                  long long* struct_ctasks, long long* bin_off,
-                                                  long long* task_off, long long* ctask_off,
+                                                  long long* struct_bins, long long* bin_off,
                                                   int64_t cap_bins, unsigned long long* status,
                                                   int fused_scan) {
     using K = RedKeys<T>;
@@ -769,11 +753,7 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
         StructRec& r = recs[b];
         const unsigned long long flags = r.flags;
         if ((flags & kAbortBits) || (load_status(status + SS_FLAGS) & kAbortBits)) {
-            if (tid == 0) {
-                struct_bins[b] = 0;
-                struct_tasks[b] = 0;
-                struct_ctasks[b] = 0;
-            }
+            if (tid == 0) struct_bins[b] = 0;
         } else {
             const int64_t n = r.natoms;
             unsigned long long v[kRedCount];
@@ -808,29 +788,23 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
                     for (int w = 1; w < kWavesPerBlock; ++w)
                         v[e] = s_red[w][e] > v[e] ? s_red[w][e] : v[e];
                 }
-                plan_structure<T>(cells, b, r, v, cutoff, requested, reach_target, struct_bins,
-                                  struct_tasks, struct_ctasks);
+                plan_structure<T>(cells, b, r, v, cutoff, requested, reach_target, struct_bins);
             }
         }
     }
     if (fused_scan) {
         __syncthreads();
-        struct_scan_block(struct_bins, struct_tasks, struct_ctasks, nb, bin_off, task_off,
-                          ctask_off, recs, status, cap_bins);
+        struct_scan_block(struct_bins, nb, bin_off, recs, status, cap_bins);
     }
 }
 
 // The batch-wide step of the planner (one workgroup, after k_plan).
 __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
-                                                         const long long* struct_tasks,
-                                                         const long long* struct_ctasks,
                                                          int64_t nb, long long* bin_off,
-                                                         long long* task_off,
-                                                         long long* ctask_off, StructRec* recs,
+                                                         StructRec* recs,
                                                          unsigned long long* status,
                                                          int64_t cap_bins) {
-    struct_scan_block(struct_bins, struct_tasks, struct_ctasks, nb, bin_off, task_off, ctask_off,
-                      recs, status, cap_bins);
+    struct_scan_block(struct_bins, nb, bin_off, recs, status, cap_bins);
 }
 
 template <typename T>
@@ -884,13 +858,12 @@ template <typename T>
 __global__ __launch_bounds__(kBlock) void k_single_bin(
     const T* cells, int64_t n_atoms, double cutoff, int requested, int reach_target,
     StructRec* recs, const BlockPartial* partials, int64_t n_partials, const Vec4<T>* atom_q,
-    int* atom_bin, int* atom_rank, int* bin_count, long long* struct_bins,
-    long long* struct_tasks, long long* struct_ctasks, long long* bin_off, long long* task_off,
-    long long* ctask_off, int64_t cap_bins, unsigned long long* status) {
+    int* atom_bin, int* atom_rank, int* bin_count, long long* struct_bins, long long* bin_off,
+    int64_t cap_bins, unsigned long long* status) {
     using K = RedKeys<T>;
     __shared__ StructRec s_rec;
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
-    __shared__ long long s_bins, s_tasks, s_ctasks;
+    __shared__ long long s_bins;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
     // the record (16-byte words) and this thread's partials in one round trip
     constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(int4));
@@ -938,31 +911,27 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
         const unsigned long long flags = r.flags | v[kRedCount];
         if (lane == 0) {
             r.flags = flags;
-            s_bins = s_tasks = s_ctasks = 0;
+            s_bins = 0;
             r.algo = ALGO_NONE;
         }
         if (!(flags & kAbortBits))
-            plan_structure<T>(cells, 0, r, v, cutoff, requested, reach_target, &s_bins, &s_tasks,
-                              &s_ctasks);
+            plan_structure<T>(cells, 0, r, v, cutoff, requested, reach_target, &s_bins);
     }
     __syncthreads();
     if (tid == 0) {
         StructRec& r = s_rec;
-        r.bin0 = r.task0 = r.ctask0 = 0;
+        r.bin0 = 0;
         if (blockIdx.x == 0) {
             recs[0] = r;
             struct_bins[0] = s_bins;
-            struct_tasks[0] = s_tasks;
-            struct_ctasks[0] = s_ctasks;
-            bin_off[0] = task_off[0] = ctask_off[0] = 0;
-            bin_off[1] = task_off[1] = ctask_off[1] = s_bins;
+            bin_off[0] = 0;
+            bin_off[1] = s_bins;
             for (int k = 0; k < SS_SLOTS; ++k) status[k] = 0;
             const unsigned long long images = (unsigned long long)r.img_total;
             unsigned long long st = r.flags;
             if (s_bins > cap_bins) st |= ST_CAPACITY;
             if (images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
-            status[SS_TOTAL_BINS] = status[SS_TOTAL_TASKS] = status[SS_TOTAL_CTASKS] =
-                (unsigned long long)s_bins;
+            status[SS_TOTAL_BINS] = (unsigned long long)s_bins;
             status[SS_PLAN] = r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
             status[SS_TOTAL_IMAGES] = images;
             status[SS_FLAGS] = st;

@@ -1,7 +1,6 @@
 // Device-wide exclusive scans: a single-pass scan with decoupled look-back
-// (k_scan_lookback), the one-block scan of the bins per structure
-// (struct_scan_block, run by the last workgroup of k_plan), the three-kernel scan (reduce, scan of block totals,
-// apply) and small fill kernels.
+// (k_scan_lookback) and the one-workgroup scan of the bins per structure
+// (struct_scan_block, run by k_plan or k_struct_scan).
 #pragma once
 
 #include "nl_math.h"
@@ -27,79 +26,6 @@ __device__ __forceinline__ long long block_exclusive_scan(long long x, long long
     __syncthreads();
     *total = all;
     return before + inc - x;
-}
-
-// ------------------------------------------------------------- fill / scan
-
-__global__ void k_fill_i64(long long* p, int64_t n, long long v) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = v;
-}
-
-__global__ void k_fill_i32(int* p, int64_t n, int v) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x)
-        p[i] = v;
-}
-
-template <typename In>
-__global__ __launch_bounds__(kBlock) void k_scan_reduce(const In* in, int64_t n,
-                                                         long long* partial) {
-    const int64_t base = (int64_t)blockIdx.x * kScanChunk;
-    long long s = 0;
-#pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
-        const int64_t i = base + threadIdx.x + (int64_t)j * kBlock;
-        if (i < n) s += (long long)in[i];
-    }
-    long long total;
-    block_exclusive_scan(s, &total);
-    if (threadIdx.x == 0) partial[blockIdx.x] = total;
-}
-
-// One block: exclusive scan of partial[0..np) in place, partial[np] = total.
-__global__ __launch_bounds__(kBlock) void k_scan_partials(long long* partial, int64_t np) {
-    __shared__ long long carry_s;
-    if (threadIdx.x == 0) carry_s = 0;
-    __syncthreads();
-    for (int64_t base = 0; base < np; base += kBlock) {
-        const int64_t i = base + threadIdx.x;
-        const long long v = i < np ? partial[i] : 0;
-        long long total;
-        const long long ex = block_exclusive_scan(v, &total);
-        const long long carry = carry_s;
-        if (i < np) partial[i] = carry + ex;
-        __syncthreads();
-        if (threadIdx.x == 0) carry_s = carry + total;
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) partial[np] = carry_s;
-}
-
-template <typename In, typename Out>
-__global__ __launch_bounds__(kBlock) void k_scan_apply(const In* in, int64_t n,
-                                                        const long long* partial,
-                                                        int64_t np, Out* out) {
-    const int64_t base = (int64_t)blockIdx.x * kScanChunk + (int64_t)threadIdx.x * kScanItems;
-    long long v[kScanItems];
-    long long s = 0;
-#pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
-        const int64_t i = base + j;
-        v[j] = i < n ? (long long)in[i] : 0;
-        s += v[j];
-    }
-    long long total;
-    long long run = block_exclusive_scan(s, &total) +
-                    (blockIdx.x < np ? partial[blockIdx.x] : 0);
-#pragma unroll
-    for (int j = 0; j < kScanItems; ++j) {
-        const int64_t i = base + j;
-        if (i < n) out[i] = (Out)run;
-        run += v[j];
-    }
-    if (blockIdx.x == 0 && threadIdx.x == 0) out[n] = (Out)partial[np];
 }
 
 // ------------------------------------------------------- single-pass scan
@@ -200,18 +126,13 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     }
 }
 
-// One workgroup: exclusive scans of the bins, the emitting tasks and the
-// counting tasks per structure into bin_off, task_off and ctask_off
-// ([0..nb]; each structure's first bin and tasks go to its record), their
-// totals, and the batch checks that need every structure's plan: total
-// periodic images and bin capacity.
-__device__ void struct_scan_block(const long long* struct_bins, const long long* struct_tasks,
-                                  const long long* struct_ctasks, int64_t nb, long long* bin_off,
-                                  long long* task_off, long long* ctask_off, StructRec* recs,
-                                  unsigned long long* status, int64_t cap_bins) {
-    // every bin is one task of both query passes: one scan fills the three offsets
-    (void)struct_tasks;
-    (void)struct_ctasks;
+// One workgroup: exclusive scan of the bins per structure into bin_off
+// ([0..nb]; each structure's first bin also goes to its record), the total,
+// and the batch checks that need every structure's plan: total periodic
+// images and bin capacity.
+__device__ void struct_scan_block(const long long* struct_bins, int64_t nb, long long* bin_off,
+                                  StructRec* recs, unsigned long long* status,
+                                  int64_t cap_bins) {
     __shared__ long long s_carry;
     __shared__ unsigned long long s_flags, s_plan, s_images;
     if (threadIdx.x == 0) {
@@ -245,11 +166,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
             const int64_t i = i0 + k;
             if (i < nb) {
                 bin_off[i] = run;
-                task_off[i] = run;
-                ctask_off[i] = run;
                 recs[i].bin0 = run;
-                recs[i].task0 = run;
-                recs[i].ctask0 = run;
             }
             run += v[k];
         }
@@ -263,10 +180,8 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
     __syncthreads();
     if (threadIdx.x == 0) {
         const long long total = s_carry;
-        bin_off[nb] = task_off[nb] = ctask_off[nb] = total;
+        bin_off[nb] = total;
         status[SS_TOTAL_BINS] = (unsigned long long)total;
-        status[SS_TOTAL_TASKS] = (unsigned long long)total;
-        status[SS_TOTAL_CTASKS] = (unsigned long long)total;
         status[SS_PLAN] = s_plan;
         status[SS_TOTAL_IMAGES] = s_images;
         unsigned long long st = s_flags;
@@ -274,17 +189,6 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         if (s_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
         if (st) atomicOr(status + SS_FLAGS, st);
     }
-}
-
-template <typename In, typename Out>
-static hipError_t device_scan(const In* in, int64_t n, Out* out, long long* partial,
-                              hipStream_t stream) {
-    const int64_t np = (n + kScanChunk - 1) / kScanChunk;
-    if (np > 0) k_scan_reduce<In><<<dim3((unsigned)np), dim3(kBlock), 0, stream>>>(in, n, partial);
-    k_scan_partials<<<1, kBlock, 0, stream>>>(partial, np);
-    k_scan_apply<In, Out><<<dim3((unsigned)(np > 0 ? np : 1)), dim3(kBlock), 0, stream>>>(
-        in, n, partial, np, out);
-    return hipGetLastError();
 }
 
 }  // namespace tnr

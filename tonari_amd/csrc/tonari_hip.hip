@@ -53,10 +53,6 @@ struct Views {
     StructRec* recs;
     long long* struct_bins;
     long long* struct_bin_off;
-    long long* struct_tasks;
-    long long* struct_task_off;
-    long long* struct_ctasks;
-    long long* struct_ctask_off;
     int* atom_struct;
     int4* atom_wrap;
     void* atom_q;
@@ -67,7 +63,6 @@ struct Views {
     void* binned;
     long long* counts;
     long long* offsets;
-    long long* partials;
     BlockPartial* block_partials;
     unsigned long long* masks;
     unsigned long long* tiles_bins;
@@ -81,10 +76,6 @@ static Views views(void* ws, const Layout& L) {
     v.recs = (StructRec*)(base + L.structs);
     v.struct_bins = (long long*)(base + L.struct_bins);
     v.struct_bin_off = (long long*)(base + L.struct_bin_off);
-    v.struct_tasks = (long long*)(base + L.struct_tasks);
-    v.struct_task_off = (long long*)(base + L.struct_task_off);
-    v.struct_ctasks = (long long*)(base + L.struct_ctasks);
-    v.struct_ctask_off = (long long*)(base + L.struct_ctask_off);
     v.atom_struct = (int*)(base + L.atom_struct);
     v.atom_wrap = (int4*)(base + L.atom_wrap);
     v.atom_q = base + L.atom_q;
@@ -95,7 +86,6 @@ static Views views(void* ws, const Layout& L) {
     v.binned = base + L.binned;
     v.counts = (long long*)(base + L.counts);
     v.offsets = (long long*)(base + L.offsets);
-    v.partials = (long long*)(base + L.partials);
     v.block_partials = (BlockPartial*)(base + L.block_partials);
     v.masks = (unsigned long long*)(base + L.masks);
     v.tiles_bins = (unsigned long long*)(base + L.tiles_bins);
@@ -179,7 +169,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
 
 // Counting: one persistent kernel covers both families (the plan is only
 // known on the device).  Emitting: plan bit 0 launches the brute-force
-// family, bit 1 the cell-list family over n_tasks tasks (bin parts).
+// family, bit 1 the cell-list family over n_tasks bins (one workgroup each).
 template <typename T, int MODE, bool EMIT>
 static void launch_queries(const tnr_request* req, const Layout& L, const QueryArgs<T>& q,
                            int64_t plan, int64_t n_tasks, hipStream_t stream) {
@@ -227,8 +217,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_single_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->cell, n, req->cutoff, req->algorithm, reach, v.recs, v.block_partials,
             (int64_t)blocks_for(n), (const Vec4<T>*)v.atom_q, v.atom_bin, v.atom_rank,
-            v.bin_count, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.struct_bin_off,
-            v.struct_task_off, v.struct_ctask_off, L.cap_bins, v.status);
+            v.bin_count, v.struct_bins, v.struct_bin_off, L.cap_bins, v.status);
     } else {
         // k_setup zeroes the status words; k_atoms zeroes the bin counters and
         // the tile states of both single-pass scans.
@@ -243,12 +232,9 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         const int fused_scan = nb <= 1 ? 1 : 0;
         k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
             (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
-            v.block_partials, v.struct_bins, v.struct_tasks, v.struct_ctasks, v.struct_bin_off,
-            v.struct_task_off, v.struct_ctask_off, L.cap_bins, v.status, fused_scan);
+            v.block_partials, v.struct_bins, v.struct_bin_off, L.cap_bins, v.status, fused_scan);
         if (!fused_scan)
-            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_tasks,
-                                                    v.struct_ctasks, nb, v.struct_bin_off,
-                                                    v.struct_task_off, v.struct_ctask_off, v.recs,
+            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, nb, v.struct_bin_off, v.recs,
                                                     v.status, L.cap_bins);
         if (n > 0 && req->algorithm != TNR_BRUTE_FORCE)
             k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
