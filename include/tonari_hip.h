@@ -48,7 +48,7 @@ extern "C" {
 #define TNR_DEVICE_ERROR 3
 
 /* Slots of host_result: status flags, E, total periodic images, plan mask,
- * total cell-list bins, two internal tickets, total cell-list tasks. */
+ * total cell-list bins, two internal tickets, one unused slot. */
 #define TNR_HOST_RESULT_SLOTS 8
 
 #define TNR_FLOAT32 0
@@ -72,8 +72,8 @@ typedef struct tnr_request {
     double cutoff;            /* strict, finite, positive */
     int32_t half_list;        /* 0 / 1 */
     int32_t include_self;     /* 0 / 1 */
-    int32_t sorted;           /* 0 / 1 (output is always source-major) */
-    int32_t stencil_reach;    /* cell-list bins per cutoff along each axis, 1-4; 0 = default (2) */
+    int32_t sorted;           /* 0 / 1: sources in index order (see tnr_emit) */
+    int32_t stencil_reach;    /* cell-list bins per cutoff along each axis, 1-4; 0 = chosen per structure */
 } tnr_request;
 
 /* Output buffers for tnr_emit; any pointer may be NULL (not requested). */
