@@ -1,6 +1,6 @@
 // Cell-list query kernels: the stencil walk over the bins of a structure in
-// a counting flavour (k_cell_count: pairs per source and hit masks; a
-// persistent grid that also counts the brute-force structures) and an
+// a counting flavour (k_cell_count: pairs per source and hit masks, in a
+// persistent grid) and an
 // emitting flavour (k_cell_emit: writes i/j/P/S/d/D at the scanned offsets).
 //
 // Work unit: one source bin per workgroup.  The four waves build the bin's
@@ -136,28 +136,6 @@ struct CellBin {
     T outer2, inner2, cut2;
     bool wrapped, diagonal;
 };
-
-// Structure of the last bin looked up by this workgroup: bins [lo, hi)
-// belong to structure b.  Consecutive bins usually share a structure.
-struct StructCache {
-    int b;
-    int64_t lo, hi;
-};
-
-__device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb, int64_t g,
-                                                 StructCache& sc) {
-    if (nb == 1) return 0;  // every bin belongs to the only structure
-    if (g >= sc.lo && g < sc.hi) return sc.b;
-    int64_t lo = 0, hi = nb;
-    while (hi - lo > 1) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (off[mid] <= g) lo = mid; else hi = mid;
-    }
-    sc.b = (int)lo;
-    sc.lo = off[lo];
-    sc.hi = off[lo + 1];
-    return sc.b;
-}
 
 // Geometry of the stencil of one bin, decoded from its structure record.
 struct BinGeom {
@@ -1066,10 +1044,9 @@ __device__ __forceinline__ ItemRange xcd_block_range(int64_t W) {
 
 // Counting pass, persistent grid: every workgroup walks its share of the
 // bins of the cell-list structures (one bin at a time, stencil built and
-// staged once, sources split over the four waves), then every wave its
-// share of the source atoms of the brute-force structures; writes counts[s]
-// for each source s.  The status word is read once: abort bits only come
-// from earlier kernels.
+// staged once, sources split over the four waves); writes counts[s] for each
+// source s of a cell-list structure.  The status word is read once: abort
+// bits only come from earlier kernels.
 template <typename T, int MODE>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void
 k_cell_count(
@@ -1107,15 +1084,6 @@ k_cell_count(
                 }
                 __syncthreads();  // the bin's LDS is free
             }
-        }
-    }
-    if (plan & 1) {
-        const int wv = uniform(threadIdx.x / kWave);
-        const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-        for (int64_t s = (int64_t)blockIdx.x * kWavesPerBlock + wv; s < a.n_atoms; s += nwaves) {
-            const int b = a.atom_struct[s];
-            const StructRec& r = a.recs[b];
-            if (r.algo == ALGO_BRUTE) brute_source<T, MODE, false>(a, (int)s, b, r);
         }
     }
 }

@@ -23,6 +23,10 @@ constexpr int kPieceCap = 192;            // stencil pieces per source bin
 constexpr double kBinOverhead = 6.0;
 constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
 constexpr int64_t kAutoBruteCandidates = 4096;     // N_b * images at or below: brute force
+// Brute force: a work unit takes about this many rounds of one image walk
+// per lane, a round costing 1 + images / 4 (most images fall outside the
+// cutoff sphere and are never visited).
+constexpr double kBruteUnitWork = 16.0;
 
 // Status bits.  Input errors map to ValueError, search errors to RuntimeError.
 enum StatusBit : unsigned long long {
@@ -60,6 +64,7 @@ enum StatusSlot : int {
     SS_TOTAL_BINS = 4,
     SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
+    SS_TOTAL_UNITS = 7,   // brute-force work units of the batch
     SS_SLOTS = 64,
 };
 
@@ -74,6 +79,7 @@ struct alignas(16) StructRec {
     int64_t nimages;
     int64_t bin0;
     int64_t nbins;
+    int64_t unit0;       // first brute-force work unit of the structure
     double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
     double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
     double lo[3];        // grid origin (inactive axes)
@@ -95,6 +101,7 @@ struct alignas(16) StructRec {
     int32_t algo;
     int32_t any_wrap;
     int32_t diagonal;    // every off-diagonal cell entry is zero
+    int32_t bgroup;      // brute force: sources per work unit
 };
 
 // The 14 per-structure reductions over atoms, all kept as maxima of
@@ -119,7 +126,8 @@ struct alignas(16) BlockPartial {
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
-    size_t status, structs, struct_bins, struct_bin_off, atom_struct, atom_wrap, atom_q,
+    size_t status, structs, struct_bins, struct_bin_off, struct_units, struct_unit_off,
+        atom_struct, atom_wrap, atom_q,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets,
         block_partials, masks, tiles_bins, tiles_pairs, total;
     int64_t cap_bins, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
@@ -148,6 +156,8 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.structs = take(sizeof(StructRec) * (size_t)(b > 0 ? b : 1));
     L.struct_bins = take(sizeof(int64_t) * (size_t)(b + 1));
     L.struct_bin_off = take(sizeof(int64_t) * (size_t)(b + 2));
+    L.struct_units = take(sizeof(int64_t) * (size_t)(b + 1));
+    L.struct_unit_off = take(sizeof(int64_t) * (size_t)(b + 2));
     L.atom_struct = take(sizeof(int32_t) * (size_t)(n + 1));
     L.atom_wrap = take(sizeof(int32_t) * 4 * (size_t)(n + 1));
     L.atom_q = take(tsize * 4 * (size_t)(n + 1));

@@ -112,6 +112,11 @@ __device__ __forceinline__ bool fits_i32(long long v) {
     return v >= -2147483648ll && v <= 2147483647ll;
 }
 
+// The same for an integer held exactly in a double.
+__device__ __forceinline__ bool fits_i32d(double v) {
+    return v >= -2147483648.0 && v <= 2147483647.0;
+}
+
 // ----------------------------------------------------------- wave reductions
 
 __device__ __forceinline__ long long wave_inclusive_scan(long long x) {

@@ -114,6 +114,8 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     r.natoms = natoms;
     r.bin0 = 0;
     r.nbins = 0;
+    r.unit0 = 0;
+    r.bgroup = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         r.lo[a] = 0.0;
@@ -540,7 +542,7 @@ template <typename T>
 __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, StructRec& r,
                                                const unsigned long long red[kRedCount],
                                                double cutoff, int requested, int reach_target,
-                                               long long* struct_bins) {
+                                               long long* struct_bins, long long* struct_units) {
     using K = RedKeys<T>;
     const bool writer = lane_id() == 0;
     const int64_t n = r.natoms;
@@ -549,6 +551,7 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
             r.algo = ALGO_NONE;
             r.nbins = 0;
             struct_bins[b] = 0;
+            struct_units[b] = 0;
         }
         return;
     }
@@ -729,6 +732,23 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
         r.algo = algo;
         r.nbins = nbins;
         struct_bins[b] = nbins;
+        // brute force: work units of bgroup consecutive sources
+        int64_t units = 0;
+        if (algo == ALGO_BRUTE) {
+            // a round: 64 / n sources of a structure of at most 32 atoms, or
+            // one source and its targets 64 at a time
+            const double round = 1.0 + 0.25 * (double)nimages;
+            const double rounds = fmax(floor(kBruteUnitWork / round), 1.0);
+            double g;
+            if (n <= 32)
+                g = (double)(kWave / n) * rounds;
+            else
+                g = fmax(floor(rounds / (double)((n + kWave - 1) / kWave)), 1.0);
+            g = fmin(g, (double)n);
+            r.bgroup = (int32_t)g;
+            units = (n + (int64_t)g - 1) / (int64_t)g;
+        }
+        struct_units[b] = units;
         r.flags |= st;
     }
 }
@@ -743,6 +763,7 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
                                                   double cutoff, int requested, int reach_target,
                                                   StructRec* recs, const BlockPartial* partials,
                                                   long long* struct_bins, long long* bin_off,
+                                                  long long* struct_units, long long* unit_off,
                                                   int64_t cap_bins, unsigned long long* status,
                                                   int fused_scan) {
     using K = RedKeys<T>;
@@ -753,7 +774,10 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
         StructRec& r = recs[b];
         const unsigned long long flags = r.flags;
         if ((flags & kAbortBits) || (load_status(status + SS_FLAGS) & kAbortBits)) {
-            if (tid == 0) struct_bins[b] = 0;
+            if (tid == 0) {
+                struct_bins[b] = 0;
+                struct_units[b] = 0;
+            }
         } else {
             const int64_t n = r.natoms;
             unsigned long long v[kRedCount];
@@ -788,23 +812,26 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
                     for (int w = 1; w < kWavesPerBlock; ++w)
                         v[e] = s_red[w][e] > v[e] ? s_red[w][e] : v[e];
                 }
-                plan_structure<T>(cells, b, r, v, cutoff, requested, reach_target, struct_bins);
+                plan_structure<T>(cells, b, r, v, cutoff, requested, reach_target, struct_bins,
+                                  struct_units);
             }
         }
     }
     if (fused_scan) {
         __syncthreads();
-        struct_scan_block(struct_bins, nb, bin_off, recs, status, cap_bins);
+        struct_scan_block(struct_bins, struct_units, nb, bin_off, unit_off, recs, status,
+                          cap_bins);
     }
 }
 
 // The batch-wide step of the planner (one workgroup, after k_plan).
 __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
+                                                         const long long* struct_units,
                                                          int64_t nb, long long* bin_off,
-                                                         StructRec* recs,
+                                                         long long* unit_off, StructRec* recs,
                                                          unsigned long long* status,
                                                          int64_t cap_bins) {
-    struct_scan_block(struct_bins, nb, bin_off, recs, status, cap_bins);
+    struct_scan_block(struct_bins, struct_units, nb, bin_off, unit_off, recs, status, cap_bins);
 }
 
 template <typename T>
@@ -859,11 +886,11 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
     const T* cells, int64_t n_atoms, double cutoff, int requested, int reach_target,
     StructRec* recs, const BlockPartial* partials, int64_t n_partials, const Vec4<T>* atom_q,
     int* atom_bin, int* atom_rank, int* bin_count, long long* struct_bins, long long* bin_off,
-    int64_t cap_bins, unsigned long long* status) {
+    long long* struct_units, long long* unit_off, int64_t cap_bins, unsigned long long* status) {
     using K = RedKeys<T>;
     __shared__ StructRec s_rec;
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
-    __shared__ long long s_bins;
+    __shared__ long long s_bins, s_units;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
     // the record (16-byte words) and this thread's partials in one round trip
     constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(int4));
@@ -912,26 +939,33 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
         if (lane == 0) {
             r.flags = flags;
             s_bins = 0;
+            s_units = 0;
             r.algo = ALGO_NONE;
         }
         if (!(flags & kAbortBits))
-            plan_structure<T>(cells, 0, r, v, cutoff, requested, reach_target, &s_bins);
+            plan_structure<T>(cells, 0, r, v, cutoff, requested, reach_target, &s_bins,
+                              &s_units);
     }
     __syncthreads();
     if (tid == 0) {
         StructRec& r = s_rec;
         r.bin0 = 0;
+        r.unit0 = 0;
         if (blockIdx.x == 0) {
             recs[0] = r;
             struct_bins[0] = s_bins;
             bin_off[0] = 0;
             bin_off[1] = s_bins;
+            struct_units[0] = s_units;
+            unit_off[0] = 0;
+            unit_off[1] = s_units;
             for (int k = 0; k < SS_SLOTS; ++k) status[k] = 0;
             const unsigned long long images = (unsigned long long)r.img_total;
             unsigned long long st = r.flags;
             if (s_bins > cap_bins) st |= ST_CAPACITY;
             if (images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
             status[SS_TOTAL_BINS] = (unsigned long long)s_bins;
+            status[SS_TOTAL_UNITS] = (unsigned long long)s_units;
             status[SS_PLAN] = r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
             status[SS_TOTAL_IMAGES] = images;
             status[SS_FLAGS] = st;

@@ -19,6 +19,7 @@ struct QueryArgs {
     const T* cells;
     const StructRec* recs;
     const int64_t* struct_bin_off;    // B + 1: first cell-list bin of each structure
+    const int64_t* struct_unit_off;   // B + 1: first brute-force work unit of each structure
     const int* atom_struct;
     const int4* atom_wrap;
     const Vec4<T>* atom_q;
@@ -132,109 +133,355 @@ __device__ __forceinline__ bool identity_pass(unsigned key, int s) {
     return true;
 }
 
-// -------------------------------------------------------------------- brute
+// Structure of the last item (cell-list bin or brute-force unit) looked up
+// by this workgroup: items [lo, hi) belong to structure b.  Consecutive items
+// usually share a structure.
+struct StructCache {
+    int b;
+    int64_t lo, hi;
+};
 
-// One source atom s of brute-force structure b, walked by one wave.  Lanes
-// hold 64 targets; the wave walks the image box of the structure in the
-// reference order (x-major, z fastest).  Counting writes counts[s]; emitting
-// writes the pairs of s from offsets[s] on.
-template <typename T, int MODE, bool EMIT>
-__device__ __forceinline__ void brute_source(const QueryArgs<T>& a, int s, int b,
-                                             const StructRec& r) {
-    using O = Ops<T>;
-    const int lane = lane_id();
-    {
-        const int a0 = (int)r.atom0;
-        const int a1 = (int)(r.atom0 + r.natoms);
-        const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
-        const T* cell = a.cells + 9 * b;
-        T c[9];
+__device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb, int64_t g,
+                                                 StructCache& sc) {
+    if (nb == 1) return 0;  // every item belongs to the only structure
+    if (g >= sc.lo && g < sc.hi) return sc.b;
+    int64_t lo = 0, hi = nb;
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (off[mid] <= g) lo = mid; else hi = mid;
+    }
+    sc.b = (int)lo;
+    sc.lo = off[lo];
+    sc.hi = off[lo + 1];
+    return sc.b;
+}
+
+// -------------------------------------------------------------------- brute
+//
+// Brute-force structures (neighbors_cuda.cu:89-279,443-556 and the brute path
+// of neighbors_cpu.cpp): every (source, target) pair of a structure with every
+// periodic image k of the box |k_a| <= R_a.  Here each lane takes one
+// (source, target) pair; the wave walks the rows (k0, k1) of the box, and
+// each lane visits only the k2 of a row whose translate can lie within the
+// padded cutoff (pair_images): a superset of the images the public predicate
+// can keep, widened far beyond its rounding and clipped to the reference's
+// box.  Every visited image is then decided as everywhere else: fused broad
+// phase, identity, and the public predicate in the band.  A wave takes one
+// work unit: bgroup consecutive sources of one structure (the planner sizes
+// units to similar work).
+
+// The integers k in [-R, R] within c - h .. c + h, each end widened by 1/256
+// plus 2^-16 of the magnitudes (the rounding of the float evaluations that
+// produce c and h is far smaller).  A NaN end keeps the box's end.
+template <typename T>
+__device__ __forceinline__ void axis_range(T c, T h, int R, int& lo, int& hi) {
+    const T slack = (T)(1.0 / 256.0) + (fabs(c) + h) * (T)(1.0 / 65536.0);
+    const T fr = (T)R;
+    lo = (int)fmin(fmax(ceil(c - h - slack), -fr), fr + (T)1);
+    hi = (int)fmax(fmin(floor(c + h + slack), fr), -fr - (T)1);
+}
+
+// The integers k in [-R, R] for which |p + k v|^2 < rho2 may hold: the
+// closest approach of the line p + x v lies at x = c = -(p.v)/|v|^2, at
+// distance |q| with q = p + c v, and |p + x v|^2 = |q|^2 + (x - c)^2 |v|^2.
+// rho2 is widened by 2^-20 |p|^2, which covers the cancellation in |q|.
+template <typename T>
+__device__ __forceinline__ void line_range(T px, T py, T pz, T vx, T vy, T vz, T inv_vv, T rho2,
+                                           int R, int& lo, int& hi) {
+    const T c = -(px * vx + py * vy + pz * vz) * inv_vv;
+    const T qx = px + c * vx, qy = py + c * vy, qz = pz + c * vz;
+    const T pp = px * px + py * py + pz * pz;
+    const T h2 = (rho2 + pp * (T)(1.0 / 1048576.0) - (qx * qx + qy * qy + qz * qz)) * inv_vv;
+    if (h2 < (T)0) {
+        lo = 1;
+        hi = 0;
+        return;
+    }
+    axis_range(c, sqrt(h2), R, lo, hi);
+}
+
+// Wave-uniform geometry of a brute-force structure.
+template <typename T>
+struct BruteGeom {
+    T c[9];  // cell rows
+    T inv2;  // 1/|c2|^2
+    T rho2, inner2, outer2, cut2;
+    int R0, R1, R2;
+    bool any_wrap, diagonal;
+};
+
+// The search radius rho2 is outer2 widened by 2^-8, so every image with a
+// broad-phase distance below outer2 is visited.
+template <typename T>
+__device__ __forceinline__ void brute_geom(const QueryArgs<T>& a, const StructRec& r, int b,
+                                           BruteGeom<T>& g) {
+    const T* cell = a.cells + 9 * b;
 #pragma unroll
-        for (int e = 0; e < 9; ++e) c[e] = cell[e];
-        const T inner2 = (T)r.inner2, outer2 = (T)r.outer2, cut2 = (T)r.cut2;
-        const bool any_wrap = r.any_wrap != 0;
-        const bool diagonal = r.diagonal != 0;
-        const Vec4<T> qs4 = a.atom_q[s];
-        const int4 ws = a.atom_wrap[s];
-        const T ps[3] = {a.pos[3 * s], a.pos[3 * s + 1], a.pos[3 * s + 2]};
-        long long total = 0;
-        long long cursor = EMIT ? a.offsets[s] : 0;
-        const int tstart = (MODE & 2) ? s : a0;
-        for (int tb = tstart; tb < a1; tb += kWave) {
-            const int t = tb + lane;
-            const bool vt = t < a1;
-            T bx = T(0), by = T(0), bz = T(0);
-            T pt[3] = {T(0), T(0), T(0)};
-            int4 wt = make_int4(0, 0, 0, 0);
-            if (vt) {
-                const Vec4<T> qt = a.atom_q[t];
-                bx = O::sub(qt.x, qs4.x);
-                by = O::sub(qt.y, qs4.y);
-                bz = O::sub(qt.z, qs4.z);
-                pt[0] = a.pos[3 * t];
-                pt[1] = a.pos[3 * t + 1];
-                pt[2] = a.pos[3 * t + 2];
-                wt = a.atom_wrap[t];
-            }
-            for (int i0 = -R0; i0 <= R0; ++i0) {
-                const T f0 = (T)i0;
-                for (int i1 = -R1; i1 <= R1; ++i1) {
-                    const T f1 = (T)i1;
-                    const T ex = O::fma_(f1, c[3], O::fma_(f0, c[0], bx));
-                    const T ey = O::fma_(f1, c[4], O::fma_(f0, c[1], by));
-                    const T ez = O::fma_(f1, c[5], O::fma_(f0, c[2], bz));
-                    for (int i2 = -R2; i2 <= R2; ++i2) {
-                        const T f2 = (T)i2;
-                        const T dx = O::fma_(f2, c[6], ex);
-                        const T dy = O::fma_(f2, c[7], ey);
-                        const T dz = O::fma_(f2, c[8], ez);
-                        const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
-                        const bool kzero = i0 == 0 && i1 == 0 && i2 == 0;
-                        const bool zs = t == s && kzero;
-                        bool ok = vt && (d2 < outer2 || zs) &&
-                                  identity_ok<MODE>(s, t, kzero, lex_negative(i0, i1, i2));
-                        const long long S0 = (long long)i0 - wt.x + ws.x;
-                        const long long S1 = (long long)i1 - wt.y + ws.y;
-                        const long long S2 = (long long)i2 - wt.z + ws.z;
-                        if (ok && !zs && !(d2 < inner2)) {
-                            T D[3];
-                            ok = public_vector(ps, pt, S0, S1, S2, c, D) < cut2;
-                        }
-                        const unsigned long long m = ballot(ok);
-                        if (m == 0) continue;
-                        if (!EMIT) {
-                            if (any_wrap && ok && !(fits_i32(S0) && fits_i32(S1) && fits_i32(S2)))
-                                atomicOr(a.status + SS_FLAGS, ST_SHIFT_RANGE);
-                            total += __popcll(m);
-                        } else {
-                            if (ok)
-                                write_hit(a, cursor + lanes_below(m), s, t, (int)S0, (int)S1,
-                                          (int)S2, ps, pt, c, diagonal);
-                            cursor += __popcll(m);
-                        }
+    for (int e = 0; e < 9; ++e) g.c[e] = cell[e];
+    g.R0 = r.reps[0];
+    g.R1 = r.reps[1];
+    g.R2 = r.reps[2];
+    g.inner2 = (T)r.inner2;
+    g.outer2 = (T)r.outer2;
+    g.cut2 = (T)r.cut2;
+    g.any_wrap = r.any_wrap != 0;
+    g.diagonal = r.diagonal != 0;
+    g.rho2 = g.outer2 * (T)(1.0 + 1.0 / 256.0);
+    g.inv2 = g.R2 > 0 ? (T)1 / (g.c[6] * g.c[6] + g.c[7] * g.c[7] + g.c[8] * g.c[8]) : T(0);
+}
+
+// Decision for image (k0, k1, k2) of the pair (s, t), whose broad-phase
+// displacement before the k2 term is (ex, ey, ez): broad phase, identity,
+// and the public predicate in the band.  dw = wrap_s - wrap_t in double
+// (exact), so the output shift k + dw is exact in double and rounds to T as
+// the integer itself would.
+template <typename T, int MODE>
+__device__ __forceinline__ bool image_decide(const BruteGeom<T>& g, int k0, int k1, int k2, T ex,
+                                             T ey, T ez, int s, int t, const double dw[3],
+                                             const T ps[3], const T pt[3]) {
+    using O = Ops<T>;
+    const T f2 = (T)k2;
+    const T dx = O::fma_(f2, g.c[6], ex);
+    const T dy = O::fma_(f2, g.c[7], ey);
+    const T dz = O::fma_(f2, g.c[8], ez);
+    const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
+    const bool kzero = k0 == 0 && k1 == 0 && k2 == 0;
+    const bool zs = t == s && kzero;
+    if (!((d2 < g.outer2 || zs) && identity_ok<MODE>(s, t, kzero, lex_negative(k0, k1, k2))))
+        return false;
+    if (zs || d2 < g.inner2) return true;
+    const T S0 = (T)((double)k0 + dw[0]), S1 = (T)((double)k1 + dw[1]),
+            S2 = (T)((double)k2 + dw[2]);
+    T D[3];
+    return public_vector(ps, pt, S0, S1, S2, g.c, D) < g.cut2;
+}
+
+// An atom's data for pair_images: wrapped position, wraps, position.
+template <typename T>
+struct WalkAtom {
+    Vec4<T> q;
+    int4 w;
+    T p[3];
+};
+
+template <typename T>
+__device__ __forceinline__ WalkAtom<T> walk_atom(const QueryArgs<T>& a, int i) {
+    WalkAtom<T> x;
+    x.q = a.atom_q[i];
+    x.w = a.atom_wrap[i];
+#pragma unroll
+    for (int e = 0; e < 3; ++e) x.p[e] = a.pos[3 * i + e];
+    return x;
+}
+
+// The atom held by lane l, for a wave-uniform l.
+template <typename T>
+__device__ __forceinline__ WalkAtom<T> lane_atom(const WalkAtom<T>& x, int l) {
+    WalkAtom<T> y;
+    y.q.x = read_lane(x.q.x, l);
+    y.q.y = read_lane(x.q.y, l);
+    y.q.z = read_lane(x.q.z, l);
+    y.q.w = read_lane(x.q.w, l);
+    y.w.x = read_lane(x.w.x, l);
+    y.w.y = read_lane(x.w.y, l);
+    y.w.z = read_lane(x.w.z, l);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) y.p[e] = read_lane(x.p[e], l);
+    return y;
+}
+
+// The atom held by lane l (l may differ between lanes).
+template <typename T>
+__device__ __forceinline__ WalkAtom<T> shfl_atom(const WalkAtom<T>& x, int l) {
+    WalkAtom<T> y;
+    y.q.x = __shfl(x.q.x, l);
+    y.q.y = __shfl(x.q.y, l);
+    y.q.z = __shfl(x.q.z, l);
+    y.q.w = __shfl(x.q.w, l);
+    y.w.x = __shfl(x.w.x, l);
+    y.w.y = __shfl(x.w.y, l);
+    y.w.z = __shfl(x.w.z, l);
+#pragma unroll
+    for (int e = 0; e < 3; ++e) y.p[e] = __shfl(x.p[e], l);
+    return y;
+}
+
+// The images of the lane's (source, target) pair, row by row: the rows
+// (k0, k1) of the box are walked by the whole wave in the reference order
+// (x-major), and each lane restricts k2 to the integers where |e + k2 c2|
+// can fall below the search radius (line_range; k2 = 0 when axis 2 is not
+// periodic), so only the images near the cutoff sphere are decided.
+//   PASS 0 (count): returns the kept pairs, raising the int32 shift-range
+//                   error where a kept shift does not fit.
+//   PASS 1 (write): writes the kept pairs.  Every lane runs every step of a
+//                   row (as long as the row's longest range); the hits of a
+//                   step are placed by ballot after the earlier hits of the
+//                   same source: `seg` marks the lanes of the lane's source,
+//                   and `cursor` (equal on those lanes) is the source's next
+//                   output position, advanced here.
+template <typename T, int MODE, int PASS>
+__device__ __forceinline__ int pair_images(const QueryArgs<T>& a, const BruteGeom<T>& g, bool valid,
+                                           int s, int t, const WalkAtom<T>& xs,
+                                           const WalkAtom<T>& xt, unsigned long long seg,
+                                           long long& cursor) {
+    using O = Ops<T>;
+    const T bx = O::sub(xt.q.x, xs.q.x), by = O::sub(xt.q.y, xs.q.y), bz = O::sub(xt.q.z, xs.q.z);
+    const double dw[3] = {(double)xs.w.x - (double)xt.w.x, (double)xs.w.y - (double)xt.w.y,
+                          (double)xs.w.z - (double)xt.w.z};
+    const unsigned long long below = (1ull << lane_id()) - 1ull;
+    int hits = 0;
+    for (int k0 = -g.R0; k0 <= g.R0; ++k0) {
+        const T f0 = (T)k0;
+        const T e0x = O::fma_(f0, g.c[0], bx), e0y = O::fma_(f0, g.c[1], by),
+                e0z = O::fma_(f0, g.c[2], bz);
+        for (int k1 = -g.R1; k1 <= g.R1; ++k1) {
+            const T f1 = (T)k1;
+            const T ex = O::fma_(f1, g.c[3], e0x), ey = O::fma_(f1, g.c[4], e0y),
+                    ez = O::fma_(f1, g.c[5], e0z);
+            int lo2 = 0, hi2 = 0;
+            if (g.R2 > 0)
+                line_range(ex, ey, ez, g.c[6], g.c[7], g.c[8], g.inv2, g.rho2, g.R2, lo2, hi2);
+            if (!valid) hi2 = lo2 - 1;
+            if (PASS == 0) {
+                for (int k2 = lo2; k2 <= hi2; ++k2) {
+                    if (image_decide<T, MODE>(g, k0, k1, k2, ex, ey, ez, s, t, dw, xs.p, xt.p)) {
+                        ++hits;
+                        if (g.any_wrap && !(fits_i32d((double)k0 + dw[0]) &&
+                                            fits_i32d((double)k1 + dw[1]) &&
+                                            fits_i32d((double)k2 + dw[2])))
+                            atomicOr(a.status + SS_FLAGS, ST_SHIFT_RANGE);
                     }
+                }
+            } else {
+                const int len = max(hi2 - lo2 + 1, 0);
+                const int steps = read_lane(wave_inclusive_max_i32(len), kWave - 1);
+                for (int j = 0; j < steps; ++j) {
+                    const int k2 = lo2 + j;
+                    const bool hit = j < len && image_decide<T, MODE>(g, k0, k1, k2, ex, ey, ez,
+                                                                      s, t, dw, xs.p, xt.p);
+                    const unsigned long long m = ballot(hit) & seg;
+                    if (hit)
+                        write_hit(a, cursor + __popcll(m & below), s, t,
+                                  shift_i32(k0, xt.w.x, xs.w.x), shift_i32(k1, xt.w.y, xs.w.y),
+                                  shift_i32(k2, xt.w.z, xs.w.z), xs.p, xt.p, g.c, g.diagonal);
+                    cursor += __popcll(m);
                 }
             }
         }
-        if (!EMIT && lane == 0) a.counts[s] = total;
+    }
+    return hits;
+}
+
+// Structure of brute-force unit u: the largest b with off[b] <= u, found by
+// the whole wave, 64 candidates per step (one load per lane).
+__device__ __forceinline__ int unit_structure(const int64_t* off, int64_t nb, int64_t u) {
+    const int lane = lane_id();
+    int64_t lo = 0, len = nb;
+    while (len > 1) {
+        const int64_t step = (len + kWave - 1) / kWave;
+        const int64_t at = (int64_t)lane * step;
+        const bool le = at < len && off[lo + at] <= u;
+        const unsigned long long m = ballot(le) | 1ull;
+        const int64_t last = 63 - __builtin_clzll(m);
+        lo += last * step;
+        len = min(step, len - last * step);
+    }
+    return (int)lo;
+}
+
+// Work unit u of the brute-force structures: sources [first, end) of one
+// structure (bgroup consecutive sources).  The wave holds the structure's
+// atoms in registers (up to 128: lane l holds atoms a0 + l and a0 + 64 + l)
+// and takes every source from them, so the rounds load nothing.  A structure
+// of at most 32 atoms packs P = 64 / n sources per round, lane l taking
+// source l / n and target l % n; a larger one takes one source per round and
+// its targets 64 at a time (beyond 128 atoms loaded per round).  Counting
+// stores each source's pair count in counts[s]; emitting writes each
+// source's pairs from offsets[s] on.
+template <typename T, int MODE, bool EMIT>
+__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u) {
+    const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+    const StructRec& r = a.recs[b];
+    BruteGeom<T> g;
+    brute_geom(a, r, b, g);
+    const int a0 = (int)r.atom0, n = (int)r.natoms, a1 = a0 + n;
+    const int first = a0 + (int)(u - r.unit0) * r.bgroup;
+    const int end = min(first + r.bgroup, a1);
+    const int lane = lane_id();
+    if (n <= 32) {
+        const int P = kWave / n;
+        const int j = lane / n, tl = lane - j * n;
+        const unsigned long long seg = ((1ull << n) - 1ull) << (j * n);
+        // lane l holds atom a0 + l % n: the lane's target, and atom a0 + l
+        // for l < n (every source)
+        const WalkAtom<T> xt = walk_atom(a, a0 + tl);
+        for (int s0 = first; s0 < end; s0 += P) {
+            const int s = s0 + j, t = a0 + tl;
+            const bool src = j < P && s < end;
+            const bool valid = src && (!(MODE & 2) || t >= s);
+            const WalkAtom<T> xs = shfl_atom(xt, src ? s - a0 : 0);
+            if constexpr (EMIT) {
+                long long cursor = src ? a.offsets[s] : 0;
+                pair_images<T, MODE, 1>(a, g, valid, s, t, xs, xt, seg, cursor);
+            } else {
+                long long unused = 0;
+                const int h = pair_images<T, MODE, 0>(a, g, valid, s, t, xs, xt, seg, unused);
+                // the source's total: its lanes [j n, j n + n) of the scan
+                const int incl = wave_inclusive_scan_i32(h);
+                const int last = __shfl(incl, min(j * n + n - 1, kWave - 1));
+                const int before = __shfl(incl, max(j * n - 1, 0));
+                if (src && tl == 0) a.counts[s] = last - (j > 0 ? before : 0);
+            }
+        }
+    } else {
+        const bool resident = n <= 2 * kWave;
+        WalkAtom<T> x0, x1;
+        if (resident) {
+            x0 = walk_atom(a, a0 + min(lane, n - 1));
+            x1 = walk_atom(a, a0 + min(kWave + lane, n - 1));
+        }
+        for (int s = first; s < end; ++s) {
+            const int t0 = (MODE & 2) ? s : a0;
+            long long cursor = EMIT ? a.offsets[s] : 0;
+            WalkAtom<T> xs;
+            if (resident)
+                xs = s - a0 < kWave ? lane_atom(x0, s - a0) : lane_atom(x1, s - a0 - kWave);
+            else
+                xs = walk_atom(a, s);
+            // target chunks [a0 + 64 c, a0 + 64 c + 64) that hold targets >= t0
+            for (int tb = a0 + ((t0 - a0) / kWave) * kWave; tb < a1; tb += kWave) {
+                const int t = tb + lane;
+                const bool valid = t >= t0 && t < a1;
+                WalkAtom<T> xt;
+                if (resident)
+                    xt = tb == a0 ? x0 : x1;
+                else
+                    xt = walk_atom(a, valid ? t : s);
+                if constexpr (EMIT) {
+                    pair_images<T, MODE, 1>(a, g, valid, s, t, xs, xt, ~0ull, cursor);
+                } else {
+                    long long unused = 0;
+                    const int h = pair_images<T, MODE, 0>(a, g, valid, s, t, xs, xt, ~0ull, unused);
+                    cursor += read_lane(wave_inclusive_scan_i32(h), kWave - 1);
+                }
+            }
+            if (!EMIT && lane == 0) a.counts[s] = cursor;
+        }
     }
 }
 
-// One wave per source atom of the brute-force structures (grid-stride).
+// Counting (EMIT false) or emitting pass of the brute-force structures: one
+// wave per work unit (grid-stride).  Exits at once when the request has no
+// brute-force structure.
 template <typename T, int MODE, bool EMIT>
 __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
     if ((load_status(a.status + SS_FLAGS) & kAbortBits) ||
         !(load_status(a.status + SS_PLAN) & 1))
         return;
+    const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
     const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + uniform(threadIdx.x / kWave);
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-    for (int64_t s64 = wave0; s64 < a.n_atoms; s64 += nwaves) {
-        const int s = (int)s64;
-        const int b = a.atom_struct[s];
-        const StructRec& r = a.recs[b];
-        if (r.algo != ALGO_BRUTE) continue;
-        brute_source<T, MODE, EMIT>(a, s, b, r);
-    }
+    for (int64_t u = wave0; u < units; u += nwaves) brute_unit<T, MODE, EMIT>(a, u);
 }
 
 }  // namespace tnr

@@ -126,17 +126,20 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     }
 }
 
-// One workgroup: exclusive scan of the bins per structure into bin_off
-// ([0..nb]; each structure's first bin also goes to its record), the total,
-// and the batch checks that need every structure's plan: total periodic
-// images and bin capacity.
-__device__ void struct_scan_block(const long long* struct_bins, int64_t nb, long long* bin_off,
+// One workgroup: exclusive scans of the bins and of the brute-force work
+// units per structure into bin_off and unit_off ([0..nb]; each structure's
+// first bin and unit also go to its record), their totals, and the batch
+// checks that need every structure's plan: total periodic images and bin
+// capacity.
+__device__ void struct_scan_block(const long long* struct_bins, const long long* struct_units,
+                                  int64_t nb, long long* bin_off, long long* unit_off,
                                   StructRec* recs, unsigned long long* status,
                                   int64_t cap_bins) {
-    __shared__ long long s_carry;
+    __shared__ long long s_carry, s_ucarry;
     __shared__ unsigned long long s_flags, s_plan, s_images;
     if (threadIdx.x == 0) {
         s_carry = 0;
+        s_ucarry = 0;
         s_flags = 0;
         s_plan = 0;
         s_images = 0;
@@ -145,13 +148,15 @@ __device__ void struct_scan_block(const long long* struct_bins, int64_t nb, long
     unsigned long long flags = 0, plan = 0, images = 0;
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
-        long long v[kScanItems];
-        long long sum = 0;
+        long long v[kScanItems], u[kScanItems];
+        long long sum = 0, usum = 0;
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
             const int64_t i = i0 + k;
             v[k] = i < nb ? struct_bins[i] : 0;
+            u[k] = i < nb ? struct_units[i] : 0;
             sum += v[k];
+            usum += u[k];
             if (i < nb) {
                 const StructRec& r = recs[i];
                 flags |= r.flags;
@@ -159,19 +164,26 @@ __device__ void struct_scan_block(const long long* struct_bins, int64_t nb, long
                 images += (unsigned long long)r.img_total;
             }
         }
-        long long tot;
+        long long tot, utot;
         long long run = block_exclusive_scan(sum, &tot) + s_carry;
+        long long urun = block_exclusive_scan(usum, &utot) + s_ucarry;
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
             const int64_t i = i0 + k;
             if (i < nb) {
                 bin_off[i] = run;
                 recs[i].bin0 = run;
+                unit_off[i] = urun;
+                recs[i].unit0 = urun;
             }
             run += v[k];
+            urun += u[k];
         }
         __syncthreads();
-        if (threadIdx.x == 0) s_carry += tot;
+        if (threadIdx.x == 0) {
+            s_carry += tot;
+            s_ucarry += utot;
+        }
         __syncthreads();
     }
     if (flags) atomicOr(&s_flags, flags);
@@ -181,7 +193,9 @@ __device__ void struct_scan_block(const long long* struct_bins, int64_t nb, long
     if (threadIdx.x == 0) {
         const long long total = s_carry;
         bin_off[nb] = total;
+        unit_off[nb] = s_ucarry;
         status[SS_TOTAL_BINS] = (unsigned long long)total;
+        status[SS_TOTAL_UNITS] = (unsigned long long)s_ucarry;
         status[SS_PLAN] = s_plan;
         status[SS_TOTAL_IMAGES] = s_images;
         unsigned long long st = s_flags;

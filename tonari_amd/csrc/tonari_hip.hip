@@ -53,6 +53,8 @@ struct Views {
     StructRec* recs;
     long long* struct_bins;
     long long* struct_bin_off;
+    long long* struct_units;
+    long long* struct_unit_off;
     int* atom_struct;
     int4* atom_wrap;
     void* atom_q;
@@ -76,6 +78,8 @@ static Views views(void* ws, const Layout& L) {
     v.recs = (StructRec*)(base + L.structs);
     v.struct_bins = (long long*)(base + L.struct_bins);
     v.struct_bin_off = (long long*)(base + L.struct_bin_off);
+    v.struct_units = (long long*)(base + L.struct_units);
+    v.struct_unit_off = (long long*)(base + L.struct_unit_off);
     v.atom_struct = (int*)(base + L.atom_struct);
     v.atom_wrap = (int4*)(base + L.atom_wrap);
     v.atom_q = base + L.atom_q;
@@ -98,21 +102,18 @@ static unsigned blocks_for(int64_t n, int per = kBlock) {
     return (unsigned)(b > 0 ? b : 1);
 }
 
-// Blocks of the persistent counting kernel: as many as the device holds at
-// once (occupancy x CUs), rounded down to a multiple of 8 so that every XCD
-// gets the same number, and no more than the work needs.  The occupancy is
-// looked up once per device and kernel instantiation and cached (the only
-// state the library keeps; it is idempotent and safe under concurrent use).
-template <typename T, int MODE>
-static int64_t count_resident_blocks() {
+// Workgroups a kernel keeps resident on the whole device (occupancy x
+// CUs).  Looked up once per device and kernel and cached (the only state the
+// library keeps; it is idempotent and safe under concurrent use).
+template <typename K>
+static int64_t resident_blocks(K kernel) {
     static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int v = cache[dev].load(std::memory_order_relaxed);
     if (v > 0) return v;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_cell_count<T, MODE>, kBlock, 0) !=
-            hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0) != hipSuccess ||
         per_cu <= 0)
         per_cu = 2;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -123,10 +124,13 @@ static int64_t count_resident_blocks() {
     return v;
 }
 
+// Blocks of the persistent counting kernel: as many as the device holds at
+// once, rounded down to a multiple of 8 so that every XCD gets the same
+// number, and no more than the work needs.
 template <typename T, int MODE>
 static unsigned count_blocks(int64_t work_waves) {
     const int64_t want = (work_waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = count_resident_blocks<T, MODE>() / 8 * 8;
+    const int64_t cap = resident_blocks(k_cell_count<T, MODE>) / 8 * 8;
     int64_t b = want < cap ? want : cap;
     b = (b + 7) / 8 * 8;
     return (unsigned)(b > 0 ? b : 8);
@@ -139,9 +143,14 @@ static unsigned emit_blocks(int64_t bins) {
     return (unsigned)(b > 0 ? b : 8);
 }
 
+// Workgroups of the brute-force kernels: one wave per work unit (a batch has
+// at most one unit per atom), no more than the device holds at once (the
+// waves stride over the units; surplus workgroups would only cost dispatch).
+template <typename T, int MODE, bool EMIT>
 static unsigned brute_blocks(int64_t n) {
     const int64_t want = (n + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t b = want < 8192 ? want : 8192;
+    const int64_t cap = resident_blocks(k_brute<T, MODE, EMIT>);
+    const int64_t b = want < cap ? want : cap;
     return (unsigned)(b > 0 ? b : 1);
 }
 
@@ -152,6 +161,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.cells = (const T*)req->cell;
     q.recs = v.recs;
     q.struct_bin_off = (const int64_t*)v.struct_bin_off;
+    q.struct_unit_off = (const int64_t*)v.struct_unit_off;
     q.atom_struct = v.atom_struct;
     q.atom_wrap = v.atom_wrap;
     q.atom_q = (const Vec4<T>*)v.atom_q;
@@ -167,9 +177,13 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     return q;
 }
 
-// Counting: one persistent kernel covers both families (the plan is only
-// known on the device).  Emitting: plan bit 0 launches the brute-force
-// family, bit 1 the cell-list family over n_tasks bins (one workgroup each).
+// Counting: the plan is only known on the device, so both families are
+// launched and each exits at once when the plan has none of its structures.
+// An explicit brute_force request skips the cell-list kernel.  An explicit
+// cell_list request uses brute force only for a structure whose bin grid
+// does not fit, so its brute-force kernel gets a small grid (grid-stride).  Emitting: plan bit 0 launches
+// the brute-force family, bit 1 the cell-list family over n_tasks bins (one
+// workgroup each).
 template <typename T, int MODE, bool EMIT>
 static void launch_queries(const tnr_request* req, const Layout& L, const QueryArgs<T>& q,
                            int64_t plan, int64_t n_tasks, hipStream_t stream) {
@@ -178,12 +192,16 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
     if constexpr (!EMIT) {
         (void)plan;
         (void)n_tasks;
-        k_cell_count<T, MODE><<<count_blocks<T, MODE>(2 * (L.cap_bins > n ? L.cap_bins : n)),
-                                kBlock, 0, stream>>>(q);
+        if (req->algorithm != TNR_BRUTE_FORCE)
+            k_cell_count<T, MODE><<<count_blocks<T, MODE>(2 * (L.cap_bins > n ? L.cap_bins : n)),
+                                    kBlock, 0, stream>>>(q);
+        k_brute<T, MODE, false>
+            <<<req->algorithm == TNR_CELL_LIST ? 8u : brute_blocks<T, MODE, false>(n), kBlock, 0,
+               stream>>>(q);
     } else {
         if ((plan & 2) && n_tasks > 0)
             k_cell_emit<T, MODE><<<emit_blocks(n_tasks), kBlock, 0, stream>>>(q);
-        if (plan & 1) k_brute<T, MODE, true><<<brute_blocks(n), kBlock, 0, stream>>>(q);
+        if (plan & 1) k_brute<T, MODE, true><<<brute_blocks<T, MODE, true>(n), kBlock, 0, stream>>>(q);
     }
 }
 
@@ -217,7 +235,8 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_single_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->cell, n, req->cutoff, req->algorithm, reach, v.recs, v.block_partials,
             (int64_t)blocks_for(n), (const Vec4<T>*)v.atom_q, v.atom_bin, v.atom_rank,
-            v.bin_count, v.struct_bins, v.struct_bin_off, L.cap_bins, v.status);
+            v.bin_count, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
+            L.cap_bins, v.status);
     } else {
         // k_setup zeroes the status words; k_atoms zeroes the bin counters and
         // the tile states of both single-pass scans.
@@ -232,9 +251,11 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         const int fused_scan = nb <= 1 ? 1 : 0;
         k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
             (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
-            v.block_partials, v.struct_bins, v.struct_bin_off, L.cap_bins, v.status, fused_scan);
+            v.block_partials, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
+            L.cap_bins, v.status, fused_scan);
         if (!fused_scan)
-            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, nb, v.struct_bin_off, v.recs,
+            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb,
+                                                    v.struct_bin_off, v.struct_unit_off, v.recs,
                                                     v.status, L.cap_bins);
         if (n > 0 && req->algorithm != TNR_BRUTE_FORCE)
             k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
