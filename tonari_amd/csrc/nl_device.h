@@ -27,6 +27,7 @@ constexpr int64_t kAutoBruteCandidates = 4096;     // N_b * images at or below: 
 // per lane, a round costing 1 + images / 4 (most images fall outside the
 // cutoff sphere and are never visited).
 constexpr double kBruteUnitWork = 16.0;
+constexpr int kBruteGroupCap = 256;  // sources per brute-force work unit (at most)
 
 // Status bits.  Input errors map to ValueError, search errors to RuntimeError.
 enum StatusBit : unsigned long long {

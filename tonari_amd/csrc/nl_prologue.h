@@ -735,16 +735,11 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
         // brute force: work units of bgroup consecutive sources
         int64_t units = 0;
         if (algo == ALGO_BRUTE) {
-            // a round: 64 / n sources of a structure of at most 32 atoms, or
-            // one source and its targets 64 at a time
+            // a round: 64 (source, target) pairs, costing about 1 + images / 4
             const double round = 1.0 + 0.25 * (double)nimages;
             const double rounds = fmax(floor(kBruteUnitWork / round), 1.0);
-            double g;
-            if (n <= 32)
-                g = (double)(kWave / n) * rounds;
-            else
-                g = fmax(floor(rounds / (double)((n + kWave - 1) / kWave)), 1.0);
-            g = fmin(g, (double)n);
+            double g = fmax(floor(rounds * (double)kWave / (double)n), 1.0);
+            g = fmin(fmin(g, (double)n), (double)kBruteGroupCap);
             r.bgroup = (int32_t)g;
             units = (n + (int64_t)g - 1) / (int64_t)g;
         }

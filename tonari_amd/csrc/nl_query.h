@@ -274,38 +274,6 @@ __device__ __forceinline__ WalkAtom<T> walk_atom(const QueryArgs<T>& a, int i) {
     return x;
 }
 
-// The atom held by lane l, for a wave-uniform l.
-template <typename T>
-__device__ __forceinline__ WalkAtom<T> lane_atom(const WalkAtom<T>& x, int l) {
-    WalkAtom<T> y;
-    y.q.x = read_lane(x.q.x, l);
-    y.q.y = read_lane(x.q.y, l);
-    y.q.z = read_lane(x.q.z, l);
-    y.q.w = read_lane(x.q.w, l);
-    y.w.x = read_lane(x.w.x, l);
-    y.w.y = read_lane(x.w.y, l);
-    y.w.z = read_lane(x.w.z, l);
-#pragma unroll
-    for (int e = 0; e < 3; ++e) y.p[e] = read_lane(x.p[e], l);
-    return y;
-}
-
-// The atom held by lane l (l may differ between lanes).
-template <typename T>
-__device__ __forceinline__ WalkAtom<T> shfl_atom(const WalkAtom<T>& x, int l) {
-    WalkAtom<T> y;
-    y.q.x = __shfl(x.q.x, l);
-    y.q.y = __shfl(x.q.y, l);
-    y.q.z = __shfl(x.q.z, l);
-    y.q.w = __shfl(x.q.w, l);
-    y.w.x = __shfl(x.w.x, l);
-    y.w.y = __shfl(x.w.y, l);
-    y.w.z = __shfl(x.w.z, l);
-#pragma unroll
-    for (int e = 0; e < 3; ++e) y.p[e] = __shfl(x.p[e], l);
-    return y;
-}
-
 // The images of the lane's (source, target) pair, row by row: the rows
 // (k0, k1) of the box are walked by the whole wave in the reference order
 // (x-major), and each lane restricts k2 to the integers where |e + k2 c2|
@@ -389,85 +357,135 @@ __device__ __forceinline__ int unit_structure(const int64_t* off, int64_t nb, in
     return (int)lo;
 }
 
-// Work unit u of the brute-force structures: sources [first, end) of one
-// structure (bgroup consecutive sources).  The wave holds the structure's
-// atoms in registers (up to 128: lane l holds atoms a0 + l and a0 + 64 + l)
-// and takes every source from them, so the rounds load nothing.  A structure
-// of at most 32 atoms packs P = 64 / n sources per round, lane l taking
-// source l / n and target l % n; a larger one takes one source per round and
-// its targets 64 at a time (beyond 128 atoms loaded per round).  Counting
-// stores each source's pair count in counts[s]; emitting writes each
-// source's pairs from offsets[s] on.
+// Atoms of a structure staged in LDS per wave (structures up to this size).
+constexpr int kBruteStage = 128;
+
+// Per-wave LDS of the brute-force kernels: the structure's atoms and, per
+// source of the unit, its pair count (counting) or next output (emitting).
+template <typename T>
+struct BruteLds {
+    Vec4<T> q[kBruteStage];
+    int4 w[kBruteStage];
+    Vec4<T> p[kBruteStage];
+    union {
+        int cnt[kBruteGroupCap];
+        long long cur[kBruteGroupCap];
+    };
+};
+
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+}
+
+// Pairs of the unit's sources before source x (0 <= x <= G) when the unit
+// starts at local source f of a structure of n atoms: x n for a full list;
+// for a half list (targets t >= s) sum_{k < x} (n - f - k).
+template <int MODE>
+__device__ __forceinline__ int64_t unit_pairs_before(int x, int n, int f) {
+    if constexpr ((MODE & 2) != 0) return (int64_t)x * (2 * (int64_t)(n - f) - x + 1) / 2;
+    return (int64_t)x * n;
+}
+
+// Source offset x of pair p within the unit: the largest x with
+// unit_pairs_before(x) <= p, from a double estimate (off by at most one)
+// corrected in integers.
+template <int MODE>
+__device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G) {
+    int x;
+    if constexpr ((MODE & 2) != 0) {
+        const double A = (double)(2 * (int64_t)(n - f) + 1);
+        x = (int)((A - sqrt(fmax(A * A - 8.0 * (double)p, 0.0))) * 0.5);
+    } else {
+        x = (int)(((double)p + 0.5) / (double)n);
+    }
+    x = min(max(x, 0), G - 1);
+    if (x + 1 < G && unit_pairs_before<MODE>(x + 1, n, f) <= p) ++x;
+    if (x > 0 && unit_pairs_before<MODE>(x, n, f) > p) --x;
+    return x;
+}
+
+// Work unit u of the brute-force structures: sources [first, first + G) of
+// one structure.  Their (source, target) pairs (targets t >= s for a half
+// list) are taken 64 per round in source order, lane l taking pair 64 r + l;
+// the atoms of a structure of up to kBruteStage atoms are staged in the
+// wave's LDS first.  Counting adds each lane's pairs to its source's count
+// (one LDS add per source run of the round) and stores counts[s] at the end;
+// emitting places a source's pairs from offsets[s] on, carrying its next
+// output position from round to round in LDS.
 template <typename T, int MODE, bool EMIT>
-__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u) {
+__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, BruteLds<T>& L) {
     const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
     const StructRec& r = a.recs[b];
     BruteGeom<T> g;
     brute_geom(a, r, b, g);
-    const int a0 = (int)r.atom0, n = (int)r.natoms, a1 = a0 + n;
-    const int first = a0 + (int)(u - r.unit0) * r.bgroup;
-    const int end = min(first + r.bgroup, a1);
+    const int a0 = (int)r.atom0, n = (int)r.natoms;
+    const int f = (int)(u - r.unit0) * r.bgroup;
+    const int G = min(r.bgroup, n - f);
     const int lane = lane_id();
-    if (n <= 32) {
-        const int P = kWave / n;
-        const int j = lane / n, tl = lane - j * n;
-        const unsigned long long seg = ((1ull << n) - 1ull) << (j * n);
-        // lane l holds atom a0 + l % n: the lane's target, and atom a0 + l
-        // for l < n (every source)
-        const WalkAtom<T> xt = walk_atom(a, a0 + tl);
-        for (int s0 = first; s0 < end; s0 += P) {
-            const int s = s0 + j, t = a0 + tl;
-            const bool src = j < P && s < end;
-            const bool valid = src && (!(MODE & 2) || t >= s);
-            const WalkAtom<T> xs = shfl_atom(xt, src ? s - a0 : 0);
-            if constexpr (EMIT) {
-                long long cursor = src ? a.offsets[s] : 0;
-                pair_images<T, MODE, 1>(a, g, valid, s, t, xs, xt, seg, cursor);
-            } else {
-                long long unused = 0;
-                const int h = pair_images<T, MODE, 0>(a, g, valid, s, t, xs, xt, seg, unused);
-                // the source's total: its lanes [j n, j n + n) of the scan
-                const int incl = wave_inclusive_scan_i32(h);
-                const int last = __shfl(incl, min(j * n + n - 1, kWave - 1));
-                const int before = __shfl(incl, max(j * n - 1, 0));
-                if (src && tl == 0) a.counts[s] = last - (j > 0 ? before : 0);
-            }
-        }
-    } else {
-        const bool resident = n <= 2 * kWave;
-        WalkAtom<T> x0, x1;
-        if (resident) {
-            x0 = walk_atom(a, a0 + min(lane, n - 1));
-            x1 = walk_atom(a, a0 + min(kWave + lane, n - 1));
-        }
-        for (int s = first; s < end; ++s) {
-            const int t0 = (MODE & 2) ? s : a0;
-            long long cursor = EMIT ? a.offsets[s] : 0;
-            WalkAtom<T> xs;
-            if (resident)
-                xs = s - a0 < kWave ? lane_atom(x0, s - a0) : lane_atom(x1, s - a0 - kWave);
-            else
-                xs = walk_atom(a, s);
-            // target chunks [a0 + 64 c, a0 + 64 c + 64) that hold targets >= t0
-            for (int tb = a0 + ((t0 - a0) / kWave) * kWave; tb < a1; tb += kWave) {
-                const int t = tb + lane;
-                const bool valid = t >= t0 && t < a1;
-                WalkAtom<T> xt;
-                if (resident)
-                    xt = tb == a0 ? x0 : x1;
-                else
-                    xt = walk_atom(a, valid ? t : s);
-                if constexpr (EMIT) {
-                    pair_images<T, MODE, 1>(a, g, valid, s, t, xs, xt, ~0ull, cursor);
-                } else {
-                    long long unused = 0;
-                    const int h = pair_images<T, MODE, 0>(a, g, valid, s, t, xs, xt, ~0ull, unused);
-                    cursor += read_lane(wave_inclusive_scan_i32(h), kWave - 1);
-                }
-            }
-            if (!EMIT && lane == 0) a.counts[s] = cursor;
+    const bool staged = n <= kBruteStage;
+    if (staged) {
+        for (int i = lane; i < n; i += kWave) {
+            const WalkAtom<T> x = walk_atom(a, a0 + i);
+            L.q[i] = x.q;
+            L.w[i] = x.w;
+            L.p[i] = Vec4<T>{x.p[0], x.p[1], x.p[2], T(0)};
         }
     }
+    for (int x = lane; x < G; x += kWave) {
+        if (EMIT)
+            L.cur[x] = a.offsets[a0 + f + x];
+        else
+            L.cnt[x] = 0;
+    }
+    wave_lds_fence();
+    auto atom = [&](int i) {
+        WalkAtom<T> x;
+        if (staged) {
+            x.q = L.q[i];
+            x.w = L.w[i];
+            const Vec4<T> p = L.p[i];
+            x.p[0] = p.x;
+            x.p[1] = p.y;
+            x.p[2] = p.z;
+        } else {
+            x = walk_atom(a, a0 + i);
+        }
+        return x;
+    };
+    const int64_t total = unit_pairs_before<MODE>(G, n, f);
+    for (int64_t base = 0; base < total; base += kWave) {
+        const int64_t p = base + lane;
+        const bool valid = p < total;
+        const int64_t pc = min(p, total - 1);
+        const int x = unit_source_of<MODE>(pc, n, f, G);
+        const int64_t q0 = unit_pairs_before<MODE>(x, n, f);
+        const int li = f + x;
+        const int tl = ((MODE & 2) ? li : 0) + (int)(pc - q0);
+        // lanes of this round that hold pairs of the same source
+        const int seg_lo = (int)max(q0 - base, (int64_t)0);
+        const int seg_hi = (int)min(unit_pairs_before<MODE>(x + 1, n, f) - base, (int64_t)kWave);
+        const unsigned long long seg =
+            (seg_hi >= kWave ? ~0ull : ((1ull << seg_hi) - 1ull)) & ~((1ull << seg_lo) - 1ull);
+        const WalkAtom<T> xs = atom(li), xt = atom(tl);
+        if constexpr (EMIT) {
+            long long cursor = L.cur[x];
+            pair_images<T, MODE, 1>(a, g, valid, a0 + li, a0 + tl, xs, xt, seg, cursor);
+            wave_lds_fence();
+            if (valid && lane == seg_hi - 1) L.cur[x] = cursor;
+        } else {
+            long long unused = 0;
+            const int h = pair_images<T, MODE, 0>(a, g, valid, a0 + li, a0 + tl, xs, xt, seg,
+                                                  unused);
+            const int incl = wave_inclusive_scan_i32(h);
+            const int before = __shfl(incl, max(seg_lo - 1, 0));
+            if (valid && lane == seg_hi - 1) L.cnt[x] += incl - (seg_lo > 0 ? before : 0);
+        }
+        wave_lds_fence();
+    }
+    if (!EMIT)
+        for (int x = lane; x < G; x += kWave) a.counts[a0 + f + x] = L.cnt[x];
+    wave_lds_fence();
 }
 
 // Counting (EMIT false) or emitting pass of the brute-force structures: one
@@ -478,10 +496,12 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
     if ((load_status(a.status + SS_FLAGS) & kAbortBits) ||
         !(load_status(a.status + SS_PLAN) & 1))
         return;
+    __shared__ BruteLds<T> s_lds[kWavesPerBlock];
     const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
-    const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + uniform(threadIdx.x / kWave);
+    const int wv = uniform(threadIdx.x / kWave);
+    const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-    for (int64_t u = wave0; u < units; u += nwaves) brute_unit<T, MODE, EMIT>(a, u);
+    for (int64_t u = wave0; u < units; u += nwaves) brute_unit<T, MODE, EMIT>(a, u, s_lds[wv]);
 }
 
 }  // namespace tnr
