@@ -240,6 +240,9 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=20, help="event-timed repetitions")
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "reference", "port", "off"])
     ap.add_argument("--secondary", default="C2,C3,C5", help="comma list, or 'none'")
+    ap.add_argument("--secondary-only", action="store_true",
+                    help="time only the --secondary configurations (one JSON object per line; "
+                         "for profiling them) instead of the benchmark line")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -273,6 +276,13 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy calibration: {nbytes} bytes read and written per copy")
         del src, dst
+
+    if args.secondary_only:
+        for name in [s for s in args.secondary.split(",") if s and s != "none"]:
+            log(f"{name}: timing")
+            res = measure(name, W.CONFIGS[name](), args.steps, args.warmup, args.reps, dev)
+            print(json.dumps({"config": name, **res}), flush=True)
+        return 0
 
     cfg = W.c4()
     log("C4: timing")
