@@ -67,6 +67,7 @@ enum StatusSlot : int {
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
     SS_TOTAL_UNITS = 7,   // brute-force work units of the batch
     SS_SLOTS = 64,
+    kHostResultSlots = 8,  // status words copied to the caller's host buffer
 };
 
 enum Algo : int { ALGO_NONE = 0, ALGO_BRUTE = 1, ALGO_CELL = 2 };

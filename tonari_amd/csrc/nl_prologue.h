@@ -703,6 +703,10 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
             }
         }
         best = __builtin_amdgcn_readfirstlane(best);
+        // an explicit cell_list request is never served by brute force: a
+        // structure no bin grid fits (only beyond about 2^24 atoms) is a
+        // capacity error
+        if (!(cost < INFINITY) && requested == TNR_CELL_LIST) st |= ST_CAPACITY;
         if (cost < INFINITY) {
             algo = ALGO_CELL;
             nbins = (int64_t)__shfl(bins_f, best);

@@ -53,14 +53,19 @@ __device__ __forceinline__ unsigned long long tile_read(const unsigned long long
 // nearest inclusive prefix (decoupled look-back).  The wait on an earlier
 // tile is bounded (kLookbackSpins polls); on expiry the block raises
 // ST_SCAN_STALL and finishes, so every wave exits.  `tiles` must hold zeros
-// and `ticket` zero.  When total_slot is given the total is also stored there.
+// and `ticket` zero.  When total_slot is given the total is also stored there,
+// and when host_out is given the block of the last tile then copies the
+// first kHostResultSlots status words (total included) into it: the caller's
+// pinned host buffer, which the caller reads after synchronising with the
+// stream.
 template <typename In, typename Out>
 __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t n,
                                                            const unsigned long long* n_dev,
                                                            Out* out, unsigned long long* tiles,
                                                            unsigned long long* ticket,
                                                            unsigned long long* status,
-                                                           unsigned long long* total_slot) {
+                                                           unsigned long long* total_slot,
+                                                           long long* host_out = nullptr) {
     __shared__ long long s_tile, s_excl;
     if (threadIdx.x == 0) s_tile = (long long)atomicAdd(ticket, 1ull);
     __syncthreads();
@@ -123,6 +128,12 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     if (tile == ntiles - 1 && threadIdx.x == 0) {
         out[n] = (Out)(s_excl + total);
         if (total_slot) *total_slot = (unsigned long long)(s_excl + total);
+        if (host_out) {
+#pragma unroll
+            for (int k = 0; k < kHostResultSlots; ++k)
+                host_out[k] = (long long)__hip_atomic_load(status + k, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 

@@ -45,6 +45,8 @@
 
 namespace tnr {
 
+static_assert(kHostResultSlots == TNR_HOST_RESULT_SLOTS, "host result slots");
+
 
 // ------------------------------------------------------------------- host
 
@@ -177,11 +179,12 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     return q;
 }
 
-// Counting: the plan is only known on the device, so both families are
-// launched and each exits at once when the plan has none of its structures.
-// An explicit brute_force request skips the cell-list kernel.  An explicit
-// cell_list request uses brute force only for a structure whose bin grid
-// does not fit, so its brute-force kernel gets a small grid (grid-stride).  Emitting: plan bit 0 launches
+// Counting: the plan is only known on the device, so with auto both
+// families are launched and each exits at once when the plan has none of
+// its structures.  An explicit brute_force request launches the brute-force
+// kernel only, an explicit cell_list request the cell-list kernel only (the
+// planner turns every structure of such a request into a cell list or an
+// error).  Emitting: plan bit 0 launches
 // the brute-force family, bit 1 the cell-list family over n_tasks bins (one
 // workgroup each).
 template <typename T, int MODE, bool EMIT>
@@ -195,9 +198,8 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
         if (req->algorithm != TNR_BRUTE_FORCE)
             k_cell_count<T, MODE><<<count_blocks<T, MODE>(2 * (L.cap_bins > n ? L.cap_bins : n)),
                                     kBlock, 0, stream>>>(q);
-        k_brute<T, MODE, false>
-            <<<req->algorithm == TNR_CELL_LIST ? 8u : brute_blocks<T, MODE, false>(n), kBlock, 0,
-               stream>>>(q);
+        if (req->algorithm != TNR_CELL_LIST)
+            k_brute<T, MODE, false><<<brute_blocks<T, MODE, false>(n), kBlock, 0, stream>>>(q);
     } else {
         if ((plan & 2) && n_tasks > 0)
             k_cell_emit<T, MODE><<<emit_blocks(n_tasks), kBlock, 0, stream>>>(q);
@@ -217,9 +219,12 @@ static void dispatch_queries(const tnr_request* req, const Layout& L, const Quer
     }
 }
 
+// The count pipeline.  Its last kernel copies the status words into
+// host_out (a device-visible pointer to the caller's pinned buffer) when
+// given.
 template <typename T>
 static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
-                            hipStream_t stream) {
+                            hipStream_t stream, long long* host_out) {
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
     const int reach = req->stencil_reach;  // 0: chosen per structure
@@ -277,7 +282,8 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     k_scan_lookback<long long, long long>
         <<<(unsigned)((n + kScanTile - 1) / kScanTile > 0 ? (n + kScanTile - 1) / kScanTile : 1),
            kBlock, 0, stream>>>(v.counts, n, nullptr, v.offsets, v.tiles_pairs,
-                                v.status + SS_TICKET_PAIRS, v.status, v.status + SS_PAIRS);
+                                v.status + SS_TICKET_PAIRS, v.status, v.status + SS_PAIRS,
+                                host_out);
     return hipGetLastError();
 }
 
@@ -389,9 +395,18 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
     if (rc != TNR_OK) return rc;
     if (!host_result) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "host_result is null");
     hipStream_t s = (hipStream_t)stream;
-    hipError_t e = req->dtype == TNR_FLOAT32 ? tnr::run_count<float>(req, workspace, L, s)
-                                             : tnr::run_count<double>(req, workspace, L, s);
-    if (e == hipSuccess) {
+    // Pinned host memory is written by the count's last kernel directly;
+    // other memory gets a copy behind it.
+    void* mapped = nullptr;
+    if (hipHostGetDevicePointer(&mapped, host_result, 0) != hipSuccess) {
+        mapped = nullptr;
+        (void)hipGetLastError();
+    }
+    hipError_t e =
+        req->dtype == TNR_FLOAT32
+            ? tnr::run_count<float>(req, workspace, L, s, (long long*)mapped)
+            : tnr::run_count<double>(req, workspace, L, s, (long long*)mapped);
+    if (e == hipSuccess && !mapped) {
         const tnr::Views v = tnr::views(workspace, L);
         e = hipMemcpyAsync(host_result, v.status, TNR_HOST_RESULT_SLOTS * sizeof(int64_t),
                            hipMemcpyDeviceToHost, s);
