@@ -310,12 +310,29 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
     setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, recs[b]);
 }
 
-// Structure of atom i: the b with bp[b] <= i < bp[b + 1] (batch_ptr valid).
-__device__ __forceinline__ int structure_of(const int64_t* bp, int64_t nb, int64_t i) {
-    int64_t lo = 0, hi = nb;  // answer in [lo, hi)
+// Structure of atom i: the b in [lo, hi) with bp[b] <= i < bp[b + 1]
+// (batch_ptr valid, the answer known to lie in [lo, hi)).
+__device__ __forceinline__ int structure_of(const int64_t* bp, int64_t lo, int64_t hi, int64_t i) {
     while (hi - lo > 1) {
         const int64_t mid = (lo + hi) >> 1;
         if (bp[mid] <= i) lo = mid; else hi = mid;
+    }
+    return (int)lo;
+}
+
+// The same for a wave-uniform i, by the whole wave: 64 candidates per step
+// (one load per lane), so a batch of B structures takes log64(B) loads.
+__device__ __forceinline__ int structure_of_wave(const int64_t* bp, int64_t nb, int64_t i) {
+    const int lane = lane_id();
+    int64_t lo = 0, len = nb;
+    while (len > 1) {
+        const int64_t step = (len + kWave - 1) / kWave;
+        const int64_t at = (int64_t)lane * step;
+        const bool le = at < len && bp[lo + at] <= i;
+        const unsigned long long m = ballot(le) | 1ull;
+        const int64_t last = 63 - __builtin_clzll(m);
+        lo += last * step;
+        len = min(step, len - last * step);
     }
     return (int)lo;
 }
@@ -419,8 +436,8 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
     const int64_t last = (first + kBlock < n_atoms ? first + kBlock : n_atoms) - 1;
     const int64_t i = first + threadIdx.x;
     const bool valid = i < n_atoms;
-    const int bfirst = SINGLE ? 0 : structure_of(bp, nb, first);
-    const int blast = SINGLE ? 0 : structure_of(bp, nb, last);
+    const int bfirst = SINGLE ? 0 : __builtin_amdgcn_readfirstlane(structure_of_wave(bp, nb, first));
+    const int blast = SINGLE ? 0 : __builtin_amdgcn_readfirstlane(structure_of_wave(bp, nb, last));
     const bool uniform = bfirst == blast;
     int b = bfirst;
     bool good = false;
@@ -430,7 +447,7 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
     double pmax = 0;
     unsigned long long st = 0;
     if (valid) {
-        b = uniform ? bfirst : structure_of(bp, nb, i);
+        b = uniform ? bfirst : structure_of(bp, bfirst, (int64_t)blast + 1, i);
         atom_struct[i] = b;
         const StructRec& r = SINGLE ? s_rec : recs[b];
         T p[3];

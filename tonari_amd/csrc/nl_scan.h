@@ -1,6 +1,6 @@
 // Device-wide exclusive scans: a single-pass scan with decoupled look-back
 // (k_scan_lookback) and the one-workgroup scan of the bins per structure
-// (struct_scan_block, run by k_plan or k_struct_scan).
+// (struct_scan_block, run by k_plan for one structure or k_struct_scan).
 #pragma once
 
 #include "nl_math.h"

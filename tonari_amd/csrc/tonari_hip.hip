@@ -4,16 +4,22 @@
 // brute-force count/emit) and nl_scan.h (device-wide scans).
 //
 // Pipeline of one request (all on the caller's stream):
-//   tnr_count: k_setup (zeroes the status words; per structure: batch_ptr
-//              checks, active pseudo-inverse, image repeats, grid frame) ->
-//              k_atoms (per atom: wraps, wrapped position, block reductions;
-//              zeroes the bin counters and scan tiles) -> k_plan (one
-//              workgroup per structure: margins, algorithm, bin grid) ->
-//              k_struct_scan (bins per structure, batch status; folded into
-//              k_plan for a single structure) -> k_bin -> k_scan_lookback(bin counts) -> k_scatter ->
-//              k_cell_count (persistent: cell-list bins, then brute-force
-//              sources) -> k_scan_lookback(pairs per source; E) -> one
-//              8-word device-to-host copy (status, E, plan, bins).
+//   tnr_count, one structure: k_atoms<T, true> (every block derives the
+//              structure's periodic metadata in LDS; per atom: wraps, wrapped
+//              position, block reductions; zeroes the bin counters and scan
+//              tiles) -> k_single_bin (plan: margins, algorithm, bin grid,
+//              status words; then binning);
+//   tnr_count, a batch: k_setup (zeroes the status words; per structure:
+//              batch_ptr checks, active pseudo-inverse, image repeats, grid
+//              frame) -> k_atoms<T, false> -> k_plan (one workgroup per
+//              structure: margins, algorithm, bin grid or brute-force work
+//              units) -> k_struct_scan (their scans over the batch, batch
+//              status) -> k_bin;
+//   then       k_scan_lookback (bin counts -> bin starts) -> k_scatter
+//              (binned atoms) -> k_cell_count and/or k_brute<count> ->
+//              k_scan_lookback (pairs per source -> offsets and E; its last
+//              block copies the status words into the caller's pinned host
+//              buffer).
 //   tnr_emit:  k_cell_emit and/or k_brute<emit> write i/j/P/S/d/D in place.
 //
 // Reference semantics (songfeitong/tonari):
