@@ -127,6 +127,23 @@ int tnr_count_finish(const int64_t* host_result, int64_t* n_pairs, char* err, si
 int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
              const tnr_outputs* out, void* stream, char* err, size_t err_len);
 
+/*
+ * Backward of the d/D outputs of tnr_emit: adds the gradients of positions
+ * (T[N][3]) and cell (T[B][3][3]) into grad_positions and grad_cell (set to
+ * zero by the caller) from grad_vectors (dL/dD, T[E][3]) and grad_distances
+ * (dL/dd, T[E]); either may be NULL.  pairs, shifts, vectors and distances
+ * are the E rows tnr_emit wrote (vectors and distances are needed only with
+ * grad_distances).  Replaces the autograd of the reference's Torch
+ * expression for D and d (src/tonari/_torch_frontend.py:92-104): with
+ * g = dL/dD + dL/dd * D / d (0 where d = 0), pos[j] += g, pos[i] -= g and
+ * cell[b][a][c] += S[a] g[c].  Float atomics: the summation order varies.
+ */
+int tnr_geometry_backward(int32_t dtype, int64_t n_pairs, int64_t n_atoms, int64_t n_structures,
+                          const int64_t* batch_ptr, const int64_t* pairs, const int32_t* shifts,
+                          const void* vectors, const void* distances, const void* grad_vectors,
+                          const void* grad_distances, void* grad_positions, void* grad_cell,
+                          void* stream, char* err, size_t err_len);
+
 #ifdef __cplusplus
 }
 #endif

@@ -26,6 +26,7 @@ EXPORTS = (
     "tnr_count",
     "tnr_count_async",
     "tnr_count_finish",
+    "tnr_geometry_backward",
     "tnr_emit",
 )
 
@@ -93,6 +94,13 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     lib.tnr_count_finish.restype = ctypes.c_int
     lib.tnr_count_finish.argtypes = [
         ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_geometry_backward.restype = ctypes.c_int
+    lib.tnr_geometry_backward.argtypes = [
+        ctypes.c_int32, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p,
+        ctypes.c_size_t,
     ]
     lib.tnr_emit.restype = ctypes.c_int
     lib.tnr_emit.argtypes = [

@@ -84,21 +84,74 @@ def validate_torch_inputs(
         raise ValueError("cutoff must be finite and positive")
 
 
-def _differentiable_geometry(
-    quantities: str, positions: Tensor, cell: Tensor, batch_ptr: Tensor, pairs: Tensor,
-    shifts: Tensor,
-) -> dict[str, Tensor]:
-    """The reference's Torch expression for D and d (``_torch_frontend.py:92-104``)."""
+def _torch_geometry(positions: Tensor, cell: Tensor, batch_ptr: Tensor, pairs: Tensor,
+                    shifts: Tensor) -> Tensor:
+    """The reference's Torch expression for D (``_torch_frontend.py:92-101``)."""
     source = pairs[:, 0].contiguous()
     target = pairs[:, 1].contiguous()
     pair_batch = torch.bucketize(source, batch_ptr[1:], right=True)
-    vectors = positions[target] - positions[source] + torch.einsum(
+    return positions[target] - positions[source] + torch.einsum(
         "ei,eij->ej", shifts.to(positions.dtype), cell[pair_batch]
     )
-    values = {"D": vectors}
-    if "d" in quantities:
-        values["d"] = torch.linalg.vector_norm(vectors, dim=1)
-    return values
+
+
+class _FusedGeometry(torch.autograd.Function):
+    """D and d as the emitting kernel wrote them, differentiable in positions and cell.
+
+    The backward runs ``tnr_geometry_backward``: the gradient of the
+    reference's expression (``_torch_frontend.py:92-104``) in one kernel.
+    When a graph of the gradient is asked for (``create_graph``), the same
+    gradient comes from that Torch expression instead, so that higher
+    derivatives exist.
+    """
+
+    @staticmethod
+    def forward(ctx, positions, cell, pairs, shifts, batch_ptr, vectors, distances):
+        ctx.save_for_backward(positions, cell, pairs, shifts, batch_ptr, vectors, distances)
+        return vectors.view_as(vectors), distances.view_as(distances)
+
+    @staticmethod
+    def backward(ctx, grad_vectors, grad_distances):
+        positions, cell, pairs, shifts, batch_ptr, vectors, distances = ctx.saved_tensors
+        if torch.is_grad_enabled():
+            wrt = [x for x, need in zip((positions, cell), ctx.needs_input_grad[:2]) if need]
+            with torch.enable_grad():
+                D = _torch_geometry(positions, cell, batch_ptr, pairs, shifts)
+                outputs, grads = [], []
+                if grad_vectors is not None:
+                    outputs.append(D)
+                    grads.append(grad_vectors)
+                if grad_distances is not None:
+                    outputs.append(torch.linalg.vector_norm(D, dim=1))
+                    grads.append(grad_distances)
+                found = torch.autograd.grad(
+                    outputs, wrt, grads, create_graph=True, allow_unused=True
+                )
+            found = list(found)
+            gp = found.pop(0) if ctx.needs_input_grad[0] else None
+            gc = found.pop(0) if ctx.needs_input_grad[1] else None
+            return gp, gc, None, None, None, None, None
+        lib = load_torch_hip()
+        grad_positions = torch.zeros(positions.shape, dtype=positions.dtype, device=positions.device)
+        grad_cell = torch.zeros(cell.shape, dtype=cell.dtype, device=cell.device)
+        gD = None if grad_vectors is None else grad_vectors.contiguous()
+        gd = None if grad_distances is None else grad_distances.contiguous()
+        err = ctypes.create_string_buffer(512)
+        code = lib.tnr_geometry_backward(
+            0 if positions.dtype == torch.float32 else 1, pairs.shape[0], positions.shape[0],
+            batch_ptr.numel() - 1, batch_ptr.data_ptr(), pairs.data_ptr(), shifts.data_ptr(),
+            vectors.data_ptr(), distances.data_ptr(), None if gD is None else gD.data_ptr(),
+            None if gd is None else gd.data_ptr(), grad_positions.data_ptr(),
+            grad_cell.data_ptr(), torch.cuda.current_stream(positions.device).cuda_stream, err,
+            len(err),
+        )
+        if code != TNR_OK:
+            _raise(code, err.value.decode())
+        return (
+            grad_positions if ctx.needs_input_grad[0] else None,
+            grad_cell if ctx.needs_input_grad[1] else None,
+            None, None, None, None, None,
+        )
 
 
 _HOST = threading.local()
@@ -246,8 +299,7 @@ def neighbor_list_hip(
     dtype = positions.dtype
     want = set(quantities)
     if need_grad:
-        want |= {"P", "S"}
-        want -= {"d", "D"}
+        want |= {"P", "S", "D", "d"}
     err = ctypes.create_string_buffer(512)
     switch = device.index is not None and device.index != torch.cuda.current_device()
     with torch.cuda.device(device) if switch else contextlib.nullcontext():
@@ -296,10 +348,8 @@ def neighbor_list_hip(
                 _emit(lib, req, workspace, ws_bytes, out, count, plan, bins, stream, err)
         table[key] = (_capacity(count), plan, bins)
         if need_grad:
-            out.update(
-                _differentiable_geometry(
-                    quantities, grad_positions, grad_cell, batch_ptr, out["P"], out["S"]
-                )
+            out["D"], out["d"] = _FusedGeometry.apply(
+                grad_positions, grad_cell, out["P"], out["S"], batch_ptr, out["D"], out["d"]
             )
     return tuple(out[q] for q in quantities)
 

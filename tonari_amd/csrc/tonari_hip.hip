@@ -38,6 +38,7 @@
 #include "nl_prologue.h"
 #include "nl_query.h"
 #include "nl_scan.h"
+#include "nl_backward.h"
 
 #include "../../include/tonari_hip.h"
 
@@ -456,6 +457,40 @@ int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
     const hipError_t e = req->dtype == TNR_FLOAT32
                              ? tnr::run_emit<float>(req, workspace, L, out, s)
                              : tnr::run_emit<double>(req, workspace, L, out, s);
+    if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
+    return TNR_OK;
+}
+
+int tnr_geometry_backward(int32_t dtype, int64_t n_pairs, int64_t n_atoms, int64_t n_structures,
+                          const int64_t* batch_ptr, const int64_t* pairs, const int32_t* shifts,
+                          const void* vectors, const void* distances, const void* grad_vectors,
+                          const void* grad_distances, void* grad_positions, void* grad_cell,
+                          void* stream, char* err, size_t err_len) {
+    if (dtype != TNR_FLOAT32 && dtype != TNR_FLOAT64)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "dtype must be float32 or float64");
+    if (n_pairs < 0 || n_atoms < 0 || n_structures < 1)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "invalid sizes");
+    if (n_pairs == 0) return TNR_OK;
+    if (!batch_ptr || !pairs || !shifts || !grad_positions || !grad_cell)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "required pointers are null");
+    if (grad_distances && (!distances || !vectors))
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR,
+                              "the gradient of d needs the distances and vectors");
+    if (!grad_vectors && !grad_distances) return TNR_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t want = (n_pairs + tnr::kBlock - 1) / tnr::kBlock;
+    const unsigned blocks = (unsigned)(want < 65536 ? want : 65536);
+    if (dtype == TNR_FLOAT32)
+        tnr::k_geometry_backward<float><<<blocks, tnr::kBlock, 0, s>>>(
+            n_pairs, n_structures, batch_ptr, pairs, shifts, (const float*)vectors,
+            (const float*)distances, (const float*)grad_vectors, (const float*)grad_distances,
+            (float*)grad_positions, (float*)grad_cell);
+    else
+        tnr::k_geometry_backward<double><<<blocks, tnr::kBlock, 0, s>>>(
+            n_pairs, n_structures, batch_ptr, pairs, shifts, (const double*)vectors,
+            (const double*)distances, (const double*)grad_vectors, (const double*)grad_distances,
+            (double*)grad_positions, (double*)grad_cell);
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
     return TNR_OK;
 }
