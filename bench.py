@@ -169,6 +169,42 @@ def load_traffic(name: str):
     return data.get("hbm_bytes_per_launch")
 
 
+def time_backward(cfg, t, reps: int):
+    """HIP-event durations of the gradient of sum(w * D) for positions and cell.
+
+    D comes from the public call with positions and cell requiring grad; its
+    backward is tnr_geometry_backward (fused).  For comparison, the same
+    gradient through the reference's Torch expression for D over the same
+    pairs (autograd of gathers, einsum and their scatter-adds).
+    """
+    import torch
+
+    from tonari_amd._torch_frontend import _torch_geometry
+
+    positions = t["positions"].clone().requires_grad_()
+    cell = t["cell"].clone().requires_grad_()
+    P, S, D = public_call(dict(cfg, quantities="PSD"), dict(t, positions=positions, cell=cell))
+    w = torch.randn(D.shape, dtype=D.dtype, device=D.device)
+    D_torch = _torch_geometry(positions, cell, t["batch_ptr"], P, S)
+    result = {}
+    # the Torch expression takes seconds on C4 (its scatter-adds into the one
+    # cell contend): one timed repetition after the warm-up
+    for name, values, n_rep in (("fused_us", D, reps), ("torch_expression_us", D_torch, 1)):
+        loss = (w * values).sum()
+        times = []
+        for rep in range(n_rep + 1):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            torch.autograd.grad(loss, (positions, cell), retain_graph=True)
+            ev[1].record()
+            torch.cuda.synchronize()
+            if rep > 0:
+                times.append(ev[0].elapsed_time(ev[1]) * 1e3)
+        result[name] = round(statistics.median(times), 2)
+    result["n_pairs"] = int(P.shape[0])
+    return result
+
+
 def cpu_baseline(cfg, mode: str):
     """The reference CPU core (or the restatement) on the same workload, all host cores."""
     import oracle
@@ -296,6 +332,9 @@ def main() -> int:
             steps = max(3, args.steps // 3) if name == "C5" else args.steps
             secondary[name] = measure(name, scfg, steps, 2, max(3, args.reps // 4), dev)
             log(f"{name}: {secondary[name]}")
+    log("C4: backward of D")
+    backward = time_backward(cfg, to_device(cfg, dev), max(3, args.reps // 4))
+    log(f"C4 backward: {backward}")
     base = None
     if args.cpu_baseline != "off":
         log("cpu baseline")
@@ -341,6 +380,7 @@ def main() -> int:
         "frac_kernel_sum": head["frac_kernel_sum"],
         "GBps_end_to_end": head["GBps_end_to_end"],
         "secondary": secondary,
+        "backward_C4": backward,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -7,12 +7,16 @@
 // d_e = 0, as torch's vector_norm backward):
 //   dL/dpos[j_e] += g_e,  dL/dpos[i_e] -= g_e,  dL/dcell[b_e][a][c] += S_e[a] g_e[c].
 //
-// One thread per pair.  The pairs of a source are contiguous, so the source
-// side is reduced per run of equal sources inside a wave (segmented scan) and
-// added once per run; the target side takes one atomic add per component;
-// the cell side is reduced per run of equal structures and added once per
-// run (9 atomics).  Float atomics make the summation order vary between runs
-// (the same holds for torch's index_add on the device).
+// One thread per pair, each wave a contiguous range of pairs.  The pairs of
+// a source are contiguous, so the source side is reduced per run of equal
+// sources inside a wave (segmented scan) and added once per run; the target
+// side takes one atomic add per component.  The pairs of a structure are
+// contiguous too (sources come in index or bin order, both grouped by
+// structure), so each wave keeps a running sum of the cell gradient of its
+// current structure, adds it when the structure changes, and the waves of
+// a block merge their last sums: a structure's 9 entries take a few atomics
+// per block, not per pair.  Float atomics make the summation order vary
+// between runs (the same holds for torch's index_add on the device).
 #pragma once
 
 #include "nl_math.h"
@@ -37,11 +41,35 @@ __global__ __launch_bounds__(kBlock) void k_geometry_backward(
     int64_t n_pairs, int64_t nb, const int64_t* bp, const int64_t* pairs, const int32_t* shifts,
     const T* vec, const T* dist, const T* grad_vec, const T* grad_dist, T* grad_pos,
     T* grad_cell) {
+    __shared__ T s_acc[kWavesPerBlock][9];
+    __shared__ int s_b[kWavesPerBlock];
     const int lane = lane_id();
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    for (int64_t e0 = (int64_t)blockIdx.x * kBlock; e0 < n_pairs; e0 += stride) {
-        const int64_t e = e0 + threadIdx.x;
-        const bool valid = e < n_pairs;
+    const int wv = uniform(threadIdx.x / kWave);
+    // a contiguous range of pairs per wave
+    const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    const int64_t per = ((n_pairs + nwaves - 1) / nwaves + kWave - 1) / kWave * kWave;
+    const int64_t w_lo = min(((int64_t)blockIdx.x * kWavesPerBlock + wv) * per, n_pairs);
+    const int64_t w_hi = min(w_lo + per, n_pairs);
+    // per-lane partial cell-gradient sums of structure cur_b (wave-uniform)
+    T acc[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) acc[k] = T(0);
+    int cur_b = -1;
+    // adds the wave's sums of structure cur_b to grad_cell (lanes 0..8)
+    auto flush = [&]() {
+        if (cur_b < 0) return;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            T x = acc[k];
+#pragma unroll
+            for (int d = kWave / 2; d > 0; d >>= 1) x += __shfl_xor(x, d);
+            if (lane == k) unsafeAtomicAdd(grad_cell + 9 * cur_b + k, x);
+            acc[k] = T(0);
+        }
+    };
+    for (int64_t e0 = w_lo; e0 < w_hi; e0 += kWave) {
+        const int64_t e = e0 + lane;
+        const bool valid = e < w_hi;
         long long s = -1 - lane, t = 0;  // invalid lanes: keys no other lane has
         int b = -1 - lane;
         T g[3] = {T(0), T(0), T(0)};
@@ -77,11 +105,11 @@ __global__ __launch_bounds__(kBlock) void k_geometry_backward(
 #pragma unroll
             for (int c = 0; c < 3; ++c) unsafeAtomicAdd(grad_pos + 3 * t + c, g[c]);
         }
+        const unsigned long long le = lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1ull);
         // source side: runs of equal sources
         {
             const long long sp = __shfl_up(s, 1);
             const unsigned long long heads = ballot(lane == 0 || sp != s);
-            const unsigned long long le = lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1ull);
             const int seg0 = 63 - __builtin_clzll(heads & le);
             const bool tail = lane == kWave - 1 || ((heads >> (lane + 1)) & 1ull);
             T sum[3];
@@ -92,21 +120,64 @@ __global__ __launch_bounds__(kBlock) void k_geometry_backward(
                 for (int c = 0; c < 3; ++c) unsafeAtomicAdd(grad_pos + 3 * s + c, -sum[c]);
             }
         }
-        // cell side: runs of equal structures
+        // cell side: lanes of structure cur_b add to their partial sums; a
+        // round that holds another structure (rare: the pairs of a structure
+        // are contiguous) flushes the sums and takes that structure's runs
+        // one by one
         {
-            const int bpv = __shfl_up(b, 1);
-            const unsigned long long heads = ballot(lane == 0 || bpv != b);
-            const unsigned long long le = lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1ull);
-            const int seg0 = 63 - __builtin_clzll(heads & le);
-            const bool tail = lane == kWave - 1 || ((heads >> (lane + 1)) & 1ull);
+            T v[9];
 #pragma unroll
-            for (int a = 0; a < 3; ++a) {
+            for (int a = 0; a < 3; ++a)
 #pragma unroll
-                for (int c = 0; c < 3; ++c) {
-                    const T v = segment_inclusive_sum((T)S[a] * g[c], seg0);
-                    if (valid && tail) unsafeAtomicAdd(grad_cell + 9 * b + 3 * a + c, v);
+                for (int c = 0; c < 3; ++c) v[3 * a + c] = (T)S[a] * g[c];
+            if (ballot(valid && b != cur_b) == 0) {
+#pragma unroll
+                for (int k = 0; k < 9; ++k) acc[k] += v[k];
+            } else {
+                flush();
+                // runs of equal structures: all but the last are added now,
+                // the last one becomes the running structure
+                const int bpv = __shfl_up(b, 1);
+                const unsigned long long heads = ballot(lane == 0 || bpv != b);
+                const unsigned long long vmask = ballot(valid);
+                const int last_valid = 63 - __builtin_clzll(vmask);
+                const int b_last = __builtin_amdgcn_readfirstlane(__shfl(b, last_valid));
+                const int seg0 = 63 - __builtin_clzll(heads & le);
+                const bool tail = valid && lane != last_valid &&
+                                  (lane == kWave - 1 || ((heads >> (lane + 1)) & 1ull)) &&
+                                  b != b_last;
+#pragma unroll
+                for (int k = 0; k < 9; ++k) {
+                    const T x = segment_inclusive_sum(v[k], seg0);
+                    if (tail) unsafeAtomicAdd(grad_cell + 9 * b + k, x);
+                    acc[k] = valid && b == b_last ? v[k] : T(0);
                 }
+                cur_b = b_last;
             }
+        }
+    }
+    // the block's waves merge their last sums when they share a structure
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        T x = acc[k];
+#pragma unroll
+        for (int d = kWave / 2; d > 0; d >>= 1) x += __shfl_xor(x, d);
+        if (lane == k) s_acc[wv][k] = x;
+    }
+    if (lane == 0) s_b[wv] = cur_b;
+    __syncthreads();
+    if (threadIdx.x < 9) {
+        const int k = threadIdx.x;
+        for (int w = 0; w < kWavesPerBlock; ++w) {
+            const int bw = s_b[w];
+            if (bw < 0) continue;
+            bool first = true;
+            for (int u = 0; u < w; ++u) first = first && s_b[u] != bw;
+            if (!first) continue;
+            T sum = T(0);
+            for (int u = w; u < kWavesPerBlock; ++u)
+                if (s_b[u] == bw) sum += s_acc[u][k];
+            unsafeAtomicAdd(grad_cell + 9 * bw + k, sum);
         }
     }
 }
