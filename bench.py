@@ -276,6 +276,8 @@ def main() -> int:
     ap.add_argument("--reps", type=int, default=20, help="event-timed repetitions")
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "reference", "port", "off"])
     ap.add_argument("--secondary", default="C2,C3,C5", help="comma list, or 'none'")
+    ap.add_argument("--backward", default="on", choices=["on", "off"],
+                    help="also time the C4 backward of D (fused and Torch expression)")
     ap.add_argument("--secondary-only", action="store_true",
                     help="time only the --secondary configurations (one JSON object per line; "
                          "for profiling them) instead of the benchmark line")
@@ -332,9 +334,11 @@ def main() -> int:
             steps = max(3, args.steps // 3) if name == "C5" else args.steps
             secondary[name] = measure(name, scfg, steps, 2, max(3, args.reps // 4), dev)
             log(f"{name}: {secondary[name]}")
-    log("C4: backward of D")
-    backward = time_backward(cfg, to_device(cfg, dev), max(3, args.reps // 4))
-    log(f"C4 backward: {backward}")
+    backward = None
+    if args.backward == "on":
+        log("C4: backward of D")
+        backward = time_backward(cfg, to_device(cfg, dev), max(3, args.reps // 4))
+        log(f"C4 backward: {backward}")
     base = None
     if args.cpu_baseline != "off":
         log("cpu baseline")
