@@ -85,7 +85,7 @@ struct EmitStageCap<float> {
 };
 template <>
 struct EmitStageCap<double> {
-    static constexpr int value = 768;
+    static constexpr int value = 1280;
 };
 
 // Image shift k packed as three signed 10-bit fields (|k_a| <= 511).
@@ -462,8 +462,25 @@ __device__ __forceinline__ int stencil_piece(const StencilLds& st, int v, int np
     return p;
 }
 
+// Writes one kept candidate of source si from values in registers: the
+// output shift is the image k corrected by the wraps ws, wt (zero for an
+// unwrapped structure); D uses the original positions ps, pt.
+template <typename T>
+__device__ __forceinline__ void cell_write_regs(const QueryArgs<T>& a, long long o, int si, int tid,
+                                                int kk, const T ps[3], const T pt[3],
+                                                const int4& ws, const int4& wt,
+                                                const CellBin<T>& cb) {
+    int kx, ky, kz;
+    unpack_k(kk, kx, ky, kz);
+    kx = shift_i32(kx, wt.x, ws.x);
+    ky = shift_i32(ky, wt.y, ws.y);
+    kz = shift_i32(kz, wt.z, ws.z);
+    write_hit(a, o, si, tid, kx, ky, kz, ps, pt, cb.c, cb.diagonal);
+}
+
 // Writes one kept candidate of source si: the output shift is the image k
-// corrected by the representatives' wraps; D uses the original positions.
+// corrected by the representatives' wraps; D uses the original positions
+// (loaded here for a wrapped structure).
 template <typename T, bool WRAPPED>
 __device__ __forceinline__ void cell_write(const QueryArgs<T>& a, long long o, int si, int tid,
                                            int kk, T rx, T ry, T rz, T sx, T sy, T sz,
@@ -731,6 +748,13 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
         const int ns = min(kWave, cb.se - sg);
         const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
         const int sidx = as_idx(sq.w);
+        // wrapped: the sources' wraps and original positions (binned order)
+        int4 sw = make_int4(0, 0, 0, 0);
+        Vec4<T> sp = sq;
+        if (WRAPPED && lane < ns) {
+            sw = a.binned_w[sg + lane];
+            sp = a.binned_p[sg + lane];
+        }
         // lane gi: first output of source gi
         const long long cur = lane < ns ? a.offsets[cb.by_bin ? sg + lane : sidx] : 0;
         auto mask_of = [&](int s0_) -> unsigned long long {
@@ -768,9 +792,13 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                 __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
                 // rounds of 64 entries; the next round's record is loaded ahead.
                 // The owner lookup (a lane shuffle) runs with every lane active.
+                // A wrapped structure's candidates also bring their wraps and
+                // original positions (binned order), loaded with the record.
                 int e = 0, tg = 0, kk = 0;
-                Vec4<T> rec = zero4;
-                auto fetch = [&](int r, int& e_, int& tg_, int& kk_, Vec4<T>& rec_) {
+                Vec4<T> rec = zero4, rp = zero4;
+                int4 rw = make_int4(0, 0, 0, 0);
+                auto fetch = [&](int r, int& e_, int& tg_, int& kk_, Vec4<T>& rec_, int4& rw_,
+                                 Vec4<T>& rp_) {
                     e_ = r < L ? (int)list[r] : 0;
                     tg_ = __shfl(tag, e_ >> 6);
                     if (r < L) {
@@ -778,24 +806,41 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                         const int p = st.piece[v];
                         kk_ = st.kid[p];
                         rec_ = cand_record<T, STAGED>(a, st, cand, p, v);
+                        if (WRAPPED) {
+                            rw_ = a.binned_w[v + st.delta[p]];
+                            rp_ = a.binned_p[v + st.delta[p]];
+                        }
                     }
                 };
-                fetch(lane, e, tg, kk, rec);
+                fetch(lane, e, tg, kk, rec, rw, rp);
                 for (int r0 = 0; r0 < L; r0 += kWave) {
                     int e_n = 0, tg_n = 0, kk_n = 0;
-                    Vec4<T> rec_n = zero4;
-                    if (r0 + kWave < L) fetch(r0 + kWave + lane, e_n, tg_n, kk_n, rec_n);
+                    Vec4<T> rec_n = zero4, rp_n = zero4;
+                    int4 rw_n = make_int4(0, 0, 0, 0);
+                    if (r0 + kWave < L)
+                        fetch(r0 + kWave + lane, e_n, tg_n, kk_n, rec_n, rw_n, rp_n);
                     const int g = tg >> 6;
                     const long long o = __shfl(ob, e >> 6) + base + r0 + lane;
-                    const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                     const int si = __shfl(sidx, g);
-                    if (r0 + lane < L)
-                        cell_write<T, WRAPPED>(a, o, si, as_idx(rec.w), kk, rec.x, rec.y, rec.z,
-                                               sx, sy, sz, cb);
+                    if (WRAPPED) {
+                        const T ps[3] = {__shfl(sp.x, g), __shfl(sp.y, g), __shfl(sp.z, g)};
+                        const int4 ws = make_int4(__shfl(sw.x, g), __shfl(sw.y, g),
+                                                  __shfl(sw.z, g), 0);
+                        const T pt[3] = {rp.x, rp.y, rp.z};
+                        if (r0 + lane < L)
+                            cell_write_regs<T>(a, o, si, as_idx(rec.w), kk, ps, pt, ws, rw, cb);
+                    } else {
+                        const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
+                        if (r0 + lane < L)
+                            cell_write<T, false>(a, o, si, as_idx(rec.w), kk, rec.x, rec.y,
+                                                 rec.z, sx, sy, sz, cb);
+                    }
                     e = e_n;
                     tg = tg_n;
                     kk = kk_n;
                     rec = rec_n;
+                    rw = rw_n;
+                    rp = rp_n;
                 }
             }
         }
@@ -836,6 +881,9 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
     const int j = lane - sl * nch;
     const bool want_d = a.dist != nullptr;
     const bool want_vec = a.vec != nullptr || want_d;
+    // bits of the candidate index in a list entry
+    const unsigned vb = cb.C > 1 ? 32u - (unsigned)__builtin_clz((unsigned)(cb.C - 1)) : 1u;
+    const unsigned vmask = (1u << vb) - 1u;
     // groups of S sources of the bin (emit_group_size), dealt round-robin to the waves
     const int wv = uniform(threadIdx.x / kWave);
     const int nsrc = cb.se - cb.sb;  // at most kWave: sources and offsets come preloaded
@@ -884,10 +932,12 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
             // minus the list position of its first hit)
             const long long ob = __shfl(__shfl(cur, gi) - first, min(lane, S - 1) * nch);
             const unsigned ob32 = (unsigned)ob;  // o = ob + list position (mod 2^32)
-            // list entry: source lane g << 10 | candidate v (v < C <= 1024)
-            static_assert(EmitStageCap<float>::value <= 1024 && EmitStageCap<double>::value <= 1024,
-                          "candidate index in 10 bits");
-            const unsigned ebase = ((unsigned)gi << 10) + (unsigned)j;  // + bit * nch
+            // list entry: source lane g << vb | candidate v, with vb bits for
+            // v < C; g < 64 / nch and C <= 64 nch keep it below 2^13
+            static_assert(EmitStageCap<float>::value <= kMapCap &&
+                              EmitStageCap<double>::value <= kMapCap,
+                          "entries fit 16 bits");
+            const unsigned ebase = ((unsigned)gi << vb) + (unsigned)j;  // + bit * nch
             for (int base = 0; base < total; base += kListCap) {
                 const int L = min(kListCap, total - base);
                 __builtin_amdgcn_wave_barrier();
@@ -922,8 +972,8 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                 // rounds of 64 entries; the next round's LDS reads are issued ahead
                 auto fetch = [&](int r, int& g_, Vec4<T>& rec_, int4& k_) {
                     const unsigned e_ = list[min(r, L - 1)];
-                    g_ = (int)(e_ >> 10);
-                    const int v = (int)(e_ & 1023u);
+                    g_ = (int)(e_ >> vb);
+                    const int v = (int)(e_ & vmask);
                     rec_ = cand[v];
                     unpack_k(st.kid[st.piece[v]], k_.x, k_.y, k_.z);
                 };

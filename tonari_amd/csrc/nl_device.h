@@ -66,6 +66,7 @@ enum StatusSlot : int {
     SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
     SS_TOTAL_UNITS = 7,   // brute-force work units of the batch
+    SS_ANY_WRAP = 8,      // some cell-list atom has a nonzero wrap: binned_w / binned_p are written
     SS_SLOTS = 64,
     kHostResultSlots = 8,  // status words copied to the caller's host buffer
 };
@@ -129,7 +130,7 @@ struct alignas(16) BlockPartial {
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
     size_t status, structs, struct_bins, struct_bin_off, struct_units, struct_unit_off,
-        atom_struct, atom_wrap, atom_q,
+        atom_struct, atom_wrap, atom_q, binned_w, binned_p,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets,
         block_partials, masks, tiles_bins, tiles_pairs, total;
     int64_t cap_bins, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
@@ -168,6 +169,8 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.bin_count = take(sizeof(int32_t) * (size_t)(L.cap_bins + 1));
     L.bin_start = take(sizeof(int32_t) * (size_t)(L.cap_bins + 2));
     L.binned = take(tsize * 4 * (size_t)(n + 1));
+    L.binned_w = take(sizeof(int32_t) * 4 * (size_t)(n + 1));
+    L.binned_p = take(tsize * 4 * (size_t)(n + 1));
     L.counts = take(sizeof(int64_t) * (size_t)(n + 1));
     L.offsets = take(sizeof(int64_t) * (size_t)(n + 2));
     L.n_atom_blocks = (n + kBlock - 1) / kBlock;

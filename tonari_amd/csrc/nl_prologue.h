@@ -982,6 +982,7 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
             if (images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
             status[SS_TOTAL_BINS] = (unsigned long long)s_bins;
             status[SS_TOTAL_UNITS] = (unsigned long long)s_units;
+            status[SS_ANY_WRAP] = r.algo == ALGO_CELL && r.any_wrap ? 1ull : 0ull;
             status[SS_PLAN] = r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
             status[SS_TOTAL_IMAGES] = images;
             status[SS_FLAGS] = st;
@@ -1001,18 +1002,29 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
 }
 
 // Counting sort, last step: atom i goes to binned position
-// bin_start[bin] + rank.
+// bin_start[bin] + rank (with its wraps and original position when some
+// cell-list structure has wrapped atoms).
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<T>* atom_q,
                                                      const int* atom_bin, const int* atom_rank,
                                                      const int* bin_start, Vec4<T>* binned,
+                                                     const T* pos, const int4* atom_wrap,
+                                                     int4* binned_w, Vec4<T>* binned_p,
                                                      const unsigned long long* status) {
     if (load_status(status + SS_FLAGS) & kAbortBits) return;
+    const bool wrapped = load_status(status + SS_ANY_WRAP) != 0;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_atoms) return;
     const int g = atom_bin[i];
     if (g < 0) return;
-    binned[bin_start[g] + atom_rank[i]] = atom_q[i];
+    const int at = bin_start[g] + atom_rank[i];
+    binned[at] = atom_q[i];
+    if (wrapped) {
+        // the emitting pass of a wrapped structure reads each candidate's
+        // wraps and original position at its binned position
+        binned_w[at] = atom_wrap[i];
+        binned_p[at] = Vec4<T>{pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], T(0)};
+    }
 }
 
 }  // namespace tnr

@@ -25,6 +25,8 @@ struct QueryArgs {
     const Vec4<T>* atom_q;
     const int* bin_start;
     const Vec4<T>* binned;
+    const int4* binned_w;       // wraps in binned order (status SS_ANY_WRAP)
+    const Vec4<T>* binned_p;    // original positions in binned order (likewise)
     long long* counts;
     const long long* offsets;
     unsigned long long* status;

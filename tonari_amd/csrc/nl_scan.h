@@ -147,16 +147,17 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
                                   StructRec* recs, unsigned long long* status,
                                   int64_t cap_bins) {
     __shared__ long long s_carry, s_ucarry;
-    __shared__ unsigned long long s_flags, s_plan, s_images;
+    __shared__ unsigned long long s_flags, s_plan, s_images, s_wrap;
     if (threadIdx.x == 0) {
         s_carry = 0;
         s_ucarry = 0;
         s_flags = 0;
         s_plan = 0;
         s_images = 0;
+        s_wrap = 0;
     }
     __syncthreads();
-    unsigned long long flags = 0, plan = 0, images = 0;
+    unsigned long long flags = 0, plan = 0, images = 0, wrap = 0;
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
         long long v[kScanItems], u[kScanItems];
@@ -172,6 +173,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
                 const StructRec& r = recs[i];
                 flags |= r.flags;
                 plan |= r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
+                if (r.algo == ALGO_CELL && r.any_wrap) wrap = 1;
                 images += (unsigned long long)r.img_total;
             }
         }
@@ -200,6 +202,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
     if (flags) atomicOr(&s_flags, flags);
     if (plan) atomicOr(&s_plan, plan);
     if (images) atomicAdd(&s_images, images);
+    if (wrap) atomicOr(&s_wrap, wrap);
     __syncthreads();
     if (threadIdx.x == 0) {
         const long long total = s_carry;
@@ -209,6 +212,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         status[SS_TOTAL_UNITS] = (unsigned long long)s_ucarry;
         status[SS_PLAN] = s_plan;
         status[SS_TOTAL_IMAGES] = s_images;
+        status[SS_ANY_WRAP] = s_wrap;
         unsigned long long st = s_flags;
         if (total > cap_bins) st |= ST_CAPACITY;
         if (s_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;

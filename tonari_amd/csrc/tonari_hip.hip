@@ -72,6 +72,8 @@ struct Views {
     int* bin_count;
     int* bin_start;
     void* binned;
+    int4* binned_w;
+    void* binned_p;
     long long* counts;
     long long* offsets;
     BlockPartial* block_partials;
@@ -97,6 +99,8 @@ static Views views(void* ws, const Layout& L) {
     v.bin_count = (int*)(base + L.bin_count);
     v.bin_start = (int*)(base + L.bin_start);
     v.binned = base + L.binned;
+    v.binned_w = (int4*)(base + L.binned_w);
+    v.binned_p = base + L.binned_p;
     v.counts = (long long*)(base + L.counts);
     v.offsets = (long long*)(base + L.offsets);
     v.block_partials = (BlockPartial*)(base + L.block_partials);
@@ -176,6 +180,8 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.atom_q = (const Vec4<T>*)v.atom_q;
     q.bin_start = v.bin_start;
     q.binned = (const Vec4<T>*)v.binned;
+    q.binned_w = v.binned_w;
+    q.binned_p = (const Vec4<T>*)v.binned_p;
     q.counts = v.counts;
     q.offsets = v.offsets;
     q.status = v.status;
@@ -281,6 +287,8 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_scatter<T><<<blocks_for(n), kBlock, 0, stream>>>(n, (const Vec4<T>*)v.atom_q,
                                                            v.atom_bin, v.atom_rank,
                                                            v.bin_start, (Vec4<T>*)v.binned,
+                                                           (const T*)req->positions, v.atom_wrap,
+                                                           v.binned_w, (Vec4<T>*)v.binned_p,
                                                            v.status);
     }
     const QueryArgs<T> q = query_args<T>(req, v);
