@@ -156,3 +156,29 @@ def test_second_derivatives():
     (h_ref,) = torch.autograd.grad((f_ref ** 2).sum(), pos)
     assert_close(forces, f_ref, torch.float64)
     assert_close(hess_vec, h_ref, torch.float64)
+
+
+def test_edge_cases():
+    # no pairs: zero gradients, no kernel work
+    positions = torch.tensor([[0.0, 0.0, 0.0], [3.0, 0.0, 0.0]], dtype=torch.float64, device=DEV,
+                             requires_grad=True)
+    cell = (torch.eye(3, dtype=torch.float64, device=DEV) * 10.0).requires_grad_()
+    pbc = torch.zeros(3, dtype=torch.bool, device=DEV)
+    d, D = neighbor_list("dD", positions, cell, pbc, 1.0)
+    assert d.shape == (0,) and D.shape == (0, 3)
+    gp, gc = torch.autograd.grad(d.sum() + D.sum(), (positions, cell))
+    assert float(gp.abs().max()) == 0.0 and float(gc.abs().max()) == 0.0
+
+    # only the cell requires grad, positions given as a non-contiguous view
+    cfg = small_box(seed=21, n=150)
+    base = torch.as_tensor(cfg["positions"].T.copy()).to(DEV, torch.float64)
+    positions = base.T  # (N, 3) view with strides (1, N)
+    assert not positions.is_contiguous()
+    cell = torch.as_tensor(cfg["cell"]).to(DEV, torch.float64).requires_grad_()
+    pbc = torch.as_tensor(cfg["pbc"]).to(DEV)
+    batch_ptr = torch.as_tensor(cfg["batch_ptr"]).to(DEV)
+    P, S, D = neighbor_list("PSD", positions, cell, pbc, cfg["cutoff"], batch_ptr)
+    w = torch.randn(D.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(3)).to(DEV)
+    (gc,) = torch.autograd.grad((w * D).sum(), cell)
+    _, rc = reference_grads(positions, cell, batch_ptr, P, S, w, None)
+    assert_close(gc, rc, torch.float64)
