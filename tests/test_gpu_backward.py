@@ -68,6 +68,7 @@ def fused_grads(cfg, quantities, dtype, seed, **kw):
 def assert_close(actual, expected, dtype):
     tol = 1e-10 if dtype == torch.float64 else 1e-4
     a = actual.detach().double().cpu()
+    expected = expected.detach()
     scale = max(1.0, float(expected.abs().max()))
     err = float((a - expected).abs().max())
     assert err <= tol * scale, f"max error {err:.3e} over scale {scale:.3e}"
