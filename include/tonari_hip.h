@@ -78,8 +78,11 @@ typedef struct tnr_request {
 
 /* Output buffers for tnr_emit; any pointer may be NULL (not requested). */
 typedef struct tnr_outputs {
-    int64_t n_pairs;    /* E returned by tnr_count */
-    int64_t plan;       /* host_result[3] of tnr_count (kernel families in use) */
+    int64_t n_pairs;    /* E returned by tnr_count, or the rows the outputs hold (see plan) */
+    int64_t plan;       /* host_result[3] of tnr_count (kernel families in use), or -1: the
+                           emit reads plan and bins from the count's status words on the
+                           device, for callers that do not wait for the count (graph
+                           capture); pairs beyond n_pairs rows are then dropped and flagged */
     int64_t n_tasks;    /* host_result[4] of tnr_count (cell-list bins of the batch) */
     int64_t* pairs;     /* P: int64[E][2] (source, target) */
     int32_t* shifts;    /* S: int32[E][3] */

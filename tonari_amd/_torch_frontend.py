@@ -8,8 +8,9 @@ CUDA provider (``:138-145``); i/j/P/S/d/D are written by the emit kernel
 instead of being assembled with Torch gathers.
 
 When ``d`` or ``D`` is requested and ``positions`` or ``cell`` requires
-gradients, d/D are built from P and S with the reference's differentiable
-Torch expression so autograd works as in the reference.
+gradients, the kernel's d/D carry autograd to both through a fused backward
+kernel (``_FusedGeometry``), the gradient of the reference's Torch
+expression.
 """
 
 from __future__ import annotations

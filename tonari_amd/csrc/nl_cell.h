@@ -794,53 +794,49 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                 // The owner lookup (a lane shuffle) runs with every lane active.
                 // A wrapped structure's candidates also bring their wraps and
                 // original positions (binned order), loaded with the record.
-                int e = 0, tg = 0, kk = 0;
-                Vec4<T> rec = zero4, rp = zero4;
-                int4 rw = make_int4(0, 0, 0, 0);
-                auto fetch = [&](int r, int& e_, int& tg_, int& kk_, Vec4<T>& rec_, int4& rw_,
-                                 Vec4<T>& rp_) {
-                    e_ = r < L ? (int)list[r] : 0;
-                    tg_ = __shfl(tag, e_ >> 6);
+                struct Entry {
+                    int e, tg, kk;
+                    Vec4<T> rec, rp;
+                    int4 rw;
+                };
+                auto fetch = [&](int r) {
+                    Entry x{0, 0, 0, zero4, zero4, make_int4(0, 0, 0, 0)};
+                    x.e = r < L ? (int)list[r] : 0;
+                    x.tg = __shfl(tag, x.e >> 6);
                     if (r < L) {
-                        const int v = chunk_cand(tg_ & 63, e_ & 63, nch);
+                        const int v = chunk_cand(x.tg & 63, x.e & 63, nch);
                         const int p = st.piece[v];
-                        kk_ = st.kid[p];
-                        rec_ = cand_record<T, STAGED>(a, st, cand, p, v);
+                        x.kk = st.kid[p];
+                        x.rec = cand_record<T, STAGED>(a, st, cand, p, v);
                         if (WRAPPED) {
-                            rw_ = a.binned_w[v + st.delta[p]];
-                            rp_ = a.binned_p[v + st.delta[p]];
+                            x.rw = a.binned_w[v + st.delta[p]];
+                            x.rp = a.binned_p[v + st.delta[p]];
                         }
                     }
+                    return x;
                 };
-                fetch(lane, e, tg, kk, rec, rw, rp);
+                Entry cur = fetch(lane);
                 for (int r0 = 0; r0 < L; r0 += kWave) {
-                    int e_n = 0, tg_n = 0, kk_n = 0;
-                    Vec4<T> rec_n = zero4, rp_n = zero4;
-                    int4 rw_n = make_int4(0, 0, 0, 0);
-                    if (r0 + kWave < L)
-                        fetch(r0 + kWave + lane, e_n, tg_n, kk_n, rec_n, rw_n, rp_n);
-                    const int g = tg >> 6;
-                    const long long o = __shfl(ob, e >> 6) + base + r0 + lane;
+                    Entry nxt{0, 0, 0, zero4, zero4, make_int4(0, 0, 0, 0)};
+                    if (r0 + kWave < L) nxt = fetch(r0 + kWave + lane);
+                    const int g = cur.tg >> 6;
+                    const long long o = __shfl(ob, cur.e >> 6) + base + r0 + lane;
                     const int si = __shfl(sidx, g);
                     if (WRAPPED) {
                         const T ps[3] = {__shfl(sp.x, g), __shfl(sp.y, g), __shfl(sp.z, g)};
                         const int4 ws = make_int4(__shfl(sw.x, g), __shfl(sw.y, g),
                                                   __shfl(sw.z, g), 0);
-                        const T pt[3] = {rp.x, rp.y, rp.z};
+                        const T pt[3] = {cur.rp.x, cur.rp.y, cur.rp.z};
                         if (r0 + lane < L)
-                            cell_write_regs<T>(a, o, si, as_idx(rec.w), kk, ps, pt, ws, rw, cb);
+                            cell_write_regs<T>(a, o, si, as_idx(cur.rec.w), cur.kk, ps, pt, ws,
+                                               cur.rw, cb);
                     } else {
                         const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                         if (r0 + lane < L)
-                            cell_write<T, false>(a, o, si, as_idx(rec.w), kk, rec.x, rec.y,
-                                                 rec.z, sx, sy, sz, cb);
+                            cell_write<T, false>(a, o, si, as_idx(cur.rec.w), cur.kk, cur.rec.x,
+                                                 cur.rec.y, cur.rec.z, sx, sy, sz, cb);
                     }
-                    e = e_n;
-                    tg = tg_n;
-                    kk = kk_n;
-                    rec = rec_n;
-                    rw = rw_n;
-                    rp = rp_n;
+                    cur = nxt;
                 }
             }
         }
@@ -1144,31 +1140,14 @@ static_assert(StageCap<float>::value % kBlock == 0 && StageCap<double>::value % 
 static_assert(StageCap<float>::value <= kMapCap && StageCap<double>::value <= kMapCap,
               "staged stencils have a piece map");
 
-// Emitting pass: one workgroup per bin, mapped XCD-aware (workgroup b runs
-// on XCD b % 8; XCD x takes the x-th eighth of the bins).  The grid is sized
-// for out->n_tasks bins; the kernel reads the batch's bin count from the
-// status words and only trusts the smaller of the two, and it can run again
-// on the same workspace.
+// Emitting pass for one bin whose stencil block_bin has built: the fast
+// path (staged candidates, no wrapped representative, at most 64 sources),
+// the decode path (emit_bin) or, beyond the piece map, the slow path.
 template <typename T, int MODE>
-__global__ __launch_bounds__(kBlock) void k_cell_emit(
-    QueryArgs<T> a) {
-    __shared__ StencilLds s_st;
-    __shared__ Vec4<T> s_cand[EmitStageCap<T>::value];
-    __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
-
-    if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
-    // the batch's bins from the count's status words; the grid may cover
-    // more (a launch sized before the count finished)
-    const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_BINS);
-    const ItemRange br = xcd_block_range(min(a.n_bins, bins));
-    const int64_t g = br.first;
-    if (g >= br.end) return;
-    StructCache sc{0, 0, 0};
-    CellBin<T> cb;
-    Vec4<T> src_all;
-    if (!block_bin<T>(a, g, sc, cb, s_st, nullptr, &src_all)) return;
-    const int wv = uniform(threadIdx.x / kWave);
-    const int lane = lane_id();
+__device__ __forceinline__ void emit_one_bin(const QueryArgs<T>& a, StencilLds& s_st,
+                                             Vec4<T>* s_cand, unsigned short* list,
+                                             CellBin<T>& cb, const Vec4<T>& src_all, int wv,
+                                             int lane) {
     if (cb.C <= EmitStageCap<T>::value && !cb.wrapped) {
         const int nsrc = cb.se - cb.sb;
         const bool fast = nsrc <= kWave;
@@ -1190,22 +1169,64 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
         if (fast) {
             // every output's byte offset below 2^32: 32-bit offsets
             if (a.limit <= (int64_t)(0xffffffffll / 16))
-                emit_fast<T, true>(a, s_st, s_cand, cb, s_list[wv], src_all, cur_all, m0, m1);
+                emit_fast<T, true>(a, s_st, s_cand, cb, list, src_all, cur_all, m0, m1);
             else
-                emit_fast<T, false>(a, s_st, s_cand, cb, s_list[wv], src_all, cur_all, m0, m1);
+                emit_fast<T, false>(a, s_st, s_cand, cb, list, src_all, cur_all, m0, m1);
         } else {
             wave_sources(cb);
-            emit_bin<T, true, false>(a, s_st, s_cand, cb, s_list[wv]);
+            emit_bin<T, true, false>(a, s_st, s_cand, cb, list);
         }
     } else if (cb.C <= kMapCap) {
         wave_sources(cb);
         if (cb.wrapped)
-            emit_bin<T, false, true>(a, s_st, s_cand, cb, s_list[wv]);
+            emit_bin<T, false, true>(a, s_st, s_cand, cb, list);
         else
-            emit_bin<T, false, false>(a, s_st, s_cand, cb, s_list[wv]);
+            emit_bin<T, false, false>(a, s_st, s_cand, cb, list);
     } else {
         wave_sources(cb);
         cell_slow<T, MODE, true>(a, s_st, cb);
+    }
+}
+
+// Emitting pass: one workgroup per bin, mapped XCD-aware (workgroup b runs
+// on XCD b % 8; XCD x takes the x-th eighth of the bins).  The grid is sized
+// for out->n_tasks bins; the kernel reads the batch's bin count from the
+// status words and only trusts the smaller of the two, and it can run again
+// on the same workspace.  STRIDED: the workgroups of a grid of any size
+// stride over the bins, for a launch that does not know the bin count.
+template <typename T, int MODE, bool STRIDED = false>
+__global__ __launch_bounds__(kBlock) void k_cell_emit(
+    QueryArgs<T> a) {
+    __shared__ StencilLds s_st;
+    __shared__ Vec4<T> s_cand[EmitStageCap<T>::value];
+    __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
+
+    if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
+    // the batch's bins from the count's status words; the grid may cover
+    // more (a launch sized before the count finished)
+    const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_BINS);
+    const ItemRange br = xcd_block_range(min(a.n_bins, bins));
+    StructCache sc{0, 0, 0};
+    const int wv = uniform(threadIdx.x / kWave);
+    const int lane = lane_id();
+    if constexpr (!STRIDED) {
+        // one bin per workgroup (the grid covers the bins)
+        const int64_t g = br.first;
+        if (g >= br.end) return;
+        CellBin<T> cb;
+        Vec4<T> src_all;
+        if (block_bin<T>(a, g, sc, cb, s_st, nullptr, &src_all))
+            emit_one_bin<T, MODE>(a, s_st, s_cand, s_list[wv], cb, src_all, wv, lane);
+    } else {
+        // a grid of any size strides over the bins (a launch that does not
+        // know the bin count)
+        for (int64_t g = br.first; g < br.end; g += br.step) {
+            CellBin<T> cb;
+            Vec4<T> src_all;
+            if (block_bin<T>(a, g, sc, cb, s_st, nullptr, &src_all))
+                emit_one_bin<T, MODE>(a, s_st, s_cand, s_list[wv], cb, src_all, wv, lane);
+            __syncthreads();  // the bin's LDS is free
+        }
     }
 }
 

@@ -213,6 +213,15 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
                                     kBlock, 0, stream>>>(q);
         if (req->algorithm != TNR_CELL_LIST)
             k_brute<T, MODE, false><<<brute_blocks<T, MODE, false>(n), kBlock, 0, stream>>>(q);
+    } else if (plan < 0) {
+        // plan and bins unknown on the host: both families, grids the device
+        // holds at once, the kernels reading plan and bins from the status
+        if (req->algorithm != TNR_BRUTE_FORCE) {
+            const int64_t cap = resident_blocks(k_cell_emit<T, MODE, true>) / 8 * 8;
+            k_cell_emit<T, MODE, true><<<(unsigned)(cap > 8 ? cap : 8), kBlock, 0, stream>>>(q);
+        }
+        if (req->algorithm != TNR_CELL_LIST)
+            k_brute<T, MODE, true><<<brute_blocks<T, MODE, true>(n), kBlock, 0, stream>>>(q);
     } else {
         if ((plan & 2) && n_tasks > 0)
             k_cell_emit<T, MODE><<<emit_blocks(n_tasks), kBlock, 0, stream>>>(q);
@@ -314,7 +323,7 @@ static hipError_t run_emit(const tnr_request* req, void* ws, const Layout& L,
     q.src = out->sources;
     q.dst = out->targets;
     q.limit = out->n_pairs;
-    q.n_bins = out->n_tasks;
+    q.n_bins = out->plan < 0 ? L.cap_bins : out->n_tasks;
     dispatch_queries<T, true>(req, L, q, out->plan, out->n_tasks, stream);
     return hipGetLastError();
 }
