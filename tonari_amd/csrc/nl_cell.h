@@ -278,7 +278,8 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
         // lane l: record of the bin's source l (l < 64), in flight during the
         // rest of the stencil build (issued after the piece bounds were used)
         const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
-        *src_pre = lane < cb.se - cb.sb ? a.binned[cb.sb + lane] : zero4;
+        *src_pre = zero4;
+        if (lane < cb.se - cb.sb) *src_pre = a.binned[cb.sb + lane];
     }
     if (lane == kWave - 1) st.wtot[wv] = inc;
     __syncthreads();  // also orders the mark clearing before the marks
@@ -660,7 +661,8 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
     for (int sg = cb.sb; sg < cb.se; sg += kWave) {
         const int ns = min(kWave, cb.se - sg);
-        const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
+        Vec4<T> sq = zero4;
+        if (lane < ns) sq = a.binned[sg + lane];
         const int sidx = as_idx(sq.w);
         long long acc = 0;  // lane gi: pairs of source gi so far
         for (int c0 = 0; c0 < cb.nch; c0 += NC) {
@@ -746,7 +748,8 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
     const int j = lane - sl * nch;
     for (int sg = cb.sb; sg < cb.se; sg += kWave) {
         const int ns = min(kWave, cb.se - sg);
-        const Vec4<T> sq = lane < ns ? a.binned[sg + lane] : zero4;
+        Vec4<T> sq = zero4;
+        if (lane < ns) sq = a.binned[sg + lane];
         const int sidx = as_idx(sq.w);
         // wrapped: the sources' wraps and original positions (binned order)
         int4 sw = make_int4(0, 0, 0, 0);
@@ -800,7 +803,10 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                     int4 rw;
                 };
                 auto fetch = [&](int r) {
-                    Entry x{0, 0, 0, zero4, zero4, make_int4(0, 0, 0, 0)};
+                    Entry x;
+                    x.kk = 0;
+                    x.rec = x.rp = Vec4<T>{T(0), T(0), T(0), T(0)};
+                    x.rw = make_int4(0, 0, 0, 0);
                     x.e = r < L ? (int)list[r] : 0;
                     x.tg = __shfl(tag, x.e >> 6);
                     if (r < L) {
@@ -817,8 +823,8 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                 };
                 Entry cur = fetch(lane);
                 for (int r0 = 0; r0 < L; r0 += kWave) {
-                    Entry nxt{0, 0, 0, zero4, zero4, make_int4(0, 0, 0, 0)};
-                    if (r0 + kWave < L) nxt = fetch(r0 + kWave + lane);
+                    // past the end, fetch returns zeros that no lane writes
+                    const Entry nxt = fetch(r0 + kWave + lane);
                     const int g = cur.tg >> 6;
                     const long long o = __shfl(ob, cur.e >> 6) + base + r0 + lane;
                     const int si = __shfl(sidx, g);
