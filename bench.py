@@ -368,7 +368,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_cell_emit<float, 0>",
+            "kernel": "k_cell_emit<float, 0, false>",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
