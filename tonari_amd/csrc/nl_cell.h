@@ -44,7 +44,9 @@ template <typename T>
 struct RegChunks;
 template <>
 struct RegChunks<float> {
-    static constexpr int value = 12;
+    // six chunks keep the float count within 80 VGPRs, six waves per SIMD
+    // (its LDS allows six workgroups per CU); twelve needed 128 VGPRs
+    static constexpr int value = 6;
 };
 template <>
 struct RegChunks<double> {
@@ -1100,7 +1102,7 @@ __device__ __forceinline__ ItemRange xcd_block_range(int64_t W) {
 // source s of a cell-list structure.  The status word is read once: abort
 // bits only come from earlier kernels.
 template <typename T, int MODE>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? 6 : 4))) void
 k_cell_count(
     QueryArgs<T> a) {
     __shared__ StencilLds s_st;
