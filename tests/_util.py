@@ -128,3 +128,61 @@ def multiset_hash_torch(pairs, shifts) -> int:
     x = x * _signed(_MIX[2])
     x = x ^ shr(x, 31)
     return int(x.sum().item()) & ((1 << 64) - 1)
+
+
+def assert_geometry_close_torch(pairs, shifts, d, D, cfg, chunk: int = 1 << 24) -> None:
+    """``assert_geometry_close`` evaluated on the tensors' device, every row.
+
+    The reference formula D = x[j] - x[i] + S @ cell[b] is evaluated in float64
+    on the device in chunks of ``chunk`` rows, so full-size outputs (10^8
+    rows) are checked without copying them to the host.  Same tolerance:
+    |D - D_ref| <= rtol * (|D_ref| + cutoff) componentwise, and the same for
+    d, with rtol 1e-5 (float32) or 1e-12 (float64).
+    """
+    import torch
+
+    dev = pairs.device
+    pos = torch.as_tensor(cfg["positions"]).to(dev, torch.float64)
+    cell = torch.as_tensor(cfg["cell"]).to(dev, torch.float64)
+    bounds = torch.as_tensor(cfg["batch_ptr"][1:]).to(dev)
+    rtol = geometry_tolerance(cfg["positions"].dtype)
+    rc = cfg["cutoff"]
+    for lo in range(0, pairs.shape[0], chunk):
+        hi = min(lo + chunk, pairs.shape[0])
+        p = pairs[lo:hi]
+        b = torch.bucketize(p[:, 0], bounds, right=True)
+        ref = pos[p[:, 1]] - pos[p[:, 0]]
+        ref += torch.bmm(shifts[lo:hi].to(torch.float64).unsqueeze(1),
+                         cell[b].contiguous()).squeeze(1)
+        if D is not None:
+            err = (D[lo:hi].to(torch.float64) - ref).abs()
+            bad = err > rtol * (ref.abs() + rc)
+            assert not bool(bad.any()), (
+                f"D differs at rows {(torch.nonzero(bad.any(1))[:5, 0] + lo).tolist()}")
+        if d is not None:
+            dref = torch.linalg.vector_norm(ref, dim=1)
+            bad = (d[lo:hi].to(torch.float64) - dref).abs() > rtol * (dref + rc)
+            assert not bool(bad.any()), (
+                f"d differs at rows {(torch.nonzero(bad)[:5, 0] + lo).tolist()}")
+        del p, b, ref
+
+
+def shifts_from_vectors(pairs, D, cfg):
+    """Integer shifts S recovered from D = x[j] - x[i] + S @ cell[b] (rounded).
+
+    For outputs that carry D but not S (C4's 'PD'): S = round((D - (x[j] -
+    x[i])) @ inv(cell[b])), exact whenever D is within far less than half a
+    cell vector of the formula, which the d/D tolerance check then confirms
+    row by row.
+    """
+    import torch
+
+    dev = pairs.device
+    pos = torch.as_tensor(cfg["positions"]).to(dev, torch.float64)
+    cell = torch.as_tensor(cfg["cell"]).to(dev, torch.float64)
+    inv = torch.linalg.inv(cell.cpu()).to(dev)
+    bounds = torch.as_tensor(cfg["batch_ptr"][1:]).to(dev)
+    b = torch.bucketize(pairs[:, 0], bounds, right=True)
+    frac = D.to(torch.float64) - (pos[pairs[:, 1]] - pos[pairs[:, 0]])
+    S = torch.bmm(frac.unsqueeze(1), inv[b].contiguous()).squeeze(1)
+    return torch.round(S).to(torch.int32)

@@ -393,15 +393,31 @@ def _golden():
 
 @pytest.mark.parametrize("name", ["C2", "C3", "C4", "C5"])
 def test_full_size_matches_golden(name):
-    from tests._util import multiset_hash_torch
+    """The configuration's own call (its quantities, as the benchmark runs it).
+
+    The (i, j, S) multiset goes through the golden checksum; S comes from the
+    output when requested, is zero for a non-periodic batch (C3), and is
+    recovered from D for C4's 'PD'.  Every row of d and D is checked against
+    the float64 formula on the device.
+    """
+    from tests._util import (assert_geometry_close_torch, multiset_hash_torch,
+                             shifts_from_vectors)
     from tests.golden.cases import CASES
 
     make, options = CASES[name]
     cfg = dict(make(), **options)
     entry = _golden()[name]
-    print(f"[golden] {name}: {len(cfg['positions'])} atoms, expecting {entry['pairs']} pairs",
-          flush=True)
-    P, S = gpu("PS", cfg)
+    quantities = cfg["quantities"]
+    print(f"[golden] {name}: {len(cfg['positions'])} atoms, '{quantities}', expecting "
+          f"{entry['pairs']} pairs", flush=True)
+    out = dict(zip(quantities, gpu(quantities, cfg)))
+    P = out["P"] if "P" in out else torch.stack([out["i"], out["j"]], 1)
+    if "S" in out:
+        S = out["S"]
+    elif not cfg["pbc"].any():
+        S = torch.zeros((P.shape[0], 3), dtype=torch.int32, device=P.device)
+    else:
+        S = shifts_from_vectors(P, out["D"], cfg)
     assert P.shape[0] == entry["pairs"]
     assert f"{multiset_hash_torch(P, S):016x}" == entry["multiset"]
     if cfg.get("sorted", False):
@@ -412,7 +428,36 @@ def test_full_size_matches_golden(name):
         import oracle
 
         assert oracle.key_hash(P.cpu().numpy(), S.cpu().numpy()) == entry["sha256"]
-    del P, S
+    assert_geometry_close_torch(P, S, out.get("d"), out.get("D"), cfg)
+    del P, S, out
+    torch.cuda.empty_cache()
+
+
+def test_float64_vectors_past_32bit_byte_offsets():
+    """Float64 D rows (24 bytes) beyond 2^32 / 24 = 178,956,970 rows.
+
+    The emitting fast path stores with 32-bit byte offsets only while every
+    row of every requested output fits below 2^32 bytes; the widest row
+    decides (D of float64).  A single periodic box at density 0.1 and rc
+    7.1 A gives about 150 neighbours per atom (stencils the emit stages in
+    LDS) and, with 1.3 M atoms, more than 190 M pairs.  Every D row is
+    checked against the float64 formula, so a row written at a wrapped
+    offset (or one left unwritten) fails.
+    """
+    n, density, rc = 1_300_000, 0.1, 7.1
+    rng = np.random.Generator(np.random.PCG64(1771))
+    edge = (n / density) ** (1.0 / 3.0)
+    cfg = single(rng.uniform(0.0, edge, size=(n, 3)), edge * np.eye(3), [1, 1, 1], rc,
+                 np.float64)
+    print(f"[off32] {n} atoms, float64 'PSD', rc {rc}", flush=True)
+    P, S, D = gpu("PSD", cfg, algorithm="cell_list")
+    limit = 0xFFFFFFFF // 24
+    print(f"[off32] {P.shape[0]} pairs (32-bit limit of D rows {limit})", flush=True)
+    assert P.shape[0] > limit + 1_000_000
+    from tests._util import assert_geometry_close_torch
+
+    assert_geometry_close_torch(P, S, None, D, cfg)
+    del P, S, D
     torch.cuda.empty_cache()
 
 

@@ -44,8 +44,11 @@ def neighbor_list(
     ``batch_ptr`` optional int64 (B + 1,) structure boundaries.  Pairs have
     squared distance strictly below ``cutoff**2``; ``half_list`` keeps the
     lexicographically smaller of (i, j, S) and (j, i, -S); ``include_self``
-    adds the zero-shift self pair of every atom.  The output is always grouped
-    by source in increasing index order, so ``sorted=True`` costs nothing.
+    adds the zero-shift self pair of every atom.  The pairs of a source are
+    always contiguous.  With ``sorted=True`` sources come in increasing index
+    order.  Without it, sources come in cell-list bin order when every
+    structure of the call is searched with a cell list, and in index order
+    otherwise; the order of targets within a source is unspecified.
     """
     if not isinstance(quantities, str):
         raise TypeError("quantities must be a string")

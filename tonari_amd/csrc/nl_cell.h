@@ -862,6 +862,14 @@ __device__ __forceinline__ int emit_group_size(int nsrc, int nch) {
     return (nsrc + groups - 1) / groups;
 }
 
+// Largest pair count whose every output byte offset fits in 32 bits: the
+// widest requested row is P (16 bytes) or, for float64, D (24 bytes).
+template <typename T>
+__device__ __forceinline__ int64_t off32_limit(const QueryArgs<T>& a) {
+    const int64_t widest = a.vec != nullptr && 3 * sizeof(T) > 16 ? 3 * sizeof(T) : 16;
+    return (int64_t)0xffffffffll / widest;
+}
+
 // Emitting fast path: staged candidates, no wrapped representative (the
 // output shift is the image shift k and positions are the records).  The
 // decode of emit_bin, except that a list entry holds the source's lane in
@@ -1140,6 +1148,19 @@ k_cell_count(
             }
         }
     }
+    if ((plan & 1) && a.brute_in_cell) {
+        // brute-force structures of an explicit cell_list request (no bin
+        // grid fits them): one wave per work unit, atoms read from global
+        // memory, the per-source cursors in the candidate staging area
+        static_assert(sizeof(s_cand) >= kWavesPerBlock * sizeof(BruteCursor),
+                      "brute-force cursors fit the staging area");
+        BruteCursor* cur = reinterpret_cast<BruteCursor*>(s_cand);
+        const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
+        const int wv = uniform(threadIdx.x / kWave);
+        const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+        for (int64_t u = (int64_t)blockIdx.x * kWavesPerBlock + wv; u < units; u += nwaves)
+            brute_unit<T, MODE, false, false>(a, u, nullptr, cur[wv]);
+    }
 }
 
 static_assert(kMapCap == kMaskWords * kWave, "one mask word per chunk of the piece map");
@@ -1176,7 +1197,7 @@ __device__ __forceinline__ void emit_one_bin(const QueryArgs<T>& a, StencilLds& 
         stage_candidates<T, EmitStageCap<T>::value>(a, s_st, cb.C, s_cand);
         if (fast) {
             // every output's byte offset below 2^32: 32-bit offsets
-            if (a.limit <= (int64_t)(0xffffffffll / 16))
+            if (a.limit <= off32_limit(a))
                 emit_fast<T, true>(a, s_st, s_cand, cb, list, src_all, cur_all, m0, m1);
             else
                 emit_fast<T, false>(a, s_st, s_cand, cb, list, src_all, cur_all, m0, m1);

@@ -720,10 +720,12 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
             }
         }
         best = __builtin_amdgcn_readfirstlane(best);
-        // an explicit cell_list request is never served by brute force: a
-        // structure no bin grid fits (only beyond about 2^24 atoms) is a
-        // capacity error
-        if (!(cost < INFINITY) && requested == TNR_CELL_LIST) st |= ST_CAPACITY;
+        // A structure that no bin grid fits stays with brute force, whose
+        // pairs are the same set.  This happens where the cutoff spans two or
+        // more cell widths on every periodic axis (one bin per axis, a reach
+        // of three bins: 7^3 stencil pieces, beyond kPieceCap), or beyond
+        // about 2^24 atoms.  An explicit cell_list request then has its
+        // brute-force structures counted by the cell-list counting kernel.
         if (cost < INFINITY) {
             algo = ALGO_CELL;
             nbins = (int64_t)__shfl(bins_f, best);

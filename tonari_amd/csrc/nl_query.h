@@ -38,6 +38,11 @@ struct QueryArgs {
     // position, so sources take the outputs in binned order and every
     // emitting workgroup writes one contiguous range; otherwise by atom index
     int by_bin;
+    // count: the cell-list counting kernel also counts the brute-force
+    // structures (an explicit cell_list request, whose count launches no
+    // brute-force kernel; the planner gives such a request brute-force
+    // structures only where no bin grid fits)
+    int brute_in_cell;
     int64_t limit;  // E: emit never writes at or beyond it
     int64_t n_bins; // emit: cell-list bins covered by the grid (at least the batch's)
     // outputs (emit)
@@ -362,17 +367,21 @@ __device__ __forceinline__ int unit_structure(const int64_t* off, int64_t nb, in
 // Atoms of a structure staged in LDS per wave (structures up to this size).
 constexpr int kBruteStage = 128;
 
-// Per-wave LDS of the brute-force kernels: the structure's atoms and, per
-// source of the unit, its pair count (counting) or next output (emitting).
+// Per source of a brute-force work unit: its pair count (counting) or its
+// next output (emitting).
+union BruteCursor {
+    int cnt[kBruteGroupCap];
+    long long cur[kBruteGroupCap];
+};
+
+// Per-wave LDS of the brute-force kernels: the structure's atoms and the
+// unit's per-source cursors.
 template <typename T>
 struct BruteLds {
     Vec4<T> q[kBruteStage];
     int4 w[kBruteStage];
     Vec4<T> p[kBruteStage];
-    union {
-        int cnt[kBruteGroupCap];
-        long long cur[kBruteGroupCap];
-    };
+    BruteCursor c;
 };
 
 __device__ __forceinline__ void wave_lds_fence() {
@@ -414,9 +423,13 @@ __device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G) {
 // wave's LDS first.  Counting adds each lane's pairs to its source's count
 // (one LDS add per source run of the round) and stores counts[s] at the end;
 // emitting places a source's pairs from offsets[s] on, carrying its next
-// output position from round to round in LDS.
-template <typename T, int MODE, bool EMIT>
-__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, BruteLds<T>& L) {
+// output position from round to round in LDS.  Without STAGE (L null) the
+// atoms are always read from global memory and only the cursors C live in
+// LDS: the form the cell-list counting kernel runs for the structures of an
+// explicit cell_list request that no bin grid fits.
+template <typename T, int MODE, bool EMIT, bool STAGE = true>
+__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, BruteLds<T>* L,
+                                           BruteCursor& C) {
     const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
     const StructRec& r = a.recs[b];
     BruteGeom<T> g;
@@ -425,28 +438,28 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, Bru
     const int f = (int)(u - r.unit0) * r.bgroup;
     const int G = min(r.bgroup, n - f);
     const int lane = lane_id();
-    const bool staged = n <= kBruteStage;
+    const bool staged = STAGE && n <= kBruteStage;
     if (staged) {
         for (int i = lane; i < n; i += kWave) {
             const WalkAtom<T> x = walk_atom(a, a0 + i);
-            L.q[i] = x.q;
-            L.w[i] = x.w;
-            L.p[i] = Vec4<T>{x.p[0], x.p[1], x.p[2], T(0)};
+            L->q[i] = x.q;
+            L->w[i] = x.w;
+            L->p[i] = Vec4<T>{x.p[0], x.p[1], x.p[2], T(0)};
         }
     }
     for (int x = lane; x < G; x += kWave) {
         if (EMIT)
-            L.cur[x] = a.offsets[a0 + f + x];
+            C.cur[x] = a.offsets[a0 + f + x];
         else
-            L.cnt[x] = 0;
+            C.cnt[x] = 0;
     }
     wave_lds_fence();
     auto atom = [&](int i) {
         WalkAtom<T> x;
         if (staged) {
-            x.q = L.q[i];
-            x.w = L.w[i];
-            const Vec4<T> p = L.p[i];
+            x.q = L->q[i];
+            x.w = L->w[i];
+            const Vec4<T> p = L->p[i];
             x.p[0] = p.x;
             x.p[1] = p.y;
             x.p[2] = p.z;
@@ -471,22 +484,22 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, Bru
             (seg_hi >= kWave ? ~0ull : ((1ull << seg_hi) - 1ull)) & ~((1ull << seg_lo) - 1ull);
         const WalkAtom<T> xs = atom(li), xt = atom(tl);
         if constexpr (EMIT) {
-            long long cursor = L.cur[x];
+            long long cursor = C.cur[x];
             pair_images<T, MODE, 1>(a, g, valid, a0 + li, a0 + tl, xs, xt, seg, cursor);
             wave_lds_fence();
-            if (valid && lane == seg_hi - 1) L.cur[x] = cursor;
+            if (valid && lane == seg_hi - 1) C.cur[x] = cursor;
         } else {
             long long unused = 0;
             const int h = pair_images<T, MODE, 0>(a, g, valid, a0 + li, a0 + tl, xs, xt, seg,
                                                   unused);
             const int incl = wave_inclusive_scan_i32(h);
             const int before = __shfl(incl, max(seg_lo - 1, 0));
-            if (valid && lane == seg_hi - 1) L.cnt[x] += incl - (seg_lo > 0 ? before : 0);
+            if (valid && lane == seg_hi - 1) C.cnt[x] += incl - (seg_lo > 0 ? before : 0);
         }
         wave_lds_fence();
     }
     if (!EMIT)
-        for (int x = lane; x < G; x += kWave) a.counts[a0 + f + x] = L.cnt[x];
+        for (int x = lane; x < G; x += kWave) a.counts[a0 + f + x] = C.cnt[x];
     wave_lds_fence();
 }
 
@@ -503,7 +516,8 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
     const int wv = uniform(threadIdx.x / kWave);
     const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-    for (int64_t u = wave0; u < units; u += nwaves) brute_unit<T, MODE, EMIT>(a, u, s_lds[wv]);
+    for (int64_t u = wave0; u < units; u += nwaves)
+        brute_unit<T, MODE, EMIT>(a, u, &s_lds[wv], s_lds[wv].c);
 }
 
 }  // namespace tnr

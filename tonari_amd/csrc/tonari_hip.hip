@@ -116,17 +116,18 @@ static unsigned blocks_for(int64_t n, int per = kBlock) {
 }
 
 // Workgroups a kernel keeps resident on the whole device (occupancy x
-// CUs).  Looked up once per device and kernel and cached (the only state the
-// library keeps; it is idempotent and safe under concurrent use).
-template <typename K>
-static int64_t resident_blocks(K kernel) {
+// CUs).  Looked up once per device and kernel (one cache per template
+// argument, that is per kernel) and cached: the only state the library
+// keeps; it is idempotent and safe under concurrent use.
+template <auto Kernel>
+static int64_t resident_blocks() {
     static std::atomic<int> cache[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     int v = cache[dev].load(std::memory_order_relaxed);
     if (v > 0) return v;
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kBlock, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, kBlock, 0) != hipSuccess ||
         per_cu <= 0)
         per_cu = 2;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
@@ -143,7 +144,7 @@ static int64_t resident_blocks(K kernel) {
 template <typename T, int MODE>
 static unsigned count_blocks(int64_t work_waves) {
     const int64_t want = (work_waves + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = resident_blocks(k_cell_count<T, MODE>) / 8 * 8;
+    const int64_t cap = resident_blocks<k_cell_count<T, MODE>>() / 8 * 8;
     int64_t b = want < cap ? want : cap;
     b = (b + 7) / 8 * 8;
     return (unsigned)(b > 0 ? b : 8);
@@ -162,7 +163,7 @@ static unsigned emit_blocks(int64_t bins) {
 template <typename T, int MODE, bool EMIT>
 static unsigned brute_blocks(int64_t n) {
     const int64_t want = (n + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = resident_blocks(k_brute<T, MODE, EMIT>);
+    const int64_t cap = resident_blocks<k_brute<T, MODE, EMIT>>();
     const int64_t b = want < cap ? want : cap;
     return (unsigned)(b > 0 ? b : 1);
 }
@@ -189,16 +190,17 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.n_atoms = req->n_atoms;
     q.nb = req->n_structures;
     q.by_bin = req->sorted ? 0 : 1;
+    q.brute_in_cell = req->algorithm == TNR_CELL_LIST ? 1 : 0;
     return q;
 }
 
 // Counting: the plan is only known on the device, so with auto both
 // families are launched and each exits at once when the plan has none of
 // its structures.  An explicit brute_force request launches the brute-force
-// kernel only, an explicit cell_list request the cell-list kernel only (the
-// planner turns every structure of such a request into a cell list or an
-// error).  Emitting: plan bit 0 launches
-// the brute-force family, bit 1 the cell-list family over n_tasks bins (one
+// kernel only, an explicit cell_list request the cell-list kernel only,
+// which also counts the structures that no bin grid fits (brute force,
+// QueryArgs::brute_in_cell).  Emitting: plan bit 0 launches the
+// brute-force family, bit 1 the cell-list family over n_tasks bins (one
 // workgroup each).
 template <typename T, int MODE, bool EMIT>
 static void launch_queries(const tnr_request* req, const Layout& L, const QueryArgs<T>& q,
@@ -217,11 +219,10 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
         // plan and bins unknown on the host: both families, grids the device
         // holds at once, the kernels reading plan and bins from the status
         if (req->algorithm != TNR_BRUTE_FORCE) {
-            const int64_t cap = resident_blocks(k_cell_emit<T, MODE, true>) / 8 * 8;
+            const int64_t cap = resident_blocks<k_cell_emit<T, MODE, true>>() / 8 * 8;
             k_cell_emit<T, MODE, true><<<(unsigned)(cap > 8 ? cap : 8), kBlock, 0, stream>>>(q);
         }
-        if (req->algorithm != TNR_CELL_LIST)
-            k_brute<T, MODE, true><<<brute_blocks<T, MODE, true>(n), kBlock, 0, stream>>>(q);
+        k_brute<T, MODE, true><<<brute_blocks<T, MODE, true>(n), kBlock, 0, stream>>>(q);
     } else {
         if ((plan & 2) && n_tasks > 0)
             k_cell_emit<T, MODE><<<emit_blocks(n_tasks), kBlock, 0, stream>>>(q);
