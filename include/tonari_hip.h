@@ -131,6 +131,26 @@ int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
              const tnr_outputs* out, void* stream, char* err, size_t err_len);
 
 /*
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tnr_count_async followed by tnr_emit, on a static
+ * scratch array of 64 MiB per GPU inside the library instead of a caller
+ * workspace.  It allocates nothing and does not wait on the host.  The
+ * caller passes the inputs (req) and outputs of a chosen capacity
+ * (out->n_pairs rows; out->plan and out->n_tasks are ignored: the emit reads
+ * them from the count on the device).  Once `stream` has completed,
+ * tnr_count_finish(host_result) reports errors and E; when E exceeds the
+ * capacity, the rows beyond it were not written and the call must be
+ * repeated with larger outputs.  Requests whose tnr_workspace_size exceeds
+ * 64 MiB (one structure of more than about 176,000 float32 or 156,000
+ * float64 atoms) are rejected with TNR_INPUT_ERROR before any device work.
+ * Every call on one GPU uses that GPU's one array: calls that overlap on a
+ * GPU (two streams, two threads) race and must be serialised by the caller.
+ */
+int tnr_search_static(const tnr_request* req, const tnr_outputs* out, int64_t* host_result,
+                      void* stream, char* err, size_t err_len);
+
+/*
  * Backward of the d/D outputs of tnr_emit: adds the gradients of positions
  * (T[N][3]) and cell (T[B][3][3]) into grad_positions and grad_cell (set to
  * zero by the caller) from grad_vectors (dL/dD, T[E][3]) and grad_distances

@@ -183,3 +183,14 @@ def test_status_priority_follows_reference_order(lib):
 def test_finish_reports_pair_count(lib):
     code, text, n = _finish(lib, 0, 12345)
     assert code == ext.TNR_OK and n == 12345
+
+
+def test_static_search_rejects_requests_beyond_its_scratch(lib):
+    # 400,000 float32 atoms need more than the 64 MiB static scratch; the
+    # check happens before any device work
+    req = _request(n_atoms=400_000)
+    assert lib.tnr_workspace_size(ctypes.byref(req)) > 64 << 20
+    err = ctypes.create_string_buffer(256)
+    code = lib.tnr_search_static(ctypes.byref(req), None, None, None, err, len(err))
+    assert code == ext.TNR_INPUT_ERROR
+    assert "static scratch holds 67108864 bytes" in err.value.decode()

@@ -1,0 +1,140 @@
+"""GPU: the allocation-free entry point ``tnr_search_static`` against ``tnr_count`` + ``tnr_emit``.
+
+``tnr_search_static`` runs the same count and emit on the library's static
+scratch array instead of a caller workspace, with outputs of a capacity the
+caller chooses.  Calls in a row share that array: the second, smaller call
+must not see the first one's bins, counts or tickets.  Both entry points are
+called through the C ABI; the (i, j, S) rows must be the same multiset and
+every row's d and D bit-identical.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from tonari_amd import _extensions as ext
+from tonari_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _tensors(cfg):
+    return {k: torch.as_tensor(cfg[k]).to(DEV) for k in ("positions", "cell", "pbc", "batch_ptr")}
+
+
+def _request(cfg, t):
+    pos = t["positions"]
+    return ext.Request(
+        dtype=0 if pos.dtype == torch.float32 else 1, algorithm=ext.ALGORITHMS[cfg["algorithm"]],
+        n_atoms=pos.shape[0], n_structures=t["batch_ptr"].numel() - 1,
+        positions=pos.data_ptr(), batch_ptr=t["batch_ptr"].data_ptr(),
+        cell=t["cell"].data_ptr(), pbc=t["pbc"].data_ptr(), cutoff=cfg["cutoff"],
+        half_list=int(cfg.get("half_list", False)), include_self=int(cfg.get("include_self", False)),
+        sorted=int(cfg.get("sorted", False)), stencil_reach=0,
+    )
+
+
+def _outputs(rows, dtype, plan=0, bins=0):
+    out = {"P": torch.empty((rows, 2), dtype=torch.int64, device=DEV),
+           "S": torch.empty((rows, 3), dtype=torch.int32, device=DEV),
+           "d": torch.empty((rows,), dtype=dtype, device=DEV),
+           "D": torch.empty((rows, 3), dtype=dtype, device=DEV)}
+    ptrs = ext.Outputs(n_pairs=rows, plan=plan, n_tasks=bins, pairs=out["P"].data_ptr(),
+                       shifts=out["S"].data_ptr(), distances=out["d"].data_ptr(),
+                       vectors=out["D"].data_ptr(), sources=None, targets=None)
+    return out, ptrs
+
+
+def _with_workspace(lib, cfg, t):
+    """The existing entry points: tnr_count, then tnr_emit into exact-size outputs."""
+    req = _request(cfg, t)
+    err = ctypes.create_string_buffer(512)
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    ws_bytes = lib.tnr_workspace_size(ctypes.byref(req))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    host = torch.empty(ext.HOST_RESULT_SLOTS, dtype=torch.int64, pin_memory=True)
+    n = ctypes.c_int64(0)
+    assert lib.tnr_count(ctypes.byref(req), ws.data_ptr(), ws_bytes, host.data_ptr(), stream,
+                         ctypes.byref(n), err, len(err)) == 0, err.value
+    out, ptrs = _outputs(n.value, t["positions"].dtype, int(host[3]), int(host[4]))
+    assert lib.tnr_emit(ctypes.byref(req), ws.data_ptr(), ws_bytes, ctypes.byref(ptrs), stream,
+                        err, len(err)) == 0, err.value
+    torch.cuda.synchronize()
+    return out
+
+
+def _static(lib, cfg, t, capacity):
+    """tnr_search_static into outputs of `capacity` rows; returns (E, outputs)."""
+    req = _request(cfg, t)
+    err = ctypes.create_string_buffer(512)
+    stream = torch.cuda.current_stream(DEV).cuda_stream
+    host = torch.empty(ext.HOST_RESULT_SLOTS, dtype=torch.int64, pin_memory=True)
+    out, ptrs = _outputs(capacity, t["positions"].dtype)
+    assert lib.tnr_search_static(ctypes.byref(req), ctypes.byref(ptrs), host.data_ptr(), stream,
+                                 err, len(err)) == 0, err.value
+    torch.cuda.synchronize()
+    n = ctypes.c_int64(0)
+    assert lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err)) == 0, err.value
+    return n.value, out
+
+
+def _rows(out, count):
+    """Rows (i, j, Sx, Sy, Sz, d, D) sorted by (i, j, S), as host arrays."""
+    keys = np.concatenate([out["P"][:count].cpu().numpy(),
+                           out["S"][:count].cpu().numpy().astype(np.int64)], axis=1)
+    order = np.lexsort(tuple(keys[:, c] for c in range(4, -1, -1)))
+    return keys[order], out["d"][:count].cpu().numpy()[order], out["D"][:count].cpu().numpy()[order]
+
+
+def _assert_same(a, b):
+    ka, da, Da = a
+    kb, db, Db = b
+    assert ka.shape == kb.shape and np.array_equal(ka, kb)
+    assert np.array_equal(da, db) and np.array_equal(Da, Db)
+
+
+def _case(lib, name, cfg, slack):
+    t = _tensors(cfg)
+    print(f"[no-alloc] {name}: {len(cfg['positions'])} atoms", flush=True)
+    ref = _with_workspace(lib, cfg, t)
+    count = ref["P"].shape[0]
+    got_count, got = _static(lib, cfg, t, count + slack)
+    assert got_count == count
+    _assert_same(_rows(got, count), _rows(ref, count))
+    return count
+
+
+def test_static_scratch_matches_workspace_entry_points():
+    lib = ext.load_torch_hip()
+    # two calls in a row, the second with a smaller input of the same kind
+    big = _case(lib, "C4", W.c4(), slack=1000)
+    small = _case(lib, "C4 at 20k atoms", W.c4(seed=77, n_atoms=20_000), slack=0)
+    assert 0 < small < big
+    # a batch after them (brute force and half list), then a sorted cell-list batch
+    _case(lib, "C2 subset", dict(W.c2(n_structures=48), half_list=True), slack=5)
+    _case(lib, "C5 subset", W.c5(n_structures=3, n_min=2000, n_max=4000), slack=0)
+
+
+def test_static_scratch_reports_a_count_beyond_capacity():
+    lib = ext.load_torch_hip()
+    cfg = W.c4(seed=78, n_atoms=5_000)
+    t = _tensors(cfg)
+    count = _with_workspace(lib, cfg, t)["P"].shape[0]
+    got_count, _ = _static(lib, cfg, t, count // 2)
+    assert got_count == count
+
+
+def test_static_scratch_rejects_requests_beyond_its_size():
+    lib = ext.load_torch_hip()
+    req = ext.Request(dtype=0, algorithm=0, n_atoms=400_000, n_structures=1, positions=0,
+                      batch_ptr=0, cell=0, pbc=0, cutoff=6.0)
+    err = ctypes.create_string_buffer(512)
+    code = lib.tnr_search_static(ctypes.byref(req), None, None, None, err, len(err))
+    assert code == ext.TNR_INPUT_ERROR
+    assert b"static scratch" in err.value

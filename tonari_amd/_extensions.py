@@ -28,6 +28,7 @@ EXPORTS = (
     "tnr_count_finish",
     "tnr_geometry_backward",
     "tnr_emit",
+    "tnr_search_static",
 )
 
 
@@ -106,6 +107,11 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     lib.tnr_emit.argtypes = [
         ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(Outputs),
         ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_search_static.restype = ctypes.c_int
+    lib.tnr_search_static.argtypes = [
+        ctypes.POINTER(Request), ctypes.POINTER(Outputs), ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_char_p, ctypes.c_size_t,
     ]
     version = lib.tnr_abi_version()
     if version != ABI_VERSION:

@@ -49,6 +49,7 @@
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 
 namespace tnr {
 
@@ -396,6 +397,39 @@ static int check_request(const tnr_request* req, size_t ws_bytes, const void* ws
     return TNR_OK;
 }
 
+// ------------------------------------------------------- static scratch
+// Device memory of tnr_search_static, for callers that cannot allocate: one
+// array per GPU the library runs on (the runtime gives each device its own
+// copy, at its own address), held until the process ends.  Host code never
+// passes the array's name to a kernel or a copy: it is a host-side stand-in,
+// not a device address.  scratch_address() looks up the device address once
+// per device (with that device current) and every later use goes through it.
+constexpr size_t kStaticScratchBytes = size_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_lock;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(void** out, char* err, size_t err_len) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return put_error(err, err_len, TNR_DEVICE_ERROR, "device index beyond the library's table");
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
+        if (!ptr || ((uintptr_t)ptr & 255) != 0)
+            return put_error(err, err_len, TNR_DEVICE_ERROR, "static scratch has no usable address");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return TNR_OK;
+}
+
 }  // namespace tnr
 
 // ----------------------------------------------------------------- C ABI
@@ -477,6 +511,31 @@ int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
                              : tnr::run_emit<double>(req, workspace, L, out, s);
     if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
     return TNR_OK;
+}
+
+int tnr_search_static(const tnr_request* req, const tnr_outputs* out, int64_t* host_result,
+                      void* stream, char* err, size_t err_len) {
+    if (!req) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "request is null");
+    const size_t need = tnr_workspace_size(req);
+    if (need > tnr::kStaticScratchBytes) {
+        char msg[192];
+        std::snprintf(msg, sizeof(msg),
+                      "request needs %zu bytes of scratch; the static scratch holds %zu "
+                      "bytes (use tnr_count / tnr_emit with a workspace)",
+                      need, tnr::kStaticScratchBytes);
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, msg);
+    }
+    void* ws = nullptr;
+    int rc = tnr::scratch_address(&ws, err, err_len);
+    if (rc != TNR_OK) return rc;
+    rc = tnr_count_async(req, ws, tnr::kStaticScratchBytes, host_result, stream, err, err_len);
+    if (rc != TNR_OK || !out || out->n_pairs <= 0) return rc;
+    // the emit reads the plan and the bins from the count's status words on
+    // the device (no host wait), and drops pairs beyond out->n_pairs rows
+    tnr_outputs o = *out;
+    o.plan = -1;
+    o.n_tasks = 0;
+    return tnr_emit(req, ws, tnr::kStaticScratchBytes, &o, stream, err, err_len);
 }
 
 int tnr_geometry_backward(int32_t dtype, int64_t n_pairs, int64_t n_atoms, int64_t n_structures,
