@@ -205,41 +205,177 @@ def time_backward(cfg, t, reps: int):
     return result
 
 
-def cpu_baseline(cfg, mode: str):
-    """The reference CPU core (or the restatement) on the same workload, all host cores."""
+def cpu_quantities(quantities, positions, cell, batch_ptr, pairs, shifts):
+    """The reference frontend's assembly of i/j/d/D, on CPU tensors.
+
+    Restates ``src/tonari/_torch_frontend.py:78-105`` (bucketize of the
+    sources into structures, gathers, einsum of S with the cells, vector
+    norm), so the CPU baseline's "public call" variant pays what the
+    reference's public CPU call pays after its native search.
+    """
+    import torch
+
+    values = {"P": pairs, "S": shifts}
+    source, target = pairs[:, 0], pairs[:, 1]
+    if "i" in quantities:
+        values["i"] = source.contiguous()
+    if "j" in quantities:
+        values["j"] = target.contiguous()
+    if "d" in quantities or "D" in quantities:
+        pair_batch = torch.bucketize(source.contiguous(), batch_ptr[1:], right=True)
+        values["D"] = positions[target] - positions[source] + torch.einsum(
+            "ei,eij->ej", shifts.to(positions.dtype), cell[pair_batch])
+        if "d" in quantities:
+            values["d"] = torch.linalg.vector_norm(values["D"], dim=1)
+    return tuple(values[q] for q in quantities)
+
+
+def time_cpu(fn, warmup_s: float, budget_s: float, min_reps: int = 3, max_reps: int = 7):
+    """Warm up for at least warmup_s (at least one call), then repeat until max_reps
+    samples or budget_s elapsed (at least min_reps); median of the samples.
+
+    The method of ``benchmarks/run_cpu_benchmark.py:120-161`` (time-based warm-up,
+    median of repeats), with the repeats bounded by time.
+    """
+    t0 = time.perf_counter()
+    warm = 0
+    while warm == 0 or time.perf_counter() - t0 < warmup_s:
+        out = fn()
+        warm += 1
+        del out
+    samples = []
+    t1 = time.perf_counter()
+    while len(samples) < max_reps and (len(samples) < min_reps or
+                                       time.perf_counter() - t1 < budget_s):
+        s = time.perf_counter()
+        out = fn()
+        samples.append(time.perf_counter() - s)
+        del out
+    return statistics.median(samples), len(samples), warm
+
+
+def cpu_baseline(name, cfg, mode: str, budget_s: float = 8.0):
+    """The reference CPU path on the same workload, with every host core.
+
+    Two variants (the north star's CPU baseline): the native search alone
+    (P and S, as the reference's CPU provider returns them), and the public
+    call, which also assembles the configuration's quantities from P and S
+    with torch on the CPU as the reference frontend does.  The native search
+    is the reference's own CPU core built from its sources (oracle/_ref) when
+    present, else this repository's restatement of it (oracle/).
+    """
+    import torch
+
     import oracle
 
     kind = "reference" if mode in ("auto", "reference") and oracle.available("reference") else "port"
     if mode == "reference" and kind != "reference":
         log("oracle/_ref is not built; using the restatement")
     cores = len(os.sched_getaffinity(0))
-    call = lambda: oracle.neighbor_pairs(  # noqa: E731
-        cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"],
-        half_list=cfg["half_list"], include_self=cfg["include_self"],
-        algorithm=cfg["algorithm"], threads=cores, kind=kind)
-    t0 = time.perf_counter()
-    pairs, _ = call()
-    n_pairs = len(pairs)
-    del pairs
-    samples = []
-    while len(samples) < 7 and (time.perf_counter() - t0) < 30.0:
-        s = time.perf_counter()
-        out = call()
-        samples.append(time.perf_counter() - s)
+    torch.set_num_threads(cores)
+    positions = torch.from_numpy(cfg["positions"])
+    cell = torch.from_numpy(cfg["cell"])
+    batch_ptr = torch.from_numpy(cfg["batch_ptr"])
+    algorithm = cfg["algorithm"]
+
+    def native():
+        return oracle.neighbor_pairs(
+            cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"],
+            half_list=cfg["half_list"], include_self=cfg["include_self"],
+            algorithm=algorithm, threads=cores, kind=kind)
+
+    def public():
+        P, S = native()
+        return cpu_quantities(cfg["quantities"], positions, cell, batch_ptr,
+                              torch.from_numpy(P), torch.from_numpy(S))
+
+    pairs = len(native()[0])
+    res = {"unit": "M pairs/s", "cores": cores, "kind": kind, "n_pairs": pairs}
+    for variant, fn in (("native_PS", native), ("public", public)):
+        med, reps, warm = time_cpu(fn, 1.0, budget_s)
+        res[variant] = {"value": round(pairs / med / 1e6, 3), "ms_per_call": round(med * 1e3, 3),
+                        "repeats": reps, "warmup_calls": warm}
+    res["value"] = res["native_PS"]["value"]
+    res["sample"] = (f"full {name} workload ({len(cfg['positions'])} atoms, {pairs} pairs, "
+                     f"algorithm {algorithm}); native_PS = P+S from the CPU search with "
+                     f"{cores} threads, public = the same plus '{cfg['quantities']}' assembled "
+                     f"with torch ({cores} threads); >= 1 s warm-up, median of the repeats")
+    return res
+
+
+def boundary_report(cfg, t, width: float = 1e-5, chunk: int = 1 << 24):
+    """Pairs whose distance lies within `width` of the cutoff, on either side.
+
+    The search runs once more with the cutoff widened by 2 * width.  For every
+    pair found, the float64 distance decides nearness (|d - rc| < width), and
+    the reference's public predicate evaluated in the input type
+    (``csrc/core/neighbors_cpu.cpp:247-261``: D accumulated per axis, every
+    product and sum rounded, d^2 < (T)(rc^2)) decides whether the pair belongs
+    to the list at the real cutoff: `kept` pairs are in it, `excluded` ones
+    are not.  These are the pairs whose membership depends on rounding; the
+    parity tests compare them bit for bit like every other pair.
+    """
+    import torch
+
+    from tonari_amd import neighbor_list
+
+    rc = cfg["cutoff"]
+    P, S = neighbor_list(
+        "PS", t["positions"], t["cell"], t["pbc"], rc + 2 * width, t["batch_ptr"],
+        algorithm=cfg["algorithm"], half_list=cfg["half_list"],
+        include_self=cfg["include_self"])
+    pos, cell = t["positions"], t["cell"]
+    T = pos.dtype
+    cut2 = torch.tensor(rc * rc, dtype=torch.float64).to(T).to(pos.device)
+    bounds = t["batch_ptr"][1:].contiguous()
+    near = kept = 0
+    for lo in range(0, P.shape[0], chunk):
+        p, s = P[lo:lo + chunk], S[lo:lo + chunk]
+        b = torch.bucketize(p[:, 0].contiguous(), bounds, right=True)
+        c = cell[b]
+        ps, pt = pos[p[:, 0]], pos[p[:, 1]]
+        D64 = (pt.double() - ps.double() + torch.bmm(s.double().unsqueeze(1),
+                                                     c.double().contiguous()).squeeze(1))
+        is_near = (torch.linalg.vector_norm(D64, dim=1) - rc).abs() < width
+        comp = pt - ps
+        for a in range(3):
+            comp = comp + s[:, a:a + 1].to(T) * c[:, a, :]
+        d2 = comp[:, 0] * comp[:, 0]
+        d2 = d2 + comp[:, 1] * comp[:, 1]
+        d2 = d2 + comp[:, 2] * comp[:, 2]
+        near += int(is_near.sum())
+        kept += int((is_near & (d2 < cut2)).sum())
+    del P, S
+    return {"width_A": width, "pairs_within": near, "kept": kept, "excluded": near - kept,
+            "dtype": str(T).replace("torch.", "")}
+
+
+def time_first_call(cfg, t, reps: int = 5):
+    """Wall time of a public call whose request shape has no previous count.
+
+    The frontend then counts, waits for E and emits into exact-size outputs
+    (the reference's own sequence); repeated calls of one shape instead queue
+    the emit behind the count (what the timed loop measures).
+    """
+    import torch
+
+    from tonari_amd import _torch_frontend as F
+
+    times = []
+    for _ in range(reps + 1):
+        F._speculation().clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = public_call(cfg, t)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
         del out
-    med = statistics.median(samples)
-    return {
-        "value": round(n_pairs / med / 1e6, 3),
-        "unit": "M pairs/s",
-        "cores": cores,
-        "kind": kind,
-        "sample": f"full C4 workload ({len(cfg['positions'])} atoms, {n_pairs} pairs, P+S "
-                  f"native output), median of {len(samples)} calls after one warm-up call",
-        "ms_per_call": round(med * 1e3, 3),
-    }
+    return round(statistics.median(times[1:]) * 1e3, 4)
 
 
-def measure(name, cfg, steps, warmup, reps, dev):
+def measure(name, cfg, steps, warmup, reps, dev, extras: bool = False):
+    """GPU timings of one configuration; with `extras`, also its boundary-pair
+    report and its first-call latency."""
     from tonari_amd import workloads as W
 
     t = to_device(cfg, dev)
@@ -264,8 +400,22 @@ def measure(name, cfg, steps, warmup, reps, dev):
         "GBps_end_to_end": round(b_alg / ms_step / 1e9, 1),
         "plan": plan,
     }
+    if extras:
+        res["ms_first_call"] = time_first_call(cfg, t)
+        res["boundary"] = boundary_report(cfg, t)
     del t
     return res
+
+
+# The configurations of BASELINE.json as bench lines: C1 (the reference's
+# CPU-runnable case) in both of its algorithms, then C2, C3 and C5.
+SECONDARY = {
+    "C1": lambda W: W.c1(),
+    "C1_cell": lambda W: dict(W.c1(), algorithm="cell_list"),
+    "C2": lambda W: W.c2(),
+    "C3": lambda W: W.c3(),
+    "C5": lambda W: W.c5(),
+}
 
 
 def main() -> int:
@@ -275,7 +425,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--reps", type=int, default=20, help="event-timed repetitions")
     ap.add_argument("--cpu-baseline", default="auto", choices=["auto", "reference", "port", "off"])
-    ap.add_argument("--secondary", default="C2,C3,C5", help="comma list, or 'none'")
+    ap.add_argument("--secondary", default="C1,C1_cell,C2,C3,C5",
+                    help="comma list, or 'none'")
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of timed repeats per configuration and CPU variant")
     ap.add_argument("--backward", default="on", choices=["on", "off"],
                     help="also time the C4 backward of D (fused and Torch expression)")
     ap.add_argument("--secondary-only", action="store_true",
@@ -315,25 +468,25 @@ def main() -> int:
         log(f"copy calibration: {nbytes} bytes read and written per copy")
         del src, dst
 
+    names = [s for s in args.secondary.split(",") if s and s != "none"]
     if args.secondary_only:
-        for name in [s for s in args.secondary.split(",") if s and s != "none"]:
+        for name in names:
             log(f"{name}: timing")
-            res = measure(name, W.CONFIGS[name](), args.steps, args.warmup, args.reps, dev)
+            res = measure(name, SECONDARY[name](W), args.steps, args.warmup, args.reps, dev)
             print(json.dumps({"config": name, **res}), flush=True)
         return 0
 
     cfg = W.c4()
     log("C4: timing")
-    head = measure("C4", cfg, args.steps, args.warmup, args.reps, dev)
+    head = measure("C4", cfg, args.steps, args.warmup, args.reps, dev, extras=True)
     log(f"C4: {head}")
     secondary = {}
-    if args.secondary != "none":
-        for name in [s for s in args.secondary.split(",") if s]:
-            log(f"{name}: timing")
-            scfg = W.CONFIGS[name]()
-            steps = max(3, args.steps // 3) if name == "C5" else args.steps
-            secondary[name] = measure(name, scfg, steps, 2, max(3, args.reps // 4), dev)
-            log(f"{name}: {secondary[name]}")
+    for name in names:
+        log(f"{name}: timing")
+        scfg = SECONDARY[name](W)
+        steps = max(3, args.steps // 3) if name == "C5" else args.steps
+        secondary[name] = measure(name, scfg, steps, 2, max(3, args.reps // 4), dev, extras=True)
+        log(f"{name}: {secondary[name]}")
     backward = None
     if args.backward == "on":
         log("C4: backward of D")
@@ -341,9 +494,14 @@ def main() -> int:
         log(f"C4 backward: {backward}")
     base = None
     if args.cpu_baseline != "off":
-        log("cpu baseline")
-        base = cpu_baseline(cfg, args.cpu_baseline)
-        log(f"cpu baseline: {base}")
+        log("cpu baseline: C4")
+        base = cpu_baseline("C4", cfg, args.cpu_baseline, args.cpu_budget)
+        log(f"cpu baseline C4: {base}")
+        for name in names:
+            log(f"cpu baseline: {name}")
+            secondary[name]["cpu_baseline"] = cpu_baseline(name, SECONDARY[name](W),
+                                                           args.cpu_baseline, args.cpu_budget)
+            log(f"cpu baseline {name}: {secondary[name]['cpu_baseline']}")
 
     emit_s = head["emit_us"] * 1e-6
     achieved = head["algorithmic_bytes"] / emit_s / 1e9
@@ -376,6 +534,10 @@ def main() -> int:
             "traffic": load_traffic("c4_emit"),
             "algorithmic_bytes_per_launch": head["algorithmic_bytes"],
             "avg_launch_us": head["emit_us"],
+            # the whole request (every kernel of the count and the emit, no
+            # host gaps) against the same algorithmic bytes
+            "call_kernel_sum_us": head["kernel_sum_us"],
+            "call_frac": head["frac_kernel_sum"],
         },
         "cpu_baseline": base,
         "M_atoms_per_s": head["M_atoms_per_s"],
@@ -383,6 +545,8 @@ def main() -> int:
         "count_us": head["count_us"],
         "frac_kernel_sum": head["frac_kernel_sum"],
         "GBps_end_to_end": head["GBps_end_to_end"],
+        "ms_first_call": head["ms_first_call"],
+        "boundary": head["boundary"],
         "secondary": secondary,
         "backward_C4": backward,
     }

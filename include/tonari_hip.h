@@ -98,6 +98,13 @@ int tnr_abi_version(void);
 /* Offload target the library was compiled for ("gfx950"). */
 const char* tnr_device_arch(void);
 
+/* HIP version of the headers the library was compiled with, as
+ * major * 100 + minor.  The library calls only the C API of the HIP runtime
+ * (libamdhip64.so.<major>) loaded in the process, so the loader requires the
+ * same major version as the runtime torch loaded (replaces the CUDA runtime
+ * check of src/tonari/_extensions.py:42-48). */
+int tnr_hip_version(void);
+
 /* Device scratch bytes for `req`; depends only on dtype, N and B. */
 size_t tnr_workspace_size(const tnr_request* req);
 

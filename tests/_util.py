@@ -150,7 +150,7 @@ def assert_geometry_close_torch(pairs, shifts, d, D, cfg, chunk: int = 1 << 24) 
     for lo in range(0, pairs.shape[0], chunk):
         hi = min(lo + chunk, pairs.shape[0])
         p = pairs[lo:hi]
-        b = torch.bucketize(p[:, 0], bounds, right=True)
+        b = torch.bucketize(p[:, 0].contiguous(), bounds, right=True)
         ref = pos[p[:, 1]] - pos[p[:, 0]]
         ref += torch.bmm(shifts[lo:hi].to(torch.float64).unsqueeze(1),
                          cell[b].contiguous()).squeeze(1)
@@ -182,7 +182,7 @@ def shifts_from_vectors(pairs, D, cfg):
     cell = torch.as_tensor(cfg["cell"]).to(dev, torch.float64)
     inv = torch.linalg.inv(cell.cpu()).to(dev)
     bounds = torch.as_tensor(cfg["batch_ptr"][1:]).to(dev)
-    b = torch.bucketize(pairs[:, 0], bounds, right=True)
+    b = torch.bucketize(pairs[:, 0].contiguous(), bounds, right=True)
     frac = D.to(torch.float64) - (pos[pairs[:, 1]] - pos[pairs[:, 0]])
     S = torch.bmm(frac.unsqueeze(1), inv[b].contiguous()).squeeze(1)
     return torch.round(S).to(torch.int32)

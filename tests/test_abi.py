@@ -194,3 +194,28 @@ def test_static_search_rejects_requests_beyond_its_scratch(lib):
     code = lib.tnr_search_static(ctypes.byref(req), None, None, None, err, len(err))
     assert code == ext.TNR_INPUT_ERROR
     assert "static scratch holds 67108864 bytes" in err.value.decode()
+
+
+def test_build_records_its_hip_version(lib):
+    version = lib.tnr_hip_version()
+    m = re.search(r"#define HIP_VERSION_MAJOR (\d+)\s+#define HIP_VERSION_MINOR (\d+)",
+                  open("/opt/rocm/include/hip/hip_version.h").read()) if os.path.exists(
+        "/opt/rocm/include/hip/hip_version.h") else None
+    assert version >= 700
+    if m:
+        assert version == int(m.group(1)) * 100 + int(m.group(2))
+
+
+def test_runtime_check_follows_the_hip_major_version(lib):
+    built = lib.tnr_hip_version()
+    major, minor = built // 100, built % 100
+    # same major: accepted whatever the minor (the C API of libamdhip64.so.<major>)
+    ext.check_runtime(lib, f"{major}.{minor}.12345")
+    ext.check_runtime(lib, f"{major}.0.51831")
+    for bad in (f"{major + 1}.0.1", f"{major - 1}.4.2"):
+        with pytest.raises(ImportError, match="rebuild it"):
+            ext.check_runtime(lib, bad)
+    with pytest.raises(ImportError, match="ROCm build of PyTorch"):
+        ext.check_runtime(lib, None)
+    with pytest.raises(ImportError, match="unrecognised HIP version"):
+        ext.check_runtime(lib, "rocm")

@@ -22,6 +22,7 @@ ALGORITHMS = {"auto": 0, "brute_force": 1, "cell_list": 2}
 EXPORTS = (
     "tnr_abi_version",
     "tnr_device_arch",
+    "tnr_hip_version",
     "tnr_workspace_size",
     "tnr_count",
     "tnr_count_async",
@@ -80,6 +81,8 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     lib.tnr_abi_version.argtypes = []
     lib.tnr_device_arch.restype = ctypes.c_char_p
     lib.tnr_device_arch.argtypes = []
+    lib.tnr_hip_version.restype = ctypes.c_int
+    lib.tnr_hip_version.argtypes = []
     lib.tnr_workspace_size.restype = ctypes.c_size_t
     lib.tnr_workspace_size.argtypes = [ctypes.POINTER(Request)]
     lib.tnr_count.restype = ctypes.c_int
@@ -121,6 +124,38 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     return lib
 
 
+def hip_major_minor(version: str) -> tuple[int, int]:
+    """(major, minor) of a HIP version string such as torch.version.hip ("7.0.51831")."""
+    parts = version.split(".")
+    if len(parts) < 2 or not parts[0].isdigit() or not parts[1].isdigit():
+        raise ImportError(f"unrecognised HIP version {version!r}")
+    return int(parts[0]), int(parts[1])
+
+
+def check_runtime(lib: ctypes.CDLL, torch_hip: str | None) -> None:
+    """The build checks of the reference loader (``src/tonari/_extensions.py:33-48``).
+
+    The reference compares torch's major.minor and CUDA runtime with its
+    build, because its extension links LibTorch and the CUDA runtime.  This
+    library links neither LibTorch nor a HIP runtime of its own: it calls the
+    C API of the HIP runtime that torch loaded (libamdhip64.so.<major>).  So
+    torch must be a ROCm build whose HIP major version equals the one the
+    library was compiled with; the minor version may differ (the C API is
+    stable within a major version).
+    """
+    if not torch_hip:
+        raise ImportError(
+            "tonari_amd requires a ROCm build of PyTorch (torch.version.hip is unset)"
+        )
+    built = lib.tnr_hip_version()
+    runtime = hip_major_minor(torch_hip)
+    if runtime[0] != built // 100:
+        raise ImportError(
+            f"libtonari_hip.so was built with HIP {built // 100}.{built % 100}, but torch uses "
+            f"HIP {torch_hip}; rebuild it with a HIP {runtime[0]}.x toolchain"
+        )
+
+
 @lru_cache
 def load_torch_hip() -> ctypes.CDLL:
     """Load the provider for PyTorch tensors on ROCm (HIP) devices."""
@@ -130,4 +165,20 @@ def load_torch_hip() -> ctypes.CDLL:
         raise ImportError(
             "tonari_amd requires a ROCm build of PyTorch (torch.version.hip is unset)"
         )
-    return open_library()
+    lib = open_library()
+    check_runtime(lib, torch.version.hip)
+    return lib
+
+
+@lru_cache
+def check_device(index: int) -> None:
+    """Raise ImportError unless device `index` runs the library's offload target."""
+    import torch
+
+    lib = load_torch_hip()
+    arch = lib.tnr_device_arch().decode()
+    found = torch.cuda.get_device_properties(index).gcnArchName.split(":")[0]
+    if found != arch:
+        raise ImportError(
+            f"libtonari_hip.so holds {arch} code only; device cuda:{index} is {found}"
+        )

@@ -30,6 +30,7 @@ from ._extensions import (
     TNR_OK,
     Outputs,
     Request,
+    check_device,
     load_torch_hip,
 )
 
@@ -267,11 +268,12 @@ def neighbor_list_hip(
     values are the same; a repeated call's tensors may be views of slightly
     larger allocations.
     """
+    device = positions.device
     try:
         lib = load_torch_hip()
+        check_device(device.index if device.index is not None else torch.cuda.current_device())
     except ImportError as error:
         raise RuntimeError(f"the CUDA provider is unavailable: {error}") from error
-    device = positions.device
     if positions.shape[0] >= 2**31:
         raise ValueError("the current implementation supports fewer than 2^31 atoms")
     need_grad = (

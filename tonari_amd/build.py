@@ -42,6 +42,7 @@ def command(output: str = OUTPUT, extra: list[str] | None = None) -> list[str]:
         "-fno-gpu-flush-denormals-to-zero",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-I", os.path.join(ROOT, "include"),
+        f'-DTNR_OFFLOAD_ARCH="{ARCH}"',
         *(extra or []),
         *SOURCES,
         "-o", output,

@@ -438,7 +438,13 @@ extern "C" {
 
 int tnr_abi_version(void) { return TNR_ABI_VERSION; }
 
-const char* tnr_device_arch(void) { return "gfx950"; }
+#ifndef TNR_OFFLOAD_ARCH
+#error "build with -DTNR_OFFLOAD_ARCH=\"<offload target>\" (tonari_amd/build.py)"
+#endif
+
+const char* tnr_device_arch(void) { return TNR_OFFLOAD_ARCH; }
+
+int tnr_hip_version(void) { return HIP_VERSION_MAJOR * 100 + HIP_VERSION_MINOR; }
 
 size_t tnr_workspace_size(const tnr_request* req) {
     if (!req || req->n_atoms < 0 || req->n_structures < 0) return 0;

@@ -26,7 +26,15 @@ import ctypes
 import torch
 from torch import Tensor
 
-from ._extensions import ALGORITHMS, HOST_RESULT_SLOTS, TNR_OK, Outputs, Request, load_torch_hip
+from ._extensions import (
+    ALGORITHMS,
+    HOST_RESULT_SLOTS,
+    TNR_OK,
+    Outputs,
+    Request,
+    check_device,
+    load_torch_hip,
+)
 from ._torch_frontend import (
     _allocate,
     _raise,
@@ -72,7 +80,12 @@ class NeighborListPlan:
         self.quantities = quantities
         self.positions, self.cell, self.pbc, self.batch_ptr = positions, cell, pbc, batch_ptr
         self.capacity = int(capacity)
-        self._lib = load_torch_hip()
+        try:
+            self._lib = load_torch_hip()
+            check_device(positions.device.index if positions.device.index is not None
+                         else torch.cuda.current_device())
+        except ImportError as error:
+            raise RuntimeError(f"the CUDA provider is unavailable: {error}") from error
         self._req = Request(
             dtype=0 if positions.dtype == torch.float32 else 1,
             algorithm=ALGORITHMS[algorithm], n_atoms=positions.shape[0],
