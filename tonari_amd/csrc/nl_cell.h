@@ -137,6 +137,7 @@ struct CellBin {
     T c[9];           // cell (rows are cell vectors)
     T outer2, inner2, cut2;
     bool wrapped, diagonal;
+    bool shiftcheck;  // wrapped, and R + 2 max|wrap| may exceed int32: check kept shifts
 };
 
 // Geometry of the stencil of one bin, decoded from its structure record.
@@ -257,6 +258,10 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     cb.inner2 = (T)r.inner2;
     cb.cut2 = (T)r.cut2;
     cb.wrapped = r.any_wrap != 0;
+    // |S| = |k - w_t + w_s| <= max_a R_a + 2 max|w|: no shift of the
+    // structure can leave int32 unless that bound does
+    cb.shiftcheck = cb.wrapped && (double)max(max(r.reps[0], r.reps[1]), r.reps[2]) +
+                                         2.0 * (double)r.maxw >= 2147483647.0;
     cb.diagonal = r.diagonal != 0;
     cb.by_bin = a.by_bin && load_status(a.status + SS_PLAN) == 2ull;
     const BinGeom G = bin_geom(r, lbin);
@@ -384,8 +389,9 @@ __device__ __forceinline__ Vec4<T> cand_record(const QueryArgs<T>& a, const Sten
 // The band between inner2 and outer2: decided by the public predicate on the
 // original positions and the output shift.
 template <typename T>
-__device__ __forceinline__ bool cell_band(const QueryArgs<T>& a, int tid, int kk, int bidx,
-                                          T sx, T sy, T sz, int si, const CellBin<T>& cb) {
+__device__ __forceinline__ bool cell_band(const QueryArgs<T>& a, int tid, int kk,
+                                          const Vec4<T>& rec, T sx, T sy, T sz, int si,
+                                          const CellBin<T>& cb) {
     int kx, ky, kz;
     unpack_k(kk, kx, ky, kz);
     T ps[3], pt[3];
@@ -402,7 +408,6 @@ __device__ __forceinline__ bool cell_band(const QueryArgs<T>& a, int tid, int kk
             pt[cc] = a.pos[3 * (int64_t)tid + cc];
         }
     } else {
-        const Vec4<T> rec = a.binned[bidx];
         ps[0] = sx; ps[1] = sy; ps[2] = sz;
         pt[0] = rec.x; pt[1] = rec.y; pt[2] = rec.z;
     }
@@ -424,14 +429,14 @@ __device__ __forceinline__ void shift_check(const QueryArgs<T>& a, int tid, int 
 // Full decision for candidate v (piece p) of the stencil against the source
 // at (sx, sy, sz) with index si: broad phase, identity and band.  Used by the
 // rare paths; its broad phase is the register path's, operation for operation.
+// The candidate's record comes from `cand` (the LDS staging) when given.
 template <typename T, int MODE>
 __device__ __forceinline__ bool cell_decide(const QueryArgs<T>& a, const StencilLds& st,
                                             const CellBin<T>& cb, int p, int v, T sx, T sy,
                                             T sz, int si, int* tid_out, int* kk_out,
-                                            Vec4<T>* rec_out) {
+                                            Vec4<T>* rec_out, const Vec4<T>* cand = nullptr) {
     using O = Ops<T>;
-    const int bidx = v + st.delta[p];
-    const Vec4<T> rec = a.binned[bidx];
+    const Vec4<T> rec = cand ? cand[v] : a.binned[v + st.delta[p]];
     const int tid = as_idx(rec.w);
     const int kk = st.kid[p];
     *tid_out = tid;
@@ -448,7 +453,7 @@ __device__ __forceinline__ bool cell_decide(const QueryArgs<T>& a, const Stencil
     const bool zsf = tid == si && kzero;
     bool ok = (d2 < cb.outer2 || zsf) &&
               identity_ok<MODE>(si, tid, kzero, lex_negative(kx, ky, kz));
-    if (ok && !zsf && !(d2 < cb.inner2)) ok = cell_band(a, tid, kk, bidx, sx, sy, sz, si, cb);
+    if (ok && !zsf && !(d2 < cb.inner2)) ok = cell_band(a, tid, kk, rec, sx, sy, sz, si, cb);
     return ok;
 }
 
@@ -536,7 +541,7 @@ __device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLd
                                                               &tid, &kk, &rec);
                 const unsigned long long m = ballot(ok);
                 if (!EMIT) {
-                    if (cb.wrapped && ok) shift_check(a, tid, kk, si);
+                    if (cb.shiftcheck && ok) shift_check(a, tid, kk, si);
                     if (lane == gi) acc += __popcll(m);
                 } else if (m) {
                     const long long base = read_lane(cur, gi);
@@ -600,13 +605,15 @@ template <typename T, int MODE>
 __device__ __forceinline__ unsigned long long band_chunk(const QueryArgs<T>& a,
                                                          const StencilLds& st,
                                                          const CellBin<T>& cb, int jc, T sx,
-                                                         T sy, T sz, int si) {
+                                                         T sy, T sz, int si,
+                                                         const Vec4<T>* cand) {
     const int v = chunk_cand(jc, lane_id(), cb.nch);
     bool ok = false;
     if (v < cb.C) {
         int tid, kk;
         Vec4<T> rec;
-        ok = cell_decide<T, MODE>(a, st, cb, st.piece[v], v, sx, sy, sz, si, &tid, &kk, &rec);
+        ok = cell_decide<T, MODE>(a, st, cb, st.piece[v], v, sx, sy, sz, si, &tid, &kk, &rec,
+                                  cand);
     }
     return __builtin_amdgcn_ballot_w64(ok);
 }
@@ -618,7 +625,8 @@ __device__ __forceinline__ unsigned long long band_chunk(const QueryArgs<T>& a,
 template <typename T, int MODE, int NC>
 __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLds& st,
                                           const CellBin<T>& cb, const Chunks<T, NC>& cd, int c0,
-                                          T sx, T sy, T sz, int si, unsigned long long& mv) {
+                                          T sx, T sy, T sz, int si, unsigned long long& mv,
+                                          const Vec4<T>* cand) {
     using O = Ops<T>;
     const int lane = lane_id();
     unsigned band = 0;
@@ -643,7 +651,8 @@ __device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLd
     if (band) {
         for (int j = 0; j < NC; ++j) {
             if (!((band >> j) & 1u)) continue;
-            const unsigned long long full = band_chunk<T, MODE>(a, st, cb, c0 + j, sx, sy, sz, si);
+            const unsigned long long full =
+                band_chunk<T, MODE>(a, st, cb, c0 + j, sx, sy, sz, si, cand);
             const unsigned long long old = (unsigned long long)read_lane((long long)mv, j);
             cnt += __popcll(full) - __popcll(old);
             if (lane == j) mv = full;
@@ -677,7 +686,8 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
                         sz = read_lane(sq.z, gi);
                 const int si = read_lane(sidx, gi);
                 unsigned long long mv;  // lane j: hit mask of chunk c0 + j
-                int cnt = pass_masks<T, MODE, NC>(a, st, cb, cd, c0, sx, sy, sz, si, mv);
+                int cnt = pass_masks<T, MODE, NC>(a, st, cb, cd, c0, sx, sy, sz, si, mv,
+                                                  staged ? cand : nullptr);
                 if constexpr (MODE == 0) {
                     // drop the source itself (candidate vs, at distance 0): lane
                     // vs / nch of chunk vs % nch
@@ -690,7 +700,7 @@ __device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLd
                         if (lane == jc) mv &= ~(1ull << ls);
                     }
                 }
-                if (cb.wrapped) {
+                if (cb.shiftcheck) {
                     for (int j = 0; j < NC && c0 + j < cb.nch; ++j) {
                         const unsigned long long m = (unsigned long long)read_lane((long long)mv, j);
                         if ((m >> lane) & 1ull) {

@@ -142,7 +142,9 @@ constexpr int kMaskWords = 32;
 
 constexpr int64_t kScanItems = 8;
 constexpr int64_t kScanChunk = kBlock * kScanItems;
-constexpr int64_t kScanTile = kScanChunk;  // items per tile of the single-pass scan
+// Items per thread of the single-pass scan.
+constexpr int64_t kTileItems = 8;
+constexpr int64_t kScanTile = kBlock * kTileItems;
 
 inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 

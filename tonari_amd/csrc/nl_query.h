@@ -365,7 +365,12 @@ __device__ __forceinline__ int unit_structure(const int64_t* off, int64_t nb, in
 }
 
 // Atoms of a structure staged in LDS per wave (structures up to this size).
-constexpr int kBruteStage = 128;
+// 120 float atoms make 7,808 bytes per wave, 31,232 per workgroup: five
+// workgroups per CU fit in the 160 KiB of LDS with room to spare.  At
+// exactly 32 KiB per workgroup (128 atoms) only four were resident at once,
+// although the occupancy query reported five, so a grid sized by the query
+// left a fifth of its workgroups waiting for the first ones to finish.
+constexpr int kBruteStage = 120;
 
 // Per source of a brute-force work unit: its pair count (counting) or its
 // next output (emitting).

@@ -37,11 +37,16 @@ constexpr unsigned long long kTilePrefix = 2ull << 62;
 constexpr unsigned long long kTileValue = (1ull << 62) - 1;
 constexpr int kLookbackSpins = 1 << 22;
 
+// Tile words are relaxed device-scope atomics: a tile word carries
+// everything its readers use (flag and value in one 64-bit word), and no
+// block reads another block's other outputs, so no ordering with other
+// memory is needed.  Release / acquire at device scope would write back /
+// invalidate the XCD's L2 on every publish and poll.
 __device__ __forceinline__ void tile_publish(unsigned long long* t, unsigned long long w) {
-    __hip_atomic_store(t, w, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(t, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ unsigned long long tile_read(const unsigned long long* t) {
-    return __hip_atomic_load(t, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Exclusive scan of n (min(n, *n_dev) when n_dev is given) non-negative values of
@@ -67,17 +72,19 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
                                                            unsigned long long* total_slot,
                                                            long long* host_out = nullptr) {
     __shared__ long long s_tile, s_excl;
+    if (n_dev) n = min(n, (int64_t)*n_dev);
+    const int64_t ntiles = n > 0 ? (n + kScanTile - 1) / kScanTile : 1;
+    // blocks beyond the tiles (a grid sized for a capacity) leave without a
+    // ticket; the first ntiles blocks take tickets 0 .. ntiles - 1
+    if ((int64_t)blockIdx.x >= ntiles) return;
     if (threadIdx.x == 0) s_tile = (long long)atomicAdd(ticket, 1ull);
     __syncthreads();
-    if (n_dev) n = min(n, (int64_t)*n_dev);
     const int64_t tile = s_tile;
-    const int64_t ntiles = n > 0 ? (n + kScanTile - 1) / kScanTile : 1;
-    if (tile >= ntiles) return;
-    const int64_t base = tile * kScanTile + (int64_t)threadIdx.x * kScanItems;
-    long long v[kScanItems];
+    const int64_t base = tile * kScanTile + (int64_t)threadIdx.x * kTileItems;
+    long long v[kTileItems];
     long long s = 0;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
+    for (int k = 0; k < kTileItems; ++k) {
         const int64_t i = base + k;
         v[k] = i < n ? (long long)in[i] : 0;
         s += v[k];
@@ -120,7 +127,7 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     __syncthreads();
     long long run = s_excl + ex;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
+    for (int k = 0; k < kTileItems; ++k) {
         const int64_t i = base + k;
         if (i < n) out[i] = (Out)run;
         run += v[k];
