@@ -373,6 +373,53 @@ def time_first_call(cfg, t, reps: int = 5):
     return round(statistics.median(times[1:]) * 1e3, 4)
 
 
+def sweep_cases():
+    """Batches of equal structures for the brute-force / cell-list crossover.
+
+    Periodic cubic cells at density 0.1 /A^3 (rc 6 A) and 0.05 /A^3 (rc 8 A,
+    more images per structure), and non-periodic Gaussian clusters (rc 5 A),
+    from 4 to 2,048 atoms per structure; about 16,384 atoms per batch.
+    """
+    import numpy as np
+
+    from tonari_amd import workloads as W
+
+    rng = np.random.Generator(np.random.PCG64(2027))
+    for rc, rho in ((6.0, 0.1), (8.0, 0.05)):
+        for n in (4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048):
+            B = max(1, 16384 // n)
+            edge = (n / rho) ** (1.0 / 3.0)
+            pos = [rng.uniform(0.0, edge, size=(n, 3)) for _ in range(B)]
+            cfg = W._pack(pos, [edge * np.eye(3)] * B, [np.ones(3, bool)] * B, [n] * B,
+                          np.float32, rc, quantities="PS", algorithm="auto", half_list=False,
+                          include_self=False, sorted=False)
+            images = (2 * int(np.ceil(rc / edge)) + 1) ** 3
+            yield f"periodic rho {rho} rc {rc}", n, B, images, cfg
+    for n in (16, 32, 64, 128, 256, 512, 1024, 2048):
+        B = max(1, 16384 // n)
+        pos = [W._gaussian_molecule(rng, n, sigma=0.5 * n ** (1.0 / 3.0) + 1.0, dmin=0.9)
+               for _ in range(B)]
+        cfg = W._pack(pos, [np.zeros((3, 3))] * B, [np.zeros(3, bool)] * B, [n] * B,
+                      np.float32, 5.0, quantities="PS", algorithm="auto", half_list=False,
+                      include_self=False, sorted=False)
+        yield "molecules rc 5.0", n, B, 1, cfg
+
+
+def auto_sweep(dev, steps: int, warmup: int) -> None:
+    """Public-call time of brute_force and cell_list on sweep_cases(), one JSON line each."""
+    for family, n, B, images, cfg in sweep_cases():
+        t = to_device(cfg, dev)
+        res = {"family": family, "atoms_per_structure": n, "structures": B, "images": images,
+               "N_times_images": n * images}
+        for algorithm in ("brute_force", "cell_list"):
+            ms, pairs = time_public(dict(cfg, algorithm=algorithm), t, steps, warmup)
+            res[f"ms_{algorithm}"] = round(ms * 1e3, 4)
+            res["pairs"] = pairs
+        res["faster"] = min(("brute_force", "cell_list"), key=lambda a: res[f"ms_{a}"])
+        print(json.dumps(res), flush=True)
+        del t
+
+
 def measure(name, cfg, steps, warmup, reps, dev, extras: bool = False):
     """GPU timings of one configuration; with `extras`, also its boundary-pair
     report and its first-call latency."""
@@ -434,6 +481,9 @@ def main() -> int:
     ap.add_argument("--secondary-only", action="store_true",
                     help="time only the --secondary configurations (one JSON object per line; "
                          "for profiling them) instead of the benchmark line")
+    ap.add_argument("--auto-sweep", action="store_true",
+                    help="time brute_force against cell_list on batches of equal structures of "
+                         "4 to 2,048 atoms (one JSON line per case) instead of the benchmark line")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="also run a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -467,6 +517,10 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"copy calibration: {nbytes} bytes read and written per copy")
         del src, dst
+
+    if args.auto_sweep:
+        auto_sweep(dev, max(5, args.steps // 2), 3)
+        return 0
 
     names = [s for s in args.secondary.split(",") if s and s != "none"]
     if args.secondary_only:

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TNR_ABI_VERSION 2
+#define TNR_ABI_VERSION 3
 
 #define TNR_OK 0
 #define TNR_INPUT_ERROR 1
@@ -90,6 +90,12 @@ typedef struct tnr_outputs {
     void* vectors;      /* D: T[E][3] = pos[j] - pos[i] + S @ cell[b] */
     int64_t* sources;   /* i: int64[E] */
     int64_t* targets;   /* j: int64[E] */
+    int64_t* edge_index; /* edge-first layout int64[2][E]: sources, then targets from row E on,
+                            with E taken from the count on the device (so a buffer of
+                            2 x n_pairs rows serves a launch made before E is read); when
+                            given, `sources` and `targets` are ignored.  No counterpart in the
+                            reference, whose design leaves (2, E) layouts to graph adapters
+                            (docs/design.md:61,127). */
 } tnr_outputs;
 
 /* ABI version compiled into the library (TNR_ABI_VERSION). */

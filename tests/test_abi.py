@@ -61,7 +61,8 @@ def test_struct_layouts_match_header():
     # offsets of tnr_request / tnr_outputs as laid out by the C compiler
     assert ctypes.sizeof(ext.Request) == 80
     assert ext.Request.cutoff.offset == 56 and ext.Request.stencil_reach.offset == 76
-    assert ctypes.sizeof(ext.Outputs) == 72 and ext.Outputs.targets.offset == 64
+    assert ctypes.sizeof(ext.Outputs) == 80 and ext.Outputs.targets.offset == 64
+    assert ext.Outputs.edge_index.offset == 72
     assert ext.Outputs.n_tasks.offset == 16
 
 

@@ -69,10 +69,11 @@ def test_more_bins_than_launch_covered():
 
 
 def test_plan_switch():
-    # the same atom count searched by brute force (a small open cluster) and
-    # then by a cell list (a large periodic box)
+    # the same atom count searched by brute force (an open cluster of at
+    # most 384 atoms under auto) and then by a cell list (a periodic box of
+    # 300 x 27 atom images)
     rng = np.random.default_rng(16)
-    n = 512
+    n = 300
     cluster = {
         "positions": rng.uniform(0.0, 8.0, (n, 3)).astype(np.float32),
         "cell": np.zeros((1, 3, 3), np.float32),

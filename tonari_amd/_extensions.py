@@ -14,7 +14,7 @@ from functools import lru_cache
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 HOST_RESULT_SLOTS = 8
 
 TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR = 0, 1, 2, 3
@@ -66,6 +66,7 @@ class Outputs(ctypes.Structure):
         ("vectors", ctypes.c_void_p),
         ("sources", ctypes.c_void_p),
         ("targets", ctypes.c_void_p),
+        ("edge_index", ctypes.c_void_p),
     ]
 
 

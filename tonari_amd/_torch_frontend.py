@@ -200,10 +200,18 @@ _ROWS = {
 }
 
 
+# Internal quantity: the edge-first index (2, E) of the graph adapter, held
+# as one int64 buffer of 2 x rows (sources, then targets from row E on).
+EDGE_INDEX = "E"
+
+
 def _allocate(want: set, rows: int, dtype: torch.dtype, device: torch.device) -> dict:
     out = {}
-    for q in ("P", "S", "i", "j", "d", "D"):
+    for q in ("P", "S", "i", "j", "d", "D", EDGE_INDEX):
         if q not in want:
+            continue
+        if q == EDGE_INDEX:
+            out[q] = torch.empty(2 * rows, dtype=torch.int64, device=device)
             continue
         if q in _ROWS:
             tail, qdtype = _ROWS[q]
@@ -225,6 +233,7 @@ def _emit(lib, req, workspace: Tensor, ws_bytes: int, out: dict, rows: int, plan
         vectors=out["D"].data_ptr() if "D" in out else None,
         sources=out["i"].data_ptr() if "i" in out else None,
         targets=out["j"].data_ptr() if "j" in out else None,
+        edge_index=out[EDGE_INDEX].data_ptr() if EDGE_INDEX in out else None,
     )
     code = lib.tnr_emit(
         ctypes.byref(req), workspace.data_ptr(), ws_bytes, ctypes.byref(ptrs), stream, err,
@@ -232,6 +241,12 @@ def _emit(lib, req, workspace: Tensor, ws_bytes: int, out: dict, rows: int, plan
     )
     if code != TNR_OK:
         _raise(code, err.value.decode())
+
+
+def _rows(out: dict, count: int) -> dict:
+    """The first `count` rows of each output (the edge-first index as (2, count))."""
+    return {q: t[: 2 * count].view(2, count) if q == EDGE_INDEX else t[:count]
+            for q, t in out.items()}
 
 
 def _raise(code: int, message: str) -> None:
@@ -344,11 +359,11 @@ def neighbor_list_hip(
                 out = _allocate(want, count, dtype, device)
             if not fits and count > 0:
                 _emit(lib, req, workspace, ws_bytes, out, count, plan, bins, stream, err)
-            out = {q: t[:count] for q, t in out.items()}
         else:
             out = _allocate(want, count, dtype, device)
             if count > 0 and out:
                 _emit(lib, req, workspace, ws_bytes, out, count, plan, bins, stream, err)
+        out = _rows(out, count)
         table[key] = (_capacity(count), plan, bins)
         if need_grad:
             out["D"], out["d"] = _FusedGeometry.apply(

@@ -1241,6 +1241,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     __shared__ unsigned short s_list[kWavesPerBlock][kListCap];
 
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
+    place_edge_index(a);
     // the batch's bins from the count's status words; the grid may cover
     // more (a launch sized before the count finished)
     const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_BINS);

@@ -22,7 +22,13 @@ constexpr int kPieceCap = 192;            // stencil pieces per source bin
 // staging, register gather) against the per-source distance tests.
 constexpr double kBinOverhead = 6.0;
 constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
-constexpr int64_t kAutoBruteCandidates = 4096;     // N_b * images at or below: brute force
+// algorithm='auto', per structure: brute force at or below these sizes, the
+// crossovers measured on gfx950 (bench.py --auto-sweep, batches of ~16k atoms
+// of equal structures): periodic structures by atoms x images (brute force
+// faster at 1,728, the cell list at 3,456), non-periodic ones by atoms
+// (brute force faster at 256, the cell list at 512).
+constexpr int64_t kAutoBrutePeriodic = 2500;
+constexpr int64_t kAutoBruteIsolated = 384;
 // Brute force: a work unit takes about this many rounds of one image walk
 // per lane, a round costing 1 + images / 4 (most images fall outside the
 // cutoff sphere and are never visited).

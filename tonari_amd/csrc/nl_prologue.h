@@ -603,7 +603,7 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
     const bool safe = isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Ops<T>::max;
 
     const int64_t nimages = r.nimages;
-    const bool large = n > kAutoBruteCandidates / nimages;
+    const bool large = r.active != 0 ? n > kAutoBrutePeriodic / nimages : n > kAutoBruteIsolated;
     bool want_cell = requested == TNR_CELL_LIST || (requested == TNR_AUTO && large);
     unsigned long long st = 0;
     if (requested == TNR_CELL_LIST) {

@@ -52,7 +52,21 @@ struct QueryArgs {
     T* vec;
     int64_t* src;
     int64_t* dst;
+    int64_t* edge;  // edge-first i/j (tnr_outputs::edge_index); place_edge_index sets src, dst
 };
+
+// Edge-first outputs: sources at edge[0, E), targets at edge[E, 2E), with E
+// from the count's status words, so an emit launched before the host read E
+// writes the layout too.  When E exceeds the output length the targets are
+// not written (the sources' rows stay below the length); the caller sees E
+// and emits again into a larger buffer.
+template <typename T>
+__device__ __forceinline__ void place_edge_index(QueryArgs<T>& a) {
+    if (!a.edge) return;
+    const long long E = (long long)load_status(a.status + SS_PAIRS);
+    a.src = a.edge;
+    a.dst = E <= a.limit ? a.edge + E : nullptr;
+}
 
 // Value of x held by the first active lane, as a wave-uniform (scalar) value.
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -516,6 +530,7 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
     if ((load_status(a.status + SS_FLAGS) & kAbortBits) ||
         !(load_status(a.status + SS_PLAN) & 1))
         return;
+    if constexpr (EMIT) place_edge_index(a);
     __shared__ BruteLds<T> s_lds[kWavesPerBlock];
     const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
     const int wv = uniform(threadIdx.x / kWave);

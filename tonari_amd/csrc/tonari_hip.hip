@@ -324,6 +324,7 @@ static hipError_t run_emit(const tnr_request* req, void* ws, const Layout& L,
     q.vec = (T*)out->vectors;
     q.src = out->sources;
     q.dst = out->targets;
+    q.edge = out->edge_index;
     q.limit = out->n_pairs;
     q.n_bins = out->plan < 0 ? L.cap_bins : out->n_tasks;
     dispatch_queries<T, true>(req, L, q, out->plan, out->n_tasks, stream);
