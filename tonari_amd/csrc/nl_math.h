@@ -19,7 +19,12 @@ struct Ops<float> {
     __device__ static float sub(float a, float b) { return __fsub_rn(a, b); }
     __device__ static float mul(float a, float b) { return __fmul_rn(a, b); }
     __device__ static float fma_(float a, float b, float c) { return __fmaf_rn(a, b, c); }
-    __device__ static float sqrt_(float a) { return __fsqrt_rn(a); }
+    // Correctly rounded, in every kernel: HIP's __fsqrt_rn is the native
+    // square root (about 1 ulp) unless OCML_BASIC_ROUNDED_OPERATIONS is
+    // defined, and the optimiser may or may not drop its accuracy note; a
+    // plain llvm.sqrt.f32 (HIP's default correctly rounded divide / sqrt)
+    // is lowered to the correctly rounded sequence.
+    __device__ static float sqrt_(float a) { return __builtin_sqrtf(a); }
     // Nearest float not below / not above x.
     __device__ static float down(double x) {
         float f = (float)x;
