@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TNR_ABI_VERSION 3
+#define TNR_ABI_VERSION 4
 
 #define TNR_OK 0
 #define TNR_INPUT_ERROR 1
@@ -162,6 +162,54 @@ int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
  */
 int tnr_search_static(const tnr_request* req, const tnr_outputs* out, int64_t* host_result,
                       void* stream, char* err, size_t err_len);
+
+/*
+ * Verlet-skin lists.  No counterpart in the reference, which lists a Verlet
+ * skin as unsupported (docs/design.md:125-127); for molecular-dynamics
+ * loops that search every step.  The caller builds a list with
+ * tnr_count / tnr_emit (P and S) at build_cutoff = cutoff + skin and keeps
+ * copies of that call's positions, cell, pbc and batch_ptr.  At a later step
+ * (a request with the same dtype, N, B and pair policy, and the filter
+ * cutoff in req->cutoff) the stored pairs are re-decided with the reference's
+ * public predicate at the current positions.  tnr_skin_finish says whether
+ * the result equals a fresh search (every atom moved less than about
+ * skin / 2, less a rounding margin, and cell, pbc and batch_ptr unchanged);
+ * if not, the caller rebuilds.  The kept pairs come out in stored order.
+ */
+typedef struct tnr_skin_list {
+    int64_t n_pairs;              /* rows of the stored list */
+    const int64_t* pairs;         /* int64[n_pairs][2] */
+    const int32_t* shifts;        /* int32[n_pairs][3] */
+    const void* ref_positions;    /* T[N][3] of the build */
+    const void* ref_cell;         /* T[B][3][3] of the build */
+    const uint8_t* ref_pbc;       /* uint8 (bool) [B][3] of the build */
+    const int64_t* ref_batch_ptr; /* int64[B + 1] of the build */
+    double build_cutoff;          /* cutoff of the build; at least req->cutoff */
+} tnr_skin_list;
+
+/* Device scratch bytes of the filter of `list` for `req`. */
+size_t tnr_skin_workspace_size(const tnr_request* req, const tnr_skin_list* list);
+
+/* Enqueues the filter's counting pass on `stream`: displacement and
+ * structure checks, kept pairs per block, their scan; the status words reach
+ * `host_result` (pinned, TNR_HOST_RESULT_SLOTS int64) when the stream has
+ * reached this point.  Uses positions, cell, pbc, batch_ptr, dtype, n_atoms,
+ * n_structures and cutoff of `req`. */
+int tnr_skin_count_async(const tnr_request* req, const tnr_skin_list* list, void* workspace,
+                         size_t workspace_bytes, int64_t* host_result, void* stream, char* err,
+                         size_t err_len);
+
+/* Decodes a completed tnr_skin_count_async: *rebuild = 1 when the filtered
+ * list may differ from a fresh search at req->cutoff (the caller rebuilds);
+ * otherwise *rebuild = 0 and *n_pairs receives E. */
+int tnr_skin_finish(const tnr_request* req, const tnr_skin_list* list, const int64_t* host_result,
+                    int64_t* n_pairs, int32_t* rebuild, char* err, size_t err_len);
+
+/* Writes the kept pairs' requested quantities (out->plan and out->n_tasks
+ * are ignored) for the filter last counted in `workspace`. */
+int tnr_skin_emit(const tnr_request* req, const tnr_skin_list* list, void* workspace,
+                  size_t workspace_bytes, const tnr_outputs* out, void* stream, char* err,
+                  size_t err_len);
 
 /*
  * Backward of the d/D outputs of tnr_emit: adds the gradients of positions

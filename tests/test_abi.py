@@ -220,3 +220,46 @@ def test_runtime_check_follows_the_hip_major_version(lib):
         ext.check_runtime(lib, None)
     with pytest.raises(ImportError, match="unrecognised HIP version"):
         ext.check_runtime(lib, "rocm")
+
+
+def test_skin_list_layout_and_workspace(lib):
+    assert ctypes.sizeof(ext.SkinList) == 64 and ext.SkinList.build_cutoff.offset == 56
+    req = _request(n_atoms=1000)
+    small = ext.SkinList(n_pairs=10, build_cutoff=1.5)
+    large = ext.SkinList(n_pairs=10_000_000, build_cutoff=1.5)
+    a = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(small))
+    b = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(large))
+    assert 0 < a < b and a % 256 == 0 and b % 256 == 0
+    assert lib.tnr_skin_workspace_size(ctypes.byref(req), None) == 0
+
+
+def _skin_count(lib, req, lst, ws=1 << 24, ws_bytes=None, host=1 << 25):
+    err = ctypes.create_string_buffer(256)
+    if ws_bytes is None:
+        ws_bytes = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(lst))
+    code = lib.tnr_skin_count_async(ctypes.byref(req), ctypes.byref(lst), ws, ws_bytes, host,
+                                    None, err, len(err))
+    return code, err.value.decode()
+
+
+def test_skin_requests_are_rejected_on_the_host(lib):
+    req = _request(n_atoms=100)
+    ok = dict(n_pairs=5, pairs=1 << 26, shifts=1 << 27, ref_positions=1 << 28,
+              ref_cell=1 << 29, ref_pbc=1 << 30, ref_batch_ptr=1 << 31, build_cutoff=1.5)
+    for fields, message in (
+        ({"build_cutoff": 0.5}, "at least the cutoff"),
+        ({"build_cutoff": float("nan")}, "at least the cutoff"),
+        ({"pairs": None}, "required pointers"),
+        ({"ref_positions": None}, "required pointers"),
+        ({"n_pairs": -1}, "invalid sizes"),
+    ):
+        code, text = _skin_count(lib, req, ext.SkinList(**{**ok, **fields}))
+        assert code == ext.TNR_INPUT_ERROR and message in text, text
+    lst = ext.SkinList(**ok)
+    need = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(lst))
+    assert _skin_count(lib, req, lst, ws_bytes=need - 256)[0] == ext.TNR_INPUT_ERROR
+    assert _skin_count(lib, req, lst, ws=(1 << 24) + 8)[0] == ext.TNR_INPUT_ERROR
+    code, text = _skin_count(lib, req, lst, host=0)
+    assert code == ext.TNR_INPUT_ERROR and "host_result" in text
+    code, text = _skin_count(lib, _request(n_atoms=100, cutoff=-1.0), lst)
+    assert code == ext.TNR_INPUT_ERROR and "cutoff" in text

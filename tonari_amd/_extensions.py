@@ -14,7 +14,7 @@ from functools import lru_cache
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 HOST_RESULT_SLOTS = 8
 
 TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR = 0, 1, 2, 3
@@ -30,6 +30,10 @@ EXPORTS = (
     "tnr_geometry_backward",
     "tnr_emit",
     "tnr_search_static",
+    "tnr_skin_workspace_size",
+    "tnr_skin_count_async",
+    "tnr_skin_finish",
+    "tnr_skin_emit",
 )
 
 
@@ -67,6 +71,21 @@ class Outputs(ctypes.Structure):
         ("sources", ctypes.c_void_p),
         ("targets", ctypes.c_void_p),
         ("edge_index", ctypes.c_void_p),
+    ]
+
+
+class SkinList(ctypes.Structure):
+    """``tnr_skin_list`` of include/tonari_hip.h."""
+
+    _fields_ = [
+        ("n_pairs", ctypes.c_int64),
+        ("pairs", ctypes.c_void_p),
+        ("shifts", ctypes.c_void_p),
+        ("ref_positions", ctypes.c_void_p),
+        ("ref_cell", ctypes.c_void_p),
+        ("ref_pbc", ctypes.c_void_p),
+        ("ref_batch_ptr", ctypes.c_void_p),
+        ("build_cutoff", ctypes.c_double),
     ]
 
 
@@ -116,6 +135,24 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     lib.tnr_search_static.argtypes = [
         ctypes.POINTER(Request), ctypes.POINTER(Outputs), ctypes.c_void_p, ctypes.c_void_p,
         ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_skin_workspace_size.restype = ctypes.c_size_t
+    lib.tnr_skin_workspace_size.argtypes = [ctypes.POINTER(Request), ctypes.POINTER(SkinList)]
+    lib.tnr_skin_count_async.restype = ctypes.c_int
+    lib.tnr_skin_count_async.argtypes = [
+        ctypes.POINTER(Request), ctypes.POINTER(SkinList), ctypes.c_void_p, ctypes.c_size_t,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_skin_finish.restype = ctypes.c_int
+    lib.tnr_skin_finish.argtypes = [
+        ctypes.POINTER(Request), ctypes.POINTER(SkinList), ctypes.c_void_p,
+        ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32), ctypes.c_char_p,
+        ctypes.c_size_t,
+    ]
+    lib.tnr_skin_emit.restype = ctypes.c_int
+    lib.tnr_skin_emit.argtypes = [
+        ctypes.POINTER(Request), ctypes.POINTER(SkinList), ctypes.c_void_p, ctypes.c_size_t,
+        ctypes.POINTER(Outputs), ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
     ]
     version = lib.tnr_abi_version()
     if version != ABI_VERSION:

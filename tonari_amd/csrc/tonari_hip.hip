@@ -1,7 +1,8 @@
 // MI355X (gfx950) neighbor-list library: host orchestration and the C ABI
 // declared in include/tonari_hip.h.  Kernels live in nl_prologue.h (device
 // geometry, wraps, bin grid, counting sort), nl_query.h (cell-list and
-// brute-force count/emit) and nl_scan.h (device-wide scans).
+// brute-force count/emit), nl_scan.h (device-wide scans), nl_skin.h (the
+// Verlet-skin filter) and nl_backward.h (the geometry backward).
 //
 // Pipeline of one request (all on the caller's stream):
 //   tnr_count, one structure: k_atoms<T, true> (every block derives the
@@ -39,6 +40,7 @@
 #include "nl_query.h"
 #include "nl_scan.h"
 #include "nl_backward.h"
+#include "nl_skin.h"
 
 #include "../../include/tonari_hip.h"
 
@@ -431,6 +433,147 @@ static int scratch_address(void** out, char* err, size_t err_len) {
     return TNR_OK;
 }
 
+// ------------------------------------------------------- Verlet-skin filter
+
+struct SkinLayout {
+    int64_t blocks, n_tiles;
+    size_t status, counts, offsets, tiles, total;
+};
+
+// Workgroups of the filter's counting pass: one thread per stored pair, per
+// atom and per cell entry, whichever is most.
+static SkinLayout skin_layout(int64_t n_pairs, int64_t n_atoms, int64_t nb) {
+    int64_t g = n_pairs > n_atoms ? n_pairs : n_atoms;
+    if (9 * nb + 1 > g) g = 9 * nb + 1;
+    SkinLayout L;
+    L.blocks = (g + kBlock - 1) / kBlock;
+    L.n_tiles = (L.blocks + kScanTile - 1) / kScanTile;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = align_up(o + bytes);
+        return at;
+    };
+    L.status = take(sizeof(int64_t) * SS_SLOTS);
+    L.counts = take(sizeof(int64_t) * (size_t)(L.blocks + 1));
+    L.offsets = take(sizeof(int64_t) * (size_t)(L.blocks + 1));
+    L.tiles = take(sizeof(int64_t) * (size_t)L.n_tiles);
+    L.total = o;
+    return L;
+}
+
+static int check_skin(const tnr_request* req, const tnr_skin_list* list, size_t ws_bytes,
+                      const void* ws, char* err, size_t err_len, SkinLayout* L) {
+    if (!req || !list) return put_error(err, err_len, TNR_INPUT_ERROR, "request or list is null");
+    if (req->dtype != TNR_FLOAT32 && req->dtype != TNR_FLOAT64)
+        return put_error(err, err_len, TNR_INPUT_ERROR,
+                         "positions must have dtype float32 or float64");
+    if (!(std::isfinite(req->cutoff) && req->cutoff > 0))
+        return put_error(err, err_len, TNR_INPUT_ERROR, "cutoff must be finite and positive");
+    if (!(std::isfinite(list->build_cutoff) && list->build_cutoff >= req->cutoff))
+        return put_error(err, err_len, TNR_INPUT_ERROR,
+                         "the list's build cutoff must be finite and at least the cutoff");
+    if (req->n_atoms < 0 || req->n_structures < 1 || list->n_pairs < 0 ||
+        req->n_atoms >= (int64_t{1} << 31))
+        return put_error(err, err_len, TNR_INPUT_ERROR, "invalid sizes");
+    if (!req->batch_ptr || !req->cell || !req->pbc || !list->ref_cell || !list->ref_pbc ||
+        !list->ref_batch_ptr || (req->n_atoms > 0 && (!req->positions || !list->ref_positions)) ||
+        (list->n_pairs > 0 && (!list->pairs || !list->shifts)))
+        return put_error(err, err_len, TNR_INPUT_ERROR, "required pointers are null");
+    *L = skin_layout(list->n_pairs, req->n_atoms, req->n_structures);
+    if (!ws || ws_bytes < L->total || ((uintptr_t)ws & 255) != 0)
+        return put_error(err, err_len, TNR_INPUT_ERROR,
+                         "workspace is missing, too small or not 256-byte aligned");
+    return TNR_OK;
+}
+
+static SkinArgs skin_args(const tnr_request* req, const tnr_skin_list* list) {
+    SkinArgs k{};
+    k.n_pairs = list->n_pairs;
+    k.n_atoms = req->n_atoms;
+    k.nb = req->n_structures;
+    k.pairs = list->pairs;
+    k.shifts = list->shifts;
+    k.bp = req->batch_ptr;
+    k.pbc = req->pbc;
+    k.ref_pos = list->ref_positions;
+    k.ref_cell = list->ref_cell;
+    k.ref_pbc = list->ref_pbc;
+    k.ref_bp = list->ref_batch_ptr;
+    k.cutoff = req->cutoff;
+    return k;
+}
+
+template <typename T>
+static hipError_t run_skin_count(const tnr_request* req, const tnr_skin_list* list, void* ws,
+                                 const SkinLayout& L, hipStream_t stream, long long* host_out) {
+    char* base = (char*)ws;
+    auto* status = (unsigned long long*)(base + L.status);
+    auto* counts = (long long*)(base + L.counts);
+    auto* offsets = (long long*)(base + L.offsets);
+    auto* tiles = (unsigned long long*)(base + L.tiles);
+    k_skin_clear<<<1, kBlock, 0, stream>>>(status, tiles, L.n_tiles);
+    k_skin_count<T><<<(unsigned)L.blocks, kBlock, 0, stream>>>(
+        skin_args(req, list), (const T*)req->positions, (const T*)req->cell, counts, status);
+    k_scan_lookback<long long, long long><<<(unsigned)L.n_tiles, kBlock, 0, stream>>>(
+        counts, L.blocks, nullptr, offsets, tiles, status + SK_TICKET, status,
+        status + SK_PAIRS, host_out);
+    return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t run_skin_emit(const tnr_request* req, const tnr_skin_list* list, void* ws,
+                                const SkinLayout& L, const tnr_outputs* out, hipStream_t stream) {
+    char* base = (char*)ws;
+    QueryArgs<T> q{};
+    q.pos = (const T*)req->positions;
+    q.cells = (const T*)req->cell;
+    q.status = (unsigned long long*)(base + L.status);
+    q.n_atoms = req->n_atoms;
+    q.nb = req->n_structures;
+    q.limit = out->n_pairs;
+    q.pairs = out->pairs;
+    q.shifts = out->shifts;
+    q.dist = (T*)out->distances;
+    q.vec = (T*)out->vectors;
+    q.src = out->sources;
+    q.dst = out->targets;
+    q.edge = out->edge_index;
+    k_skin_emit<T><<<blocks_for(list->n_pairs), kBlock, 0, stream>>>(
+        skin_args(req, list), q, (const long long*)(base + L.offsets));
+    return hipGetLastError();
+}
+
+static double bits_double(int64_t v) {
+    double d;
+    std::memcpy(&d, &v, sizeof d);
+    return d;
+}
+
+// Whether the filtered list equals a search at `cutoff` for the current
+// positions.  With eps the input type's machine epsilon, m the largest atom
+// displacement, A the largest |x|_1, K the largest skin_condition and
+// Cb the build cutoff: every pair within the cutoff now has
+// |S cell|_2 <= 3 (cutoff + 2A) (when 2 eps K <= 1/3), so the terms of its
+// public D sum to at most M = 2A + 3 (cutoff + 2A) K in 1-norm and its
+// rounded D lies within 2 eps M of the exact one; the exact D moved by at
+// most 2m since the build, and the rounded d^2 and squared cutoffs add
+// relative errors of a few eps.  The pair was then in the stored list when
+//   cutoff (1 + 2e) + 2m (1 + 4e) + 2e M + 2e (M + 4m) < Cb (1 - 3e),
+// here with e = 2 eps, twice the error bounds.
+static bool skin_valid(int32_t dtype, double cutoff, double build_cutoff, const int64_t* h) {
+    if (h[SK_CHANGED]) return false;
+    const double eps = dtype == TNR_FLOAT32 ? 0x1p-23 : 0x1p-52;
+    const double e = 2 * eps;
+    const double m = std::sqrt(bits_double(h[SK_MAX_DISP2])) * (1 + 1e-12);
+    const double A = bits_double(h[SK_MAX_COORD]) * (1 + 1e-12);
+    const double K = bits_double(h[SK_MAX_COND]);
+    if (!(2 * eps * K <= 1.0 / 3.0)) return false;
+    const double M = 2 * A + 3 * (cutoff + 2 * A) * K;
+    const double lhs = cutoff * (1 + 2 * e) + 2 * m * (1 + 4 * e) + 2 * e * M + 2 * e * (M + 4 * m);
+    return lhs < build_cutoff * (1 - 3 * e);
+}
+
 }  // namespace tnr
 
 // ----------------------------------------------------------------- C ABI
@@ -543,6 +686,64 @@ int tnr_search_static(const tnr_request* req, const tnr_outputs* out, int64_t* h
     o.plan = -1;
     o.n_tasks = 0;
     return tnr_emit(req, ws, tnr::kStaticScratchBytes, &o, stream, err, err_len);
+}
+
+size_t tnr_skin_workspace_size(const tnr_request* req, const tnr_skin_list* list) {
+    if (!req || !list || req->n_atoms < 0 || req->n_structures < 0 || list->n_pairs < 0)
+        return 0;
+    return tnr::skin_layout(list->n_pairs, req->n_atoms, req->n_structures).total;
+}
+
+int tnr_skin_count_async(const tnr_request* req, const tnr_skin_list* list, void* workspace,
+                         size_t workspace_bytes, int64_t* host_result, void* stream, char* err,
+                         size_t err_len) {
+    tnr::SkinLayout L;
+    const int rc = tnr::check_skin(req, list, workspace_bytes, workspace, err, err_len, &L);
+    if (rc != TNR_OK) return rc;
+    if (!host_result) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "host_result is null");
+    hipStream_t s = (hipStream_t)stream;
+    void* mapped = nullptr;
+    if (hipHostGetDevicePointer(&mapped, host_result, 0) != hipSuccess) {
+        mapped = nullptr;
+        (void)hipGetLastError();
+    }
+    hipError_t e = req->dtype == TNR_FLOAT32
+                       ? tnr::run_skin_count<float>(req, list, workspace, L, s, (long long*)mapped)
+                       : tnr::run_skin_count<double>(req, list, workspace, L, s, (long long*)mapped);
+    if (e == hipSuccess && !mapped)
+        e = hipMemcpyAsync(host_result, (char*)workspace + L.status,
+                           TNR_HOST_RESULT_SLOTS * sizeof(int64_t), hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
+    return TNR_OK;
+}
+
+int tnr_skin_finish(const tnr_request* req, const tnr_skin_list* list, const int64_t* host_result,
+                    int64_t* n_pairs, int32_t* rebuild, char* err, size_t err_len) {
+    if (!req || !list || !host_result || !n_pairs || !rebuild)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "result pointers are null");
+    if ((unsigned long long)host_result[tnr::SK_FLAGS] & tnr::ST_SCAN_STALL)
+        return tnr::put_error(err, err_len, TNR_SEARCH_ERROR,
+                              "a device-wide scan of the neighbor search did not complete");
+    const bool ok = tnr::skin_valid(req->dtype, req->cutoff, list->build_cutoff, host_result);
+    *rebuild = ok ? 0 : 1;
+    *n_pairs = ok ? host_result[tnr::SK_PAIRS] : 0;
+    return TNR_OK;
+}
+
+int tnr_skin_emit(const tnr_request* req, const tnr_skin_list* list, void* workspace,
+                  size_t workspace_bytes, const tnr_outputs* out, void* stream, char* err,
+                  size_t err_len) {
+    tnr::SkinLayout L;
+    const int rc = tnr::check_skin(req, list, workspace_bytes, workspace, err, err_len, &L);
+    if (rc != TNR_OK) return rc;
+    if (!out) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "outputs are null");
+    if (out->n_pairs <= 0 || list->n_pairs == 0) return TNR_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const hipError_t e = req->dtype == TNR_FLOAT32
+                             ? tnr::run_skin_emit<float>(req, list, workspace, L, out, s)
+                             : tnr::run_skin_emit<double>(req, list, workspace, L, out, s);
+    if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
+    return TNR_OK;
 }
 
 int tnr_geometry_backward(int32_t dtype, int64_t n_pairs, int64_t n_atoms, int64_t n_structures,
