@@ -166,50 +166,56 @@ int tnr_search_static(const tnr_request* req, const tnr_outputs* out, int64_t* h
 /*
  * Verlet-skin lists.  No counterpart in the reference, which lists a Verlet
  * skin as unsupported (docs/design.md:125-127); for molecular-dynamics
- * loops that search every step.  The caller builds a list with
- * tnr_count / tnr_emit (P and S) at build_cutoff = cutoff + skin and keeps
- * copies of that call's positions, cell, pbc and batch_ptr.  At a later step
- * (a request with the same dtype, N, B and pair policy, and the filter
- * cutoff in req->cutoff) the stored pairs are re-decided with the reference's
- * public predicate at the current positions.  tnr_skin_finish says whether
- * the result equals a fresh search (every atom moved less than about
- * skin / 2, less a rounding margin, and cell, pbc and batch_ptr unchanged);
- * if not, the caller rebuilds.  The kept pairs come out in stored order.
+ * loops that search every step.  The caller searches once at
+ * build_cutoff = cutoff + skin (tnr_count / tnr_emit, P and S) and stores
+ * that list with tnr_skin_store, which packs it into a workspace (8 bytes per
+ * pair) together with copies of the request's positions, cell, pbc and
+ * batch_ptr.  At a later step, tnr_skin_filter_async re-decides every stored
+ * pair with the reference's public predicate at the current positions and
+ * writes the kept pairs in stored order, in one pass; tnr_skin_finish says
+ * whether the result equals a fresh search at req->cutoff (every atom moved
+ * less than about skin / 2, less a rounding margin, and cell, pbc and
+ * batch_ptr unchanged).  If not, the caller rebuilds.
  */
 typedef struct tnr_skin_list {
-    int64_t n_pairs;              /* rows of the stored list */
-    const int64_t* pairs;         /* int64[n_pairs][2] */
-    const int32_t* shifts;        /* int32[n_pairs][3] */
-    const void* ref_positions;    /* T[N][3] of the build */
-    const void* ref_cell;         /* T[B][3][3] of the build */
-    const uint8_t* ref_pbc;       /* uint8 (bool) [B][3] of the build */
-    const int64_t* ref_batch_ptr; /* int64[B + 1] of the build */
-    double build_cutoff;          /* cutoff of the build; at least req->cutoff */
+    int64_t n_pairs;      /* stored pairs */
+    int64_t n_atoms;      /* N of the stored list's request */
+    int64_t n_structures; /* B */
+    int32_t dtype;
+    int32_t reserved;
+    double build_cutoff;  /* cutoff the stored list was searched with */
 } tnr_skin_list;
 
-/* Device scratch bytes of the filter of `list` for `req`. */
-size_t tnr_skin_workspace_size(const tnr_request* req, const tnr_skin_list* list);
+/* Device bytes of a skin workspace for `req` (dtype, N, B) and n_pairs
+ * stored pairs. */
+size_t tnr_skin_workspace_size(const tnr_request* req, int64_t n_pairs);
 
-/* Enqueues the filter's counting pass on `stream`: displacement and
- * structure checks, kept pairs per block, their scan; the status words reach
- * `host_result` (pinned, TNR_HOST_RESULT_SLOTS int64) when the stream has
- * reached this point.  Uses positions, cell, pbc, batch_ptr, dtype, n_atoms,
- * n_structures and cutoff of `req`. */
-int tnr_skin_count_async(const tnr_request* req, const tnr_skin_list* list, void* workspace,
-                         size_t workspace_bytes, int64_t* host_result, void* stream, char* err,
-                         size_t err_len);
+/* Stores the list (pairs, shifts: the n_pairs rows that tnr_emit wrote for
+ * `req` at build_cutoff, 16-byte aligned pairs) and the request's positions,
+ * cell, pbc and batch_ptr in `workspace`, on `stream`; fills `list`.  Shifts
+ * beyond [-512, 511] or pairs whose sources are not contiguous make the list
+ * unfilterable: every later tnr_skin_finish then asks for a rebuild. */
+int tnr_skin_store(const tnr_request* req, double build_cutoff, const int64_t* pairs,
+                   const int32_t* shifts, int64_t n_pairs, void* workspace,
+                   size_t workspace_bytes, tnr_skin_list* list, void* stream, char* err,
+                   size_t err_len);
 
-/* Decodes a completed tnr_skin_count_async: *rebuild = 1 when the filtered
- * list may differ from a fresh search at req->cutoff (the caller rebuilds);
- * otherwise *rebuild = 0 and *n_pairs receives E. */
+/* Filters the stored list at req's positions, cell and cutoff (dtype, N and
+ * B as stored) into `out` (P, S, d, D, i, j; no edge_index), rows at and
+ * beyond out->n_pairs being dropped: out->n_pairs = list->n_pairs always
+ * suffices.  The status words reach `host_result` (pinned,
+ * TNR_HOST_RESULT_SLOTS int64) when the stream has reached this point. */
+int tnr_skin_filter_async(const tnr_request* req, const tnr_skin_list* list, void* workspace,
+                          size_t workspace_bytes, const tnr_outputs* out, int64_t* host_result,
+                          void* stream, char* err, size_t err_len);
+
+/* Decodes a completed tnr_skin_filter_async: *rebuild = 1 when the filtered
+ * list may differ from a fresh search (the caller rebuilds); otherwise
+ * *rebuild = 0 and *n_pairs receives E (when E exceeds the out->n_pairs of
+ * the filter, rows beyond it were dropped: filter again into larger
+ * outputs). */
 int tnr_skin_finish(const tnr_request* req, const tnr_skin_list* list, const int64_t* host_result,
                     int64_t* n_pairs, int32_t* rebuild, char* err, size_t err_len);
-
-/* Writes the kept pairs' requested quantities (out->plan and out->n_tasks
- * are ignored) for the filter last counted in `workspace`. */
-int tnr_skin_emit(const tnr_request* req, const tnr_skin_list* list, void* workspace,
-                  size_t workspace_bytes, const tnr_outputs* out, void* stream, char* err,
-                  size_t err_len);
 
 /*
  * Backward of the d/D outputs of tnr_emit: adds the gradients of positions

@@ -223,43 +223,61 @@ def test_runtime_check_follows_the_hip_major_version(lib):
 
 
 def test_skin_list_layout_and_workspace(lib):
-    assert ctypes.sizeof(ext.SkinList) == 64 and ext.SkinList.build_cutoff.offset == 56
+    assert ctypes.sizeof(ext.SkinList) == 40 and ext.SkinList.build_cutoff.offset == 32
     req = _request(n_atoms=1000)
-    small = ext.SkinList(n_pairs=10, build_cutoff=1.5)
-    large = ext.SkinList(n_pairs=10_000_000, build_cutoff=1.5)
-    a = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(small))
-    b = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(large))
+    a = lib.tnr_skin_workspace_size(ctypes.byref(req), 10)
+    b = lib.tnr_skin_workspace_size(ctypes.byref(req), 10_000_000)
+    # 8 bytes per stored pair, plus per-tile data
     assert 0 < a < b and a % 256 == 0 and b % 256 == 0
-    assert lib.tnr_skin_workspace_size(ctypes.byref(req), None) == 0
+    assert 8 * 10_000_000 <= b - a < 9 * 10_000_000
+    assert lib.tnr_skin_workspace_size(ctypes.byref(req), -1) == 0
+    assert lib.tnr_skin_workspace_size(None, 10) == 0
 
 
-def _skin_count(lib, req, lst, ws=1 << 24, ws_bytes=None, host=1 << 25):
+def _skin_store(lib, req, build_cutoff=1.5, n=5, pairs=1 << 26, shifts=1 << 27, ws=1 << 24,
+                ws_bytes=None):
     err = ctypes.create_string_buffer(256)
     if ws_bytes is None:
-        ws_bytes = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(lst))
-    code = lib.tnr_skin_count_async(ctypes.byref(req), ctypes.byref(lst), ws, ws_bytes, host,
-                                    None, err, len(err))
+        ws_bytes = lib.tnr_skin_workspace_size(ctypes.byref(req), max(n, 0))
+    lst = ext.SkinList()
+    code = lib.tnr_skin_store(ctypes.byref(req), build_cutoff, pairs, shifts, n, ws, ws_bytes,
+                              ctypes.byref(lst), None, err, len(err))
     return code, err.value.decode()
 
 
 def test_skin_requests_are_rejected_on_the_host(lib):
     req = _request(n_atoms=100)
-    ok = dict(n_pairs=5, pairs=1 << 26, shifts=1 << 27, ref_positions=1 << 28,
-              ref_cell=1 << 29, ref_pbc=1 << 30, ref_batch_ptr=1 << 31, build_cutoff=1.5)
-    for fields, message in (
+    for kw, message in (
         ({"build_cutoff": 0.5}, "at least the cutoff"),
         ({"build_cutoff": float("nan")}, "at least the cutoff"),
         ({"pairs": None}, "required pointers"),
-        ({"ref_positions": None}, "required pointers"),
-        ({"n_pairs": -1}, "invalid sizes"),
+        ({"n": -1}, "invalid sizes"),
+        ({"ws": (1 << 24) + 8}, "256-byte aligned"),
     ):
-        code, text = _skin_count(lib, req, ext.SkinList(**{**ok, **fields}))
+        code, text = _skin_store(lib, req, **kw)
         assert code == ext.TNR_INPUT_ERROR and message in text, text
-    lst = ext.SkinList(**ok)
-    need = lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(lst))
-    assert _skin_count(lib, req, lst, ws_bytes=need - 256)[0] == ext.TNR_INPUT_ERROR
-    assert _skin_count(lib, req, lst, ws=(1 << 24) + 8)[0] == ext.TNR_INPUT_ERROR
-    code, text = _skin_count(lib, req, lst, host=0)
-    assert code == ext.TNR_INPUT_ERROR and "host_result" in text
-    code, text = _skin_count(lib, _request(n_atoms=100, cutoff=-1.0), lst)
+    need = lib.tnr_skin_workspace_size(ctypes.byref(req), 5)
+    assert _skin_store(lib, req, ws_bytes=need - 256)[0] == ext.TNR_INPUT_ERROR
+    code, text = _skin_store(lib, _request(n_atoms=100, cutoff=-1.0))
     assert code == ext.TNR_INPUT_ERROR and "cutoff" in text
+    # a filter whose request does not match the stored list
+    err = ctypes.create_string_buffer(256)
+    lst = ext.SkinList(n_pairs=5, n_atoms=100, n_structures=1, dtype=0, build_cutoff=1.5)
+    out = ext.Outputs(n_pairs=5)
+    need = lib.tnr_skin_workspace_size(ctypes.byref(req), 5)
+
+    def run(r, o=out, host=1 << 25):
+        code = lib.tnr_skin_filter_async(ctypes.byref(r), ctypes.byref(lst), 1 << 24, need,
+                                         ctypes.byref(o), host, None, err, len(err))
+        return code, err.value.decode()
+
+    code, text = run(_request(n_atoms=101))
+    assert code == ext.TNR_INPUT_ERROR and "differ from the stored list" in text
+    code, text = run(_request(n_atoms=100, dtype=1))
+    assert code == ext.TNR_INPUT_ERROR
+    code, text = run(_request(n_atoms=100, cutoff=2.0))
+    assert code == ext.TNR_INPUT_ERROR and "at least the cutoff" in text
+    code, text = run(req, ext.Outputs(n_pairs=5, edge_index=1 << 28))
+    assert code == ext.TNR_INPUT_ERROR and "edge-first" in text
+    code, text = run(req, host=0)
+    assert code == ext.TNR_INPUT_ERROR and "host_result" in text

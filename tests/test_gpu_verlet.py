@@ -247,3 +247,48 @@ def test_gradients_equal_the_public_call():
         assert torch.allclose(gc, cell.grad, rtol=1e-10, atol=1e-10)
         t = _walk(t, np.random.default_rng(13), 0.05)
     assert vl.builds == 1
+
+
+def test_shifts_beyond_the_compact_records_fall_back_to_searches():
+    # a 0.05 A period along x with a 30 A cutoff: shifts up to about +-600,
+    # beyond the stored records' 10-bit fields; every call then equals a
+    # direct search
+    pos = torch.tensor([[0.01, 0.0, 0.0], [0.02, 1.0, 0.5], [0.03, -0.5, 2.0]],
+                       dtype=torch.float64, device=DEV)
+    cell = torch.diag(torch.tensor([0.05, 10.0, 10.0], dtype=torch.float64)).to(DEV)
+    pbc = torch.tensor([True, False, False], device=DEV)
+    bp = torch.tensor([0, 3], device=DEV)
+    t = {"positions": pos, "cell": cell[None], "pbc": pbc[None], "batch_ptr": bp}
+    vl = VerletList("PSdD", 30.0, 0.5)
+    for _ in range(2):
+        P = _assert_equal_to_fresh(vl, t, 30.0)
+        assert P.shape[0] > 3000
+        assert int(neighbor_list("S", pos, cell, pbc, 30.0)[0].abs().max()) > 511
+        t = dict(t, positions=t["positions"] + 0.001)
+
+
+def test_sources_recovered_across_tiles_and_empty_structures():
+    # structures of 0 to 300 atoms: runs of every length, tiles that start
+    # inside a run, empty structures in batch_ptr
+    rng = np.random.default_rng(14)
+    counts = [0, 300, 1, 0, 57, 2, 0, 180, 0]
+    positions, cells = [], []
+    for n in counts:
+        L = 9.0
+        positions.append(rng.uniform(0, L, size=(n, 3)))
+        cells.append(L * np.eye(3))
+    cfg = {
+        "positions": np.concatenate(positions).astype(np.float32),
+        "cell": np.stack(cells).astype(np.float32),
+        "pbc": np.ones((len(counts), 3), bool),
+        "batch_ptr": np.concatenate([[0], np.cumsum(counts)]).astype(np.int64),
+        "cutoff": 4.0,
+    }
+    t = _t(cfg)
+    for sorted_ in (True, False):
+        vl = VerletList("PSdD", 4.0, 0.8, sorted=sorted_)
+        for _ in range(3):
+            P = _assert_equal_to_fresh(vl, t, 4.0, sorted=sorted_)
+            assert P.shape[0] > 2 * 2048
+            t = _walk(t, rng, 0.1)
+        assert vl.builds == 1

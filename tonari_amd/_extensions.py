@@ -31,9 +31,9 @@ EXPORTS = (
     "tnr_emit",
     "tnr_search_static",
     "tnr_skin_workspace_size",
-    "tnr_skin_count_async",
+    "tnr_skin_store",
+    "tnr_skin_filter_async",
     "tnr_skin_finish",
-    "tnr_skin_emit",
 )
 
 
@@ -79,12 +79,10 @@ class SkinList(ctypes.Structure):
 
     _fields_ = [
         ("n_pairs", ctypes.c_int64),
-        ("pairs", ctypes.c_void_p),
-        ("shifts", ctypes.c_void_p),
-        ("ref_positions", ctypes.c_void_p),
-        ("ref_cell", ctypes.c_void_p),
-        ("ref_pbc", ctypes.c_void_p),
-        ("ref_batch_ptr", ctypes.c_void_p),
+        ("n_atoms", ctypes.c_int64),
+        ("n_structures", ctypes.c_int64),
+        ("dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
         ("build_cutoff", ctypes.c_double),
     ]
 
@@ -137,22 +135,24 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
         ctypes.c_char_p, ctypes.c_size_t,
     ]
     lib.tnr_skin_workspace_size.restype = ctypes.c_size_t
-    lib.tnr_skin_workspace_size.argtypes = [ctypes.POINTER(Request), ctypes.POINTER(SkinList)]
-    lib.tnr_skin_count_async.restype = ctypes.c_int
-    lib.tnr_skin_count_async.argtypes = [
+    lib.tnr_skin_workspace_size.argtypes = [ctypes.POINTER(Request), ctypes.c_int64]
+    lib.tnr_skin_store.restype = ctypes.c_int
+    lib.tnr_skin_store.argtypes = [
+        ctypes.POINTER(Request), ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(SkinList),
+        ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_skin_filter_async.restype = ctypes.c_int
+    lib.tnr_skin_filter_async.argtypes = [
         ctypes.POINTER(Request), ctypes.POINTER(SkinList), ctypes.c_void_p, ctypes.c_size_t,
-        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+        ctypes.POINTER(Outputs), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p,
+        ctypes.c_size_t,
     ]
     lib.tnr_skin_finish.restype = ctypes.c_int
     lib.tnr_skin_finish.argtypes = [
         ctypes.POINTER(Request), ctypes.POINTER(SkinList), ctypes.c_void_p,
         ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32), ctypes.c_char_p,
         ctypes.c_size_t,
-    ]
-    lib.tnr_skin_emit.restype = ctypes.c_int
-    lib.tnr_skin_emit.argtypes = [
-        ctypes.POINTER(Request), ctypes.POINTER(SkinList), ctypes.c_void_p, ctypes.c_size_t,
-        ctypes.POINTER(Outputs), ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
     ]
     version = lib.tnr_abi_version()
     if version != ABI_VERSION:

@@ -49,6 +49,47 @@ __device__ __forceinline__ unsigned long long tile_read(const unsigned long long
     return __hip_atomic_load(t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Decoupled look-back of tile `tile` with aggregate `total`, run by one
+// whole wave: publishes the aggregate, then looks back over the 64
+// preceding tiles at a time (one read per lane) and adds the aggregates
+// down to the nearest inclusive prefix, publishes its own inclusive prefix
+// and returns the exclusive prefix (in every lane).  The wait on an earlier
+// tile is bounded (kLookbackSpins polls); on expiry ST_SCAN_STALL is raised
+// and the wave goes on, so every wave exits.
+__device__ __forceinline__ long long lookback_exclusive(unsigned long long* tiles, int64_t tile,
+                                                        long long total,
+                                                        unsigned long long* status) {
+    const int lane = lane_id();
+    long long excl = 0;
+    if (tile > 0) {
+        if (lane == 0) tile_publish(tiles + tile, kTileAggregate | (unsigned long long)total);
+        for (int64_t hi = tile - 1;; hi -= kWave) {
+            const int64_t t = hi - lane;
+            // tiles before the first count as an inclusive prefix of 0
+            unsigned long long w = t >= 0 ? tile_read(tiles + t) : kTilePrefix;
+            for (int spin = 0; spin < kLookbackSpins; ++spin) {
+                if (!__builtin_amdgcn_ballot_w64((w >> 62) == 0)) break;
+                __builtin_amdgcn_s_sleep(1);
+                if ((w >> 62) == 0) w = tile_read(tiles + t);
+            }
+            if (__builtin_amdgcn_ballot_w64((w >> 62) == 0)) {
+                if (lane == 0) atomicOr(status + SS_FLAGS, ST_SCAN_STALL);
+                break;
+            }
+            const unsigned long long pm =
+                __builtin_amdgcn_ballot_w64((w & ~kTileValue) == kTilePrefix);
+            const int stop = pm ? __builtin_ctzll(pm) : kWave - 1;
+            long long part = lane <= stop ? (long long)(w & kTileValue) : 0;
+#pragma unroll
+            for (int d = kWave / 2; d > 0; d >>= 1) part += __shfl_xor(part, d);
+            excl += part;
+            if (pm) break;
+        }
+    }
+    if (lane == 0) tile_publish(tiles + tile, kTilePrefix | (unsigned long long)(excl + total));
+    return excl;
+}
+
 // Exclusive scan of n (min(n, *n_dev) when n_dev is given) non-negative values of
 // `in` into out[0..n], out[n] = total, in one launch.  Blocks take tiles of
 // kScanTile items in the order they start (an atomic ticket), so every
@@ -92,37 +133,8 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     long long total;
     const long long ex = block_exclusive_scan(s, &total);
     if (threadIdx.x < kWave) {
-        const int lane = lane_id();
-        long long excl = 0;
-        if (tile > 0) {
-            if (lane == 0) tile_publish(tiles + tile, kTileAggregate | (unsigned long long)total);
-            for (int64_t hi = tile - 1;; hi -= kWave) {
-                const int64_t t = hi - lane;
-                // tiles before the first count as an inclusive prefix of 0
-                unsigned long long w = t >= 0 ? tile_read(tiles + t) : kTilePrefix;
-                for (int spin = 0; spin < kLookbackSpins; ++spin) {
-                    if (!__builtin_amdgcn_ballot_w64((w >> 62) == 0)) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if ((w >> 62) == 0) w = tile_read(tiles + t);
-                }
-                if (__builtin_amdgcn_ballot_w64((w >> 62) == 0)) {
-                    if (lane == 0) atomicOr(status + SS_FLAGS, ST_SCAN_STALL);
-                    break;
-                }
-                const unsigned long long pm =
-                    __builtin_amdgcn_ballot_w64((w & ~kTileValue) == kTilePrefix);
-                const int stop = pm ? __builtin_ctzll(pm) : kWave - 1;
-                long long part = lane <= stop ? (long long)(w & kTileValue) : 0;
-#pragma unroll
-                for (int d = kWave / 2; d > 0; d >>= 1) part += __shfl_xor(part, d);
-                excl += part;
-                if (pm) break;
-            }
-        }
-        if (lane == 0) {
-            tile_publish(tiles + tile, kTilePrefix | (unsigned long long)(excl + total));
-            s_excl = excl;
-        }
+        const long long excl = lookback_exclusive(tiles, tile, total, status);
+        if (lane_id() == 0) s_excl = excl;
     }
     __syncthreads();
     long long run = s_excl + ex;

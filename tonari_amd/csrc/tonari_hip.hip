@@ -433,102 +433,202 @@ static int scratch_address(void** out, char* err, size_t err_len) {
     return TNR_OK;
 }
 
-// ------------------------------------------------------- Verlet-skin filter
+// ------------------------------------------------------- Verlet-skin lists
 
 struct SkinLayout {
-    int64_t blocks, n_tiles;
-    size_t status, counts, offsets, tiles, total;
+    int64_t n_wtiles, cap_runs, n_scan_tiles, n_scan_tiles2;
+    int64_t n_parts;
+    size_t status, persist, copy, parts, tiles, tiles2, wtile_starts, wtile_runs_before, wtile_kept,
+        wtile_offsets, wtile_run0, runs, rank, perm, nonsrc, nonsrc_before, placed, records,
+        ref_pos, ref_cell, ref_pbc, ref_bp, total;
 };
 
-// Workgroups of the filter's counting pass: one thread per stored pair, per
-// atom and per cell entry, whichever is most.
-static SkinLayout skin_layout(int64_t n_pairs, int64_t n_atoms, int64_t nb) {
-    int64_t g = n_pairs > n_atoms ? n_pairs : n_atoms;
-    if (9 * nb + 1 > g) g = 9 * nb + 1;
+// The skin workspace: the filter's status block, the store's persistent
+// words, the host copy of the status, look-back tile states of the scans
+// over wave tiles and over atoms, per-wave-tile run data and counts, the run
+// table (at most one run per atom), places, positions in place order, the
+// 8-byte records and copies of the build's inputs.
+static SkinLayout skin_layout(int64_t n_pairs, int64_t n_atoms, int64_t nb, size_t tsize) {
     SkinLayout L;
-    L.blocks = (g + kBlock - 1) / kBlock;
-    L.n_tiles = (L.blocks + kScanTile - 1) / kScanTile;
+    L.n_wtiles = (n_pairs + kSkinWaveTile - 1) / kSkinWaveTile;
+    L.cap_runs = n_atoms > 0 ? n_atoms : 1;
+    L.n_scan_tiles = (L.n_wtiles + kScanTile - 1) / kScanTile;
+    L.n_scan_tiles2 = (n_atoms + kScanTile - 1) / kScanTile;
     size_t o = 0;
     auto take = [&](size_t bytes) {
         const size_t at = o;
         o = align_up(o + bytes);
         return at;
     };
+    const size_t wtiles = (size_t)(L.n_wtiles > 0 ? L.n_wtiles : 1);
+    const size_t atoms = (size_t)(n_atoms > 0 ? n_atoms : 1);
     L.status = take(sizeof(int64_t) * SS_SLOTS);
-    L.counts = take(sizeof(int64_t) * (size_t)(L.blocks + 1));
-    L.offsets = take(sizeof(int64_t) * (size_t)(L.blocks + 1));
-    L.tiles = take(sizeof(int64_t) * (size_t)L.n_tiles);
+    L.persist = take(sizeof(int64_t) * SP_WORDS);
+    L.copy = take(sizeof(int64_t) * kHostResultSlots);
+    // one workgroup of the place kernel per 256 atoms or cell entries
+    const int64_t place = n_atoms > 9 * nb + 1 ? n_atoms : 9 * nb + 1;
+    L.n_parts = (place + kBlock - 1) / kBlock;
+    L.parts = take(sizeof(int64_t) * 4 * (size_t)L.n_parts);
+    L.tiles = take(sizeof(int64_t) * (size_t)(L.n_scan_tiles > 0 ? L.n_scan_tiles : 1));
+    L.tiles2 = take(sizeof(int64_t) * (size_t)(L.n_scan_tiles2 > 0 ? L.n_scan_tiles2 : 1));
+    L.wtile_starts = take(sizeof(int64_t) * (wtiles + 1));
+    L.wtile_runs_before = take(sizeof(int64_t) * (wtiles + 1));
+    L.wtile_kept = take(sizeof(int64_t) * (wtiles + 1));
+    L.wtile_offsets = take(sizeof(int64_t) * (wtiles + 1));
+    L.wtile_run0 = take(sizeof(int32_t) * wtiles);
+    L.runs = take(sizeof(int32_t) * 2 * (size_t)L.cap_runs);
+    L.rank = take(sizeof(int32_t) * atoms);
+    L.perm = take(sizeof(int32_t) * atoms);
+    L.nonsrc = take(sizeof(int32_t) * atoms);
+    L.nonsrc_before = take(sizeof(int32_t) * (atoms + 1));
+    L.placed = take(tsize * 4 * atoms);
+    L.records = take(sizeof(int64_t) * (size_t)(n_pairs > 0 ? n_pairs : 1));
+    L.ref_pos = take(tsize * 3 * atoms);
+    L.ref_cell = take(tsize * 9 * (size_t)(nb > 0 ? nb : 1));
+    L.ref_pbc = take(3 * (size_t)(nb > 0 ? nb : 1));
+    L.ref_bp = take(sizeof(int64_t) * (size_t)(nb + 1));
     L.total = o;
     return L;
 }
 
-static int check_skin(const tnr_request* req, const tnr_skin_list* list, size_t ws_bytes,
-                      const void* ws, char* err, size_t err_len, SkinLayout* L) {
-    if (!req || !list) return put_error(err, err_len, TNR_INPUT_ERROR, "request or list is null");
+static size_t dtype_size(int32_t dtype) { return dtype == TNR_FLOAT32 ? sizeof(float) : sizeof(double); }
+
+// Checks shared by the store and the filter: the request (dtype, cutoff,
+// sizes, input pointers) and the workspace.
+static int check_skin_request(const tnr_request* req, int64_t n_pairs, size_t ws_bytes,
+                              const void* ws, char* err, size_t err_len, SkinLayout* L) {
+    if (!req) return put_error(err, err_len, TNR_INPUT_ERROR, "request is null");
     if (req->dtype != TNR_FLOAT32 && req->dtype != TNR_FLOAT64)
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "positions must have dtype float32 or float64");
     if (!(std::isfinite(req->cutoff) && req->cutoff > 0))
         return put_error(err, err_len, TNR_INPUT_ERROR, "cutoff must be finite and positive");
-    if (!(std::isfinite(list->build_cutoff) && list->build_cutoff >= req->cutoff))
-        return put_error(err, err_len, TNR_INPUT_ERROR,
-                         "the list's build cutoff must be finite and at least the cutoff");
-    if (req->n_atoms < 0 || req->n_structures < 1 || list->n_pairs < 0 ||
+    if (req->n_atoms < 0 || req->n_structures < 1 || n_pairs < 0 ||
         req->n_atoms >= (int64_t{1} << 31))
         return put_error(err, err_len, TNR_INPUT_ERROR, "invalid sizes");
-    if (!req->batch_ptr || !req->cell || !req->pbc || !list->ref_cell || !list->ref_pbc ||
-        !list->ref_batch_ptr || (req->n_atoms > 0 && (!req->positions || !list->ref_positions)) ||
-        (list->n_pairs > 0 && (!list->pairs || !list->shifts)))
+    if (!req->batch_ptr || !req->cell || !req->pbc || (req->n_atoms > 0 && !req->positions))
         return put_error(err, err_len, TNR_INPUT_ERROR, "required pointers are null");
-    *L = skin_layout(list->n_pairs, req->n_atoms, req->n_structures);
+    *L = skin_layout(n_pairs, req->n_atoms, req->n_structures, dtype_size(req->dtype));
     if (!ws || ws_bytes < L->total || ((uintptr_t)ws & 255) != 0)
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "workspace is missing, too small or not 256-byte aligned");
     return TNR_OK;
 }
 
-static SkinArgs skin_args(const tnr_request* req, const tnr_skin_list* list) {
-    SkinArgs k{};
-    k.n_pairs = list->n_pairs;
-    k.n_atoms = req->n_atoms;
-    k.nb = req->n_structures;
-    k.pairs = list->pairs;
-    k.shifts = list->shifts;
-    k.bp = req->batch_ptr;
-    k.pbc = req->pbc;
-    k.ref_pos = list->ref_positions;
-    k.ref_cell = list->ref_cell;
-    k.ref_pbc = list->ref_pbc;
-    k.ref_bp = list->ref_batch_ptr;
-    k.cutoff = req->cutoff;
-    return k;
+static int check_skin_list(const tnr_request* req, const tnr_skin_list* list, char* err,
+                           size_t err_len) {
+    if (!list) return put_error(err, err_len, TNR_INPUT_ERROR, "list is null");
+    if (list->dtype != req->dtype || list->n_atoms != req->n_atoms ||
+        list->n_structures != req->n_structures)
+        return put_error(err, err_len, TNR_INPUT_ERROR,
+                         "the request's dtype, N or B differ from the stored list's");
+    if (!(std::isfinite(list->build_cutoff) && list->build_cutoff >= req->cutoff))
+        return put_error(err, err_len, TNR_INPUT_ERROR,
+                         "the list's build cutoff must be finite and at least the cutoff");
+    return TNR_OK;
+}
+
+static unsigned skin_blocks(int64_t n_wtiles) {
+    const int64_t b = (n_wtiles + kWavesPerBlock - 1) / kWavesPerBlock;
+    return (unsigned)(b > 0 ? b : 1);
 }
 
 template <typename T>
-static hipError_t run_skin_count(const tnr_request* req, const tnr_skin_list* list, void* ws,
-                                 const SkinLayout& L, hipStream_t stream, long long* host_out) {
+static hipError_t run_skin_store(const tnr_request* req, const int64_t* pairs,
+                                 const int32_t* shifts, int64_t n_pairs, void* ws,
+                                 const SkinLayout& L, hipStream_t stream) {
     char* base = (char*)ws;
     auto* status = (unsigned long long*)(base + L.status);
-    auto* counts = (long long*)(base + L.counts);
-    auto* offsets = (long long*)(base + L.offsets);
+    auto* persist = (unsigned long long*)(base + L.persist);
     auto* tiles = (unsigned long long*)(base + L.tiles);
-    k_skin_clear<<<1, kBlock, 0, stream>>>(status, tiles, L.n_tiles);
-    k_skin_count<T><<<(unsigned)L.blocks, kBlock, 0, stream>>>(
-        skin_args(req, list), (const T*)req->positions, (const T*)req->cell, counts, status);
-    k_scan_lookback<long long, long long><<<(unsigned)L.n_tiles, kBlock, 0, stream>>>(
-        counts, L.blocks, nullptr, offsets, tiles, status + SK_TICKET, status,
-        status + SK_PAIRS, host_out);
+    auto* tiles2 = (unsigned long long*)(base + L.tiles2);
+    const int64_t n_tiles = L.n_scan_tiles > 0 ? L.n_scan_tiles : 1;
+    const int64_t n_tiles2 = L.n_scan_tiles2 > 0 ? L.n_scan_tiles2 : 1;
+    SkinStore k{};
+    k.n_pairs = n_pairs;
+    k.n_atoms = req->n_atoms;
+    k.nb = req->n_structures;
+    k.n_wtiles = L.n_wtiles;
+    k.cap_runs = L.cap_runs;
+    k.pairs = pairs;
+    k.shifts = shifts;
+    k.pos = req->positions;
+    k.cell = req->cell;
+    k.pbc = req->pbc;
+    k.bp = req->batch_ptr;
+    k.records = (unsigned long long*)(base + L.records);
+    k.runs = (int2*)(base + L.runs);
+    k.wtile_run0 = (int*)(base + L.wtile_run0);
+    k.wtile_starts = (long long*)(base + L.wtile_starts);
+    k.wtile_runs_before = (const long long*)(base + L.wtile_runs_before);
+    k.rank = (int*)(base + L.rank);
+    k.perm = (int*)(base + L.perm);
+    k.nonsrc = (int*)(base + L.nonsrc);
+    k.nonsrc_before = (const int*)(base + L.nonsrc_before);
+    k.ref_pos = base + L.ref_pos;
+    k.ref_cell = base + L.ref_cell;
+    k.ref_pbc = (uint8_t*)(base + L.ref_pbc);
+    k.ref_bp = (int64_t*)(base + L.ref_bp);
+    k.persist = persist;
+    k_skin_clear<<<1, kBlock, 0, stream>>>(status, tiles, n_tiles, persist, tiles2, n_tiles2);
+    // the copies need about one block per 2048 input words; the records one
+    // per four wave tiles
+    int64_t grid = skin_blocks(L.n_wtiles);
+    const int64_t copy = (3 * req->n_atoms + kSkinBlockPairs - 1) / kSkinBlockPairs;
+    if (copy > grid) grid = copy;
+    k_skin_pack<T><<<(unsigned)grid, kBlock, 0, stream>>>(k);
+    if (L.n_wtiles > 0) {
+        k_scan_lookback<long long, long long><<<(unsigned)L.n_scan_tiles, kBlock, 0, stream>>>(
+            (const long long*)k.wtile_starts, L.n_wtiles, nullptr,
+            (long long*)(base + L.wtile_runs_before), tiles, persist + SP_TICKET, persist,
+            persist + SP_RUNS, nullptr);
+        k_skin_runs<<<skin_blocks(L.n_wtiles), kBlock, 0, stream>>>(k);
+    }
+    if (req->n_atoms > 0) {
+        k_scan_lookback<int, int><<<(unsigned)L.n_scan_tiles2, kBlock, 0, stream>>>(
+            k.nonsrc, req->n_atoms, nullptr, (int*)(base + L.nonsrc_before), tiles2,
+            persist + SP_TICKET2, persist, nullptr, nullptr);
+        k_skin_ranks<<<blocks_for(req->n_atoms), kBlock, 0, stream>>>(k);
+    }
+    if (n_pairs > 0) k_skin_retarget<<<blocks_for(n_pairs), kBlock, 0, stream>>>(k);
+    // the filter starts from zeroed status words and scan tiles
+    k_skin_clear<<<1, kBlock, 0, stream>>>(status, tiles, n_tiles, nullptr, tiles2, 0);
     return hipGetLastError();
 }
 
 template <typename T>
-static hipError_t run_skin_emit(const tnr_request* req, const tnr_skin_list* list, void* ws,
-                                const SkinLayout& L, const tnr_outputs* out, hipStream_t stream) {
+static hipError_t run_skin_filter(const tnr_request* req, const tnr_skin_list* list, void* ws,
+                                  const SkinLayout& L, const tnr_outputs* out,
+                                  hipStream_t stream, long long* host_out) {
     char* base = (char*)ws;
+    auto* status = (unsigned long long*)(base + L.status);
+    auto* persist = (unsigned long long*)(base + L.persist);
+    auto* tiles = (unsigned long long*)(base + L.tiles);
+    SkinFilter k{};
+    k.n_pairs = list->n_pairs;
+    k.n_atoms = req->n_atoms;
+    k.nb = req->n_structures;
+    k.n_wtiles = L.n_wtiles;
+    k.cap_runs = L.cap_runs;
+    k.records = (const unsigned long long*)(base + L.records);
+    k.runs = (const int2*)(base + L.runs);
+    k.wtile_run0 = (const int*)(base + L.wtile_run0);
+    k.perm = (const int*)(base + L.perm);
+    k.ref_pos = base + L.ref_pos;
+    k.ref_cell = base + L.ref_cell;
+    k.ref_pbc = (const uint8_t*)(base + L.ref_pbc);
+    k.ref_bp = (const int64_t*)(base + L.ref_bp);
+    k.bp = req->batch_ptr;
+    k.pbc = req->pbc;
+    k.persist = persist;
+    k.placed = base + L.placed;
+    k.wtile_kept = (long long*)(base + L.wtile_kept);
+    k.wtile_offsets = (const long long*)(base + L.wtile_offsets);
+    k.cutoff = req->cutoff;
     QueryArgs<T> q{};
     q.pos = (const T*)req->positions;
     q.cells = (const T*)req->cell;
-    q.status = (unsigned long long*)(base + L.status);
+    q.status = status;
     q.n_atoms = req->n_atoms;
     q.nb = req->n_structures;
     q.limit = out->n_pairs;
@@ -538,9 +638,20 @@ static hipError_t run_skin_emit(const tnr_request* req, const tnr_skin_list* lis
     q.vec = (T*)out->vectors;
     q.src = out->sources;
     q.dst = out->targets;
-    q.edge = out->edge_index;
-    k_skin_emit<T><<<blocks_for(list->n_pairs), kBlock, 0, stream>>>(
-        skin_args(req, list), q, (const long long*)(base + L.offsets));
+    auto* parts = (unsigned long long*)(base + L.parts);
+    k_skin_place<T><<<(unsigned)L.n_parts, kBlock, 0, stream>>>(k, (const T*)req->positions,
+                                                               (const T*)req->cell, parts);
+    if (L.n_wtiles > 0) {
+        k_skin_count<T><<<skin_blocks(L.n_wtiles), kBlock, 0, stream>>>(k, q);
+        k_scan_lookback<long long, long long><<<(unsigned)L.n_scan_tiles, kBlock, 0, stream>>>(
+            (const long long*)k.wtile_kept, L.n_wtiles, nullptr,
+            (long long*)(base + L.wtile_offsets), tiles, status + SK_TICKET, status,
+            status + SK_PAIRS, nullptr);
+        if (out->n_pairs > 0) k_skin_emit<T><<<skin_blocks(L.n_wtiles), kBlock, 0, stream>>>(k, q);
+    }
+    k_skin_publish<<<1, kBlock, 0, stream>>>(status, persist, parts, L.n_parts, host_out,
+                                             (long long*)(base + L.copy), tiles,
+                                             L.n_scan_tiles > 0 ? L.n_scan_tiles : 1);
     return hipGetLastError();
 }
 
@@ -688,30 +799,69 @@ int tnr_search_static(const tnr_request* req, const tnr_outputs* out, int64_t* h
     return tnr_emit(req, ws, tnr::kStaticScratchBytes, &o, stream, err, err_len);
 }
 
-size_t tnr_skin_workspace_size(const tnr_request* req, const tnr_skin_list* list) {
-    if (!req || !list || req->n_atoms < 0 || req->n_structures < 0 || list->n_pairs < 0)
-        return 0;
-    return tnr::skin_layout(list->n_pairs, req->n_atoms, req->n_structures).total;
+size_t tnr_skin_workspace_size(const tnr_request* req, int64_t n_pairs) {
+    if (!req || req->n_atoms < 0 || req->n_structures < 0 || n_pairs < 0) return 0;
+    return tnr::skin_layout(n_pairs, req->n_atoms, req->n_structures, tnr::dtype_size(req->dtype))
+        .total;
 }
 
-int tnr_skin_count_async(const tnr_request* req, const tnr_skin_list* list, void* workspace,
-                         size_t workspace_bytes, int64_t* host_result, void* stream, char* err,
-                         size_t err_len) {
+int tnr_skin_store(const tnr_request* req, double build_cutoff, const int64_t* pairs,
+                   const int32_t* shifts, int64_t n_pairs, void* workspace,
+                   size_t workspace_bytes, tnr_skin_list* list, void* stream, char* err,
+                   size_t err_len) {
     tnr::SkinLayout L;
-    const int rc = tnr::check_skin(req, list, workspace_bytes, workspace, err, err_len, &L);
+    const int rc =
+        tnr::check_skin_request(req, n_pairs, workspace_bytes, workspace, err, err_len, &L);
     if (rc != TNR_OK) return rc;
-    if (!host_result) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "host_result is null");
+    if (!list) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "list is null");
+    if (!(std::isfinite(build_cutoff) && build_cutoff >= req->cutoff))
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR,
+                              "the list's build cutoff must be finite and at least the cutoff");
+    if (n_pairs > 0 && (!pairs || !shifts))
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "required pointers are null");
+    hipStream_t s = (hipStream_t)stream;
+    const hipError_t e =
+        req->dtype == TNR_FLOAT32
+            ? tnr::run_skin_store<float>(req, pairs, shifts, n_pairs, workspace, L, s)
+            : tnr::run_skin_store<double>(req, pairs, shifts, n_pairs, workspace, L, s);
+    if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
+    list->n_pairs = n_pairs;
+    list->n_atoms = req->n_atoms;
+    list->n_structures = req->n_structures;
+    list->dtype = req->dtype;
+    list->reserved = 0;
+    list->build_cutoff = build_cutoff;
+    return TNR_OK;
+}
+
+int tnr_skin_filter_async(const tnr_request* req, const tnr_skin_list* list, void* workspace,
+                          size_t workspace_bytes, const tnr_outputs* out, int64_t* host_result,
+                          void* stream, char* err, size_t err_len) {
+    tnr::SkinLayout L;
+    if (!list) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "list is null");
+    int rc = tnr::check_skin_request(req, list->n_pairs, workspace_bytes, workspace, err,
+                                     err_len, &L);
+    if (rc != TNR_OK) return rc;
+    rc = tnr::check_skin_list(req, list, err, err_len);
+    if (rc != TNR_OK) return rc;
+    if (!out || !host_result)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "outputs or host_result are null");
+    if (out->edge_index)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR,
+                              "the skin filter does not write the edge-first layout");
+    if (out->n_pairs < 0) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "invalid sizes");
     hipStream_t s = (hipStream_t)stream;
     void* mapped = nullptr;
     if (hipHostGetDevicePointer(&mapped, host_result, 0) != hipSuccess) {
         mapped = nullptr;
         (void)hipGetLastError();
     }
-    hipError_t e = req->dtype == TNR_FLOAT32
-                       ? tnr::run_skin_count<float>(req, list, workspace, L, s, (long long*)mapped)
-                       : tnr::run_skin_count<double>(req, list, workspace, L, s, (long long*)mapped);
+    hipError_t e =
+        req->dtype == TNR_FLOAT32
+            ? tnr::run_skin_filter<float>(req, list, workspace, L, out, s, (long long*)mapped)
+            : tnr::run_skin_filter<double>(req, list, workspace, L, out, s, (long long*)mapped);
     if (e == hipSuccess && !mapped)
-        e = hipMemcpyAsync(host_result, (char*)workspace + L.status,
+        e = hipMemcpyAsync(host_result, (char*)workspace + L.copy,
                            TNR_HOST_RESULT_SLOTS * sizeof(int64_t), hipMemcpyDeviceToHost, s);
     if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
     return TNR_OK;
@@ -724,25 +874,10 @@ int tnr_skin_finish(const tnr_request* req, const tnr_skin_list* list, const int
     if ((unsigned long long)host_result[tnr::SK_FLAGS] & tnr::ST_SCAN_STALL)
         return tnr::put_error(err, err_len, TNR_SEARCH_ERROR,
                               "a device-wide scan of the neighbor search did not complete");
-    const bool ok = tnr::skin_valid(req->dtype, req->cutoff, list->build_cutoff, host_result);
+    const bool ok = host_result[tnr::SK_STORE] == 0 &&
+                    tnr::skin_valid(req->dtype, req->cutoff, list->build_cutoff, host_result);
     *rebuild = ok ? 0 : 1;
     *n_pairs = ok ? host_result[tnr::SK_PAIRS] : 0;
-    return TNR_OK;
-}
-
-int tnr_skin_emit(const tnr_request* req, const tnr_skin_list* list, void* workspace,
-                  size_t workspace_bytes, const tnr_outputs* out, void* stream, char* err,
-                  size_t err_len) {
-    tnr::SkinLayout L;
-    const int rc = tnr::check_skin(req, list, workspace_bytes, workspace, err, err_len, &L);
-    if (rc != TNR_OK) return rc;
-    if (!out) return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "outputs are null");
-    if (out->n_pairs <= 0 || list->n_pairs == 0) return TNR_OK;
-    hipStream_t s = (hipStream_t)stream;
-    const hipError_t e = req->dtype == TNR_FLOAT32
-                             ? tnr::run_skin_emit<float>(req, list, workspace, L, out, s)
-                             : tnr::run_skin_emit<double>(req, list, workspace, L, out, s);
-    if (e != hipSuccess) return tnr::put_error(err, err_len, TNR_DEVICE_ERROR, hipGetErrorString(e));
     return TNR_OK;
 }
 

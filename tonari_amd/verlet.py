@@ -2,15 +2,17 @@
 
 The reference lists a Verlet skin as unsupported (``docs/design.md:125-127``);
 every step of an MD loop then pays a full search.  ``VerletList`` searches
-once at ``cutoff + skin`` (the public call, P and S), keeps that call's
-positions, cell, pbc and batch_ptr, and at later steps filters the stored
-pairs with the reference's public predicate at the current positions
-(``tnr_skin_count_async`` / ``tnr_skin_emit``).  The filter's counting pass
-also measures the largest displacement since the build and compares cell,
-pbc and batch_ptr with the build's; ``tnr_skin_finish`` accepts the filtered
-list only when it provably equals a fresh search at ``cutoff`` (every atom
-moved less than about skin / 2, less a rounding margin, and nothing else
-changed).  Otherwise the list is rebuilt at the current positions.
+once at ``cutoff + skin`` (the public call, P and S) and stores that list,
+8 bytes per pair, with the call's positions, cell, pbc and batch_ptr
+(``tnr_skin_store``).  At later steps one pass over the stored pairs
+re-decides each with the reference's public predicate at the current
+positions and writes the kept ones (``tnr_skin_filter_async``); the same
+pass measures the largest displacement since the build and compares cell,
+pbc and batch_ptr with the build's, and ``tnr_skin_finish`` accepts the
+filtered list only when it provably equals a fresh search at ``cutoff``
+(every atom moved less than about skin / 2, less a rounding margin, and
+nothing else changed).  Otherwise the list is rebuilt at the current
+positions.
 
 Either way a call returns what ``neighbor_list`` returns for the same
 arguments: the same (i, j, S) pairs with the same d and D.  The pairs come in
@@ -56,25 +58,11 @@ __all__ = ["VerletList"]
 
 
 class _Stored:
-    """The list of one build: its pairs, shifts and inputs, and the filter's buffers."""
+    """One stored list: its key, the skin workspace that holds it, its ABI record."""
 
-    def __init__(self, key, pairs: Tensor, shifts: Tensor, positions: Tensor, cell: Tensor,
-                 pbc: Tensor, batch_ptr: Tensor, build_cutoff: float):
+    def __init__(self, key, workspace: Tensor, ws_bytes: int, lst: SkinList):
         self.key = key
-        self.pairs, self.shifts = pairs, shifts
-        self.positions, self.cell, self.pbc, self.batch_ptr = positions, cell, pbc, batch_ptr
-        self.list = SkinList(
-            n_pairs=pairs.shape[0],
-            pairs=pairs.data_ptr() if pairs.numel() else None,
-            shifts=shifts.data_ptr() if shifts.numel() else None,
-            ref_positions=positions.data_ptr() if positions.numel() else None,
-            ref_cell=cell.data_ptr(),
-            ref_pbc=pbc.data_ptr(),
-            ref_batch_ptr=batch_ptr.data_ptr(),
-            build_cutoff=build_cutoff,
-        )
-        self.ws_bytes = 0
-        self.workspace: Tensor | None = None
+        self.workspace, self.ws_bytes, self.list = workspace, ws_bytes, lst
 
 
 class VerletList:
@@ -165,13 +153,22 @@ class VerletList:
             include_self=self.include_self, algorithm=self.algorithm, sorted=self.sorted,
         )
         pairs, shifts = pairs.contiguous(), shifts.contiguous()
-        stored = _Stored(key, pairs, shifts, pos.clone(), cell.clone(), pbc.clone(),
-                         batch_ptr.clone(), build_cutoff)
         req = self._request(pos, cell, pbc, batch_ptr)
-        ws_bytes = int(lib.tnr_skin_workspace_size(ctypes.byref(req), ctypes.byref(stored.list)))
-        stored.ws_bytes = ws_bytes
-        stored.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=pos.device)
-        self._stored = stored
+        n = pairs.shape[0]
+        ws_bytes = int(lib.tnr_skin_workspace_size(ctypes.byref(req), n))
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=pos.device)
+        lst = SkinList()
+        stream = torch.cuda.current_stream(pos.device).cuda_stream
+        code = lib.tnr_skin_store(
+            ctypes.byref(req), build_cutoff, pairs.data_ptr() if n else None,
+            shifts.data_ptr() if n else None, n, workspace.data_ptr(), ws_bytes,
+            ctypes.byref(lst), stream, self._err, len(self._err),
+        )
+        if code != TNR_OK:
+            _raise(code, self._err.value.decode())
+        # the store runs on the stream: P and S may be released once it is
+        # enqueued (later work on the stream reuses their memory after it)
+        self._stored = _Stored(key, workspace, ws_bytes, lst)
         self._capacity = None
         self.builds += 1
 
@@ -198,7 +195,7 @@ class VerletList:
             self._host = (host, torch.cuda.Event())
         return self._host
 
-    def _emit(self, lib, req: Request, out: dict, rows: int, stream: int) -> None:
+    def _run(self, lib, req: Request, out: dict, rows: int, stream: int, host) -> None:
         s = self._stored
         ptrs = Outputs(
             n_pairs=rows, plan=0, n_tasks=0,
@@ -210,22 +207,33 @@ class VerletList:
             targets=out["j"].data_ptr() if "j" in out else None,
             edge_index=None,
         )
-        code = lib.tnr_skin_emit(ctypes.byref(req), ctypes.byref(s.list), s.workspace.data_ptr(),
-                                 s.ws_bytes, ctypes.byref(ptrs), stream, self._err,
-                                 len(self._err))
+        code = lib.tnr_skin_filter_async(
+            ctypes.byref(req), ctypes.byref(s.list), s.workspace.data_ptr(), s.ws_bytes,
+            ctypes.byref(ptrs), host.data_ptr(), stream, self._err, len(self._err),
+        )
         if code != TNR_OK:
             _raise(code, self._err.value.decode())
+
+    def _finish(self, lib, req: Request, host) -> int | None:
+        n_pairs = ctypes.c_int64(0)
+        rebuild = ctypes.c_int32(0)
+        code = lib.tnr_skin_finish(ctypes.byref(req), ctypes.byref(self._stored.list),
+                                   host.data_ptr(), ctypes.byref(n_pairs), ctypes.byref(rebuild),
+                                   self._err, len(self._err))
+        if code != TNR_OK:
+            _raise(code, self._err.value.decode())
+        return None if rebuild.value else int(n_pairs.value)
 
     def _filter(self, lib, pos: Tensor, cell: Tensor, pbc: Tensor, batch_ptr: Tensor,
                 grad_positions: Tensor, grad_cell: Tensor) -> tuple[Tensor, ...] | None:
         """The filtered list, or None when it may differ from a fresh search.
 
-        The writing pass goes out right behind the count, into outputs sized
-        from the previous step's count plus a margin; the host then waits for
-        the count only, and writes again with exact sizes when E outgrew them.
+        One pass writes the kept pairs into outputs sized from the previous
+        step's count plus a margin (at most the stored count, which always
+        suffices); the host waits for the status words only, and filters
+        again into outputs of the stored count when E outgrew them.
         """
-        s = self._stored
-        err = self._err
+        stored = self._stored.list.n_pairs
         need_grad = (
             any(q in self.quantities for q in "dD")
             and torch.is_grad_enabled()
@@ -238,31 +246,23 @@ class VerletList:
         torch_stream = torch.cuda.current_stream(pos.device)
         stream = torch_stream.cuda_stream
         host, arrived = self._host_buffer()
-        code = lib.tnr_skin_count_async(ctypes.byref(req), ctypes.byref(s.list),
-                                        s.workspace.data_ptr(), s.ws_bytes, host.data_ptr(),
-                                        stream, err, len(err))
-        if code != TNR_OK:
-            _raise(code, err.value.decode())
+        rows = stored if self._capacity is None else min(stored, self._capacity)
+        out = _allocate(want, rows, pos.dtype, pos.device)
+        self._run(lib, req, out, rows, stream, host)
         arrived.record(torch_stream)
-        capacity = self._capacity
-        out: dict[str, Tensor] = {}
-        if capacity is not None:
-            out = _allocate(want, capacity, pos.dtype, pos.device)
-            self._emit(lib, req, out, capacity, stream)
         arrived.synchronize()
-        n_pairs = ctypes.c_int64(0)
-        rebuild = ctypes.c_int32(0)
-        code = lib.tnr_skin_finish(ctypes.byref(req), ctypes.byref(s.list), host.data_ptr(),
-                                   ctypes.byref(n_pairs), ctypes.byref(rebuild), err, len(err))
-        if code != TNR_OK:
-            _raise(code, err.value.decode())
-        if rebuild.value:
+        count = self._finish(lib, req, host)
+        if count is None:
             return None
-        count = int(n_pairs.value)
-        if capacity is None or count > capacity:
-            out = _allocate(want, count, pos.dtype, pos.device)
-            if count > 0:
-                self._emit(lib, req, out, count, stream)
+        if count > rows:
+            rows = stored
+            out = _allocate(want, rows, pos.dtype, pos.device)
+            self._run(lib, req, out, rows, stream, host)
+            arrived.record(torch_stream)
+            arrived.synchronize()
+            count = self._finish(lib, req, host)
+            if count is None:
+                return None
         out = _rows(out, count)
         self._capacity = _capacity(count)
         if need_grad:
