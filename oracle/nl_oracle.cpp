@@ -21,10 +21,15 @@
 //   input checks                               csrc/core/neighbors_cpu.cpp:976-1030
 //   worker pool semantics                      csrc/core/thread_pool.cpp:22-191
 //
-// Pinned by: the reference test suite's known-answer tests restated in
-// tests/test_oracle_kat.py, closed forms and invariants in
-// tests/test_oracle_invariants.py, and key hashes of the compiled reference
-// core (oracle/_ref) in tests/golden/.
+// Pinned by (all in tests/test_oracle.py): the reference test suite's
+// known-answer tests restated as test_kat_*, the error contract
+// (test_error_contract), an independent numpy enumeration
+// (test_port_matches_numpy_enumeration, test_batched_structures_match_numpy),
+// closed forms and invariants (test_half_and_self_algebra,
+// test_cell_list_equals_brute_force, test_thread_count_invariance,
+// test_quantities_closed_form), golden key hashes written by the compiled
+// reference core (test_port_matches_golden*, tests/golden/) and that core
+// itself when it builds here (test_port_matches_reference_core, oracle/_ref).
 
 #include <algorithm>
 #include <atomic>
