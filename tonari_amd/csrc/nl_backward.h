@@ -9,8 +9,15 @@
 //
 // One thread per pair, each wave a contiguous range of pairs.  The pairs of
 // a source are contiguous, so the source side is reduced per run of equal
-// sources inside a wave (segmented scan) and added once per run; the target
-// side takes one atomic add per component.  The pairs of a structure are
+// sources inside a wave (segmented scan) and added once per run.  The target
+// side is accumulated in an LDS hash table of the workgroup (open
+// addressing, keyed by target atom, LDS atomics) and added to grad_pos once
+// per distinct target at the end: the targets of a workgroup's consecutive
+// pairs are few when the list comes in bin order (a few hundred stencil
+// atoms for 8,192 pairs), where one global atomic per pair and component
+// serialised (27 M on a 100,000-atom list: 1.25 ms of a 1.39 ms kernel).
+// A target that finds no slot within kBwdProbes probes takes the global
+// atomics directly.  The pairs of a structure are
 // contiguous too (sources come in index or bin order, both grouped by
 // structure), so each wave keeps a running sum of the cell gradient of its
 // current structure, adds it when the structure changes, and the waves of
@@ -36,6 +43,10 @@ __device__ __forceinline__ V segment_inclusive_sum(V x, int seg0) {
     return x;
 }
 
+constexpr int kBwdSlots = 2048;  // LDS hash slots per workgroup (power of two)
+constexpr int kBwdProbes = 8;
+constexpr int kBwdPairsPerBlock = 8192;  // the launcher's grid: at most this many pairs per workgroup
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_geometry_backward(
     int64_t n_pairs, int64_t nb, const int64_t* bp, const int64_t* pairs, const int32_t* shifts,
@@ -43,6 +54,13 @@ __global__ __launch_bounds__(kBlock) void k_geometry_backward(
     T* grad_cell) {
     __shared__ T s_acc[kWavesPerBlock][9];
     __shared__ int s_b[kWavesPerBlock];
+    __shared__ int s_key[kBwdSlots];
+    __shared__ T s_val[3][kBwdSlots];
+    for (int i = threadIdx.x; i < kBwdSlots; i += kBlock) {
+        s_key[i] = -1;
+        s_val[0][i] = s_val[1][i] = s_val[2][i] = T(0);
+    }
+    __syncthreads();
     const int lane = lane_id();
     const int wv = uniform(threadIdx.x / kWave);
     // a contiguous range of pairs per wave
@@ -100,10 +118,26 @@ __global__ __launch_bounds__(kBlock) void k_geometry_backward(
             }
             b = (int)lo;
         }
-        // target side
+        // target side: the workgroup's hash table, else global atomics
         if (valid) {
+            const int key = (int)t;
+            unsigned h = ((unsigned)key * 2654435761u) >> (32 - 11);
+            static_assert(kBwdSlots == 1 << 11, "hash width");
+            bool placed = false;
+            for (int p = 0; p < kBwdProbes; ++p) {
+                const int old = atomicCAS(&s_key[h], -1, key);
+                if (old == -1 || old == key) {
 #pragma unroll
-            for (int c = 0; c < 3; ++c) unsafeAtomicAdd(grad_pos + 3 * t + c, g[c]);
+                    for (int c = 0; c < 3; ++c) atomicAdd(&s_val[c][h], g[c]);
+                    placed = true;
+                    break;
+                }
+                h = (h + 1) & (kBwdSlots - 1);
+            }
+            if (!placed) {
+#pragma unroll
+                for (int c = 0; c < 3; ++c) unsafeAtomicAdd(grad_pos + 3 * t + c, g[c]);
+            }
         }
         const unsigned long long le = lane == kWave - 1 ? ~0ull : ((2ull << lane) - 1ull);
         // source side: runs of equal sources
@@ -166,6 +200,13 @@ __global__ __launch_bounds__(kBlock) void k_geometry_backward(
     }
     if (lane == 0) s_b[wv] = cur_b;
     __syncthreads();
+    // the table's targets, once each
+    for (int i = threadIdx.x; i < kBwdSlots; i += kBlock) {
+        const int key = s_key[i];
+        if (key < 0) continue;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) unsafeAtomicAdd(grad_pos + 3 * (int64_t)key + c, s_val[c][i]);
+    }
     if (threadIdx.x < 9) {
         const int k = threadIdx.x;
         for (int w = 0; w < kWavesPerBlock; ++w) {

@@ -898,9 +898,12 @@ int tnr_geometry_backward(int32_t dtype, int64_t n_pairs, int64_t n_atoms, int64
                               "the gradient of d needs the distances and vectors");
     if (!grad_vectors && !grad_distances) return TNR_OK;
     hipStream_t s = (hipStream_t)stream;
-    // about 32 rounds of 64 pairs per wave, at most 1024 workgroups
-    const int64_t want = (n_pairs + tnr::kBlock * 32 - 1) / (tnr::kBlock * 32);
-    const unsigned blocks = (unsigned)(want < 1024 ? want : 1024);
+    // at most kBwdPairsPerBlock pairs per workgroup (32 rounds of 64 per
+    // wave): the targets of that many consecutive pairs fit its hash table
+    const int64_t blocks_wanted = (n_pairs + tnr::kBwdPairsPerBlock - 1) / tnr::kBwdPairsPerBlock;
+    if (blocks_wanted > 0x7fffffff)
+        return tnr::put_error(err, err_len, TNR_INPUT_ERROR, "invalid sizes");
+    const unsigned blocks = (unsigned)blocks_wanted;
     if (dtype == TNR_FLOAT32)
         tnr::k_geometry_backward<float><<<blocks, tnr::kBlock, 0, s>>>(
             n_pairs, n_structures, batch_ptr, pairs, shifts, (const float*)vectors,
