@@ -88,15 +88,23 @@ def test_batched_validation():
         neighbor_list("PS", pos, cell.numpy(), pbc, 1.0, bp)
 
 
-def test_cpu_tensors_fail_loudly():
-    # No CPU fallback: the neighbor search runs only on the HIP device.
+def test_cpu_tensors_and_numpy_arrays_take_the_host_provider():
+    # CPU tensors and NumPy arrays go to libtonari_cpu.so (tests/test_cpu_provider.py)
+    P, S = neighbor_list("PS", np.zeros((2, 3)), np.eye(3), np.array([1, 0, 0], bool), 1.0)
+    assert isinstance(P, np.ndarray) and P.shape == (2, 2)
+    P, S = neighbor_list("PS", *_args())
+    assert isinstance(P, torch.Tensor) and P.device.type == "cpu"
+
+
+def test_missing_cpu_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(ext, "load_cpu", lambda: ext.open_cpu_library(str(tmp_path / "x.so")))
+    import tonari_amd._cpu_provider as provider
+
+    monkeypatch.setattr(provider, "load_cpu", ext.load_cpu)
+    with pytest.raises(RuntimeError, match="NumPy CPU extension is not built"):
+        neighbor_list("PS", np.zeros((2, 3)), np.eye(3), np.array([1, 0, 0], bool), 1.0)
     with pytest.raises(RuntimeError, match="Torch CPU provider is unavailable"):
         neighbor_list("PS", *_args())
-
-
-def test_numpy_inputs_fail_loudly():
-    with pytest.raises(RuntimeError, match="NumPy CPU provider is unavailable"):
-        neighbor_list("PS", np.zeros((2, 3)), np.eye(3), np.array([1, 0, 0], bool), 1.0)
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

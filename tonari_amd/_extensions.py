@@ -162,6 +162,47 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     return lib
 
 
+CPU_LIBRARY = os.path.join(HERE, "_lib", "libtonari_cpu.so")
+CPU_ABI_VERSION = 1
+CPU_EXPORTS = ("tnr_cpu_abi_version", "tnr_cpu_search", "tnr_cpu_copy", "tnr_cpu_free")
+
+
+def open_cpu_library(path: str = CPU_LIBRARY) -> ctypes.CDLL:
+    """Open the host provider (include/tonari_cpu.h) and declare its signatures."""
+    if not os.path.exists(path):
+        raise ImportError(
+            f"the CPU provider was not built ({path} is missing); "
+            "run `python -m tonari_amd.build`"
+        )
+    lib = ctypes.CDLL(path)
+    lib.tnr_cpu_abi_version.restype = ctypes.c_int
+    lib.tnr_cpu_abi_version.argtypes = []
+    lib.tnr_cpu_search.restype = ctypes.c_int
+    lib.tnr_cpu_search.argtypes = [
+        ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double, ctypes.c_int32, ctypes.c_int32,
+        ctypes.c_int32, ctypes.c_int64, ctypes.POINTER(ctypes.c_void_p),
+        ctypes.POINTER(ctypes.c_int64), ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_cpu_copy.restype = None
+    lib.tnr_cpu_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+    lib.tnr_cpu_free.restype = None
+    lib.tnr_cpu_free.argtypes = [ctypes.c_void_p]
+    version = lib.tnr_cpu_abi_version()
+    if version != CPU_ABI_VERSION:
+        raise ImportError(
+            f"libtonari_cpu.so has ABI version {version}, expected {CPU_ABI_VERSION}; rebuild it"
+        )
+    return lib
+
+
+@lru_cache
+def load_cpu() -> ctypes.CDLL:
+    """The host provider, loaded once (replaces the reference's load_numpy_cpu /
+    load_torch_cpu, src/tonari/_extensions.py:51-59)."""
+    return open_cpu_library()
+
+
 def hip_major_minor(version: str) -> tuple[int, int]:
     """(major, minor) of a HIP version string such as torch.version.hip ("7.0.51831")."""
     parts = version.split(".")

@@ -11,6 +11,9 @@ When ``d`` or ``D`` is requested and ``positions`` or ``cell`` requires
 gradients, the kernel's d/D carry autograd to both through a fused backward
 kernel (``_FusedGeometry``), the gradient of the reference's Torch
 expression.
+
+CPU tensors go to this build's host provider (``_cpu_provider``), and i/j/d/D
+are assembled from its P and S as the reference does (``:78-105``).
 """
 
 from __future__ import annotations
@@ -23,6 +26,7 @@ from math import isfinite
 import torch
 from torch import Tensor
 
+from . import _cpu_provider
 from ._extensions import (
     ALGORITHMS,
     HOST_RESULT_SLOTS,
@@ -372,6 +376,52 @@ def neighbor_list_hip(
     return tuple(out[q] for q in quantities)
 
 
+def _select_torch_quantities(quantities: str, positions: Tensor, cell: Tensor,
+                             batch_ptr: Tensor, pairs: Tensor, shifts: Tensor) -> tuple[Tensor, ...]:
+    """i/j/P/S/d/D from the CPU provider's P and S, as the reference assembles them
+    (``_torch_frontend.py:78-105``): D and d by the Torch expression, so they
+    carry autograd to positions and cell."""
+    values: dict[str, Tensor] = {"P": pairs, "S": shifts}
+    if "i" in quantities:
+        values["i"] = pairs[:, 0].contiguous()
+    if "j" in quantities:
+        values["j"] = pairs[:, 1].contiguous()
+    if "D" in quantities or "d" in quantities:
+        values["D"] = _torch_geometry(positions, cell, batch_ptr, pairs, shifts)
+        if "d" in quantities:
+            values["d"] = torch.linalg.vector_norm(values["D"], dim=1)
+    return tuple(values[q] for q in quantities)
+
+
+def _neighbor_list_cpu(quantities: str, positions: Tensor, cell: Tensor, pbc: Tensor,
+                       cutoff: float, batch_ptr: Tensor, *, algorithm: str,
+                       cpu_threads: int | None, half_list: bool,
+                       include_self: bool) -> tuple[Tensor, ...]:
+    """CPU tensors: the host provider (``_cpu_provider``) on ``cpu_threads``
+    threads (1 by default), replacing the reference's ``_torch_cpu`` module
+    (``_torch_frontend.py:147-156``).  Sources come in index order."""
+    pos = positions.detach().contiguous()
+    cel = cell.detach().contiguous()
+    bp = batch_ptr.contiguous()
+    flags = pbc.contiguous()  # bool: one byte per entry, 0 or 1
+
+    def allocate(n_pairs: int):
+        pairs = torch.empty((n_pairs, 2), dtype=torch.int64)
+        shifts = torch.empty((n_pairs, 3), dtype=torch.int32)
+        return pairs, shifts, pairs.data_ptr(), shifts.data_ptr()
+
+    try:
+        pairs, shifts = _cpu_provider.search(
+            pos.dtype == torch.float64, pos.data_ptr() if pos.numel() else None, pos.shape[0],
+            bp.data_ptr(), bp.numel() - 1, cel.data_ptr() if cel.numel() else None,
+            flags.data_ptr() if flags.numel() else None, cutoff, half_list, include_self,
+            algorithm, 1 if cpu_threads is None else cpu_threads, allocate,
+        )
+    except ImportError as error:
+        raise RuntimeError(f"the Torch CPU provider is unavailable: {error}") from error
+    return _select_torch_quantities(quantities, positions, cell, batch_ptr, pairs, shifts)
+
+
 def neighbor_list_torch(
     quantities: str,
     positions: Tensor,
@@ -391,9 +441,9 @@ def neighbor_list_torch(
     cutoff = float(cutoff)
     validate_torch_inputs(positions, cell, pbc, cutoff, batch_ptr)
     if not positions.is_cuda:
-        raise RuntimeError(
-            "the Torch CPU provider is unavailable: tonari_amd runs the neighbor search "
-            "on ROCm (HIP) devices; move the tensors to a GPU"
+        return _neighbor_list_cpu(
+            quantities, positions, cell, pbc, cutoff, batch_ptr, algorithm=algorithm,
+            cpu_threads=cpu_threads, half_list=half_list, include_self=include_self,
         )
     if cpu_threads is not None:
         raise ValueError("cpu_threads only applies to CPU inputs")

@@ -2,8 +2,8 @@
 
 Same signature, defaults, scalar validation and messages as the reference
 (``src/tonari/api.py:18-234``).  PyTorch tensors on a ROCm (HIP) device go to
-the MI355X provider; other ecosystems raise ``RuntimeError`` because their CPU
-providers are not part of this build.
+the MI355X provider; PyTorch CPU tensors and NumPy arrays go to this build's
+host provider (``include/tonari_cpu.h``) on ``cpu_threads`` threads.
 """
 
 from __future__ import annotations
@@ -46,9 +46,10 @@ def neighbor_list(
     lexicographically smaller of (i, j, S) and (j, i, -S); ``include_self``
     adds the zero-shift self pair of every atom.  The pairs of a source are
     always contiguous.  With ``sorted=True`` sources come in increasing index
-    order.  Without it, sources come in cell-list bin order when every
-    structure of the call is searched with a cell list, and in index order
-    otherwise; the order of targets within a source is unspecified.
+    order.  Without it, on the device, sources come in cell-list bin order
+    when every structure of the call is searched with a cell list, and in
+    index order otherwise; on the CPU they always come in index order.  The
+    order of targets within a source is unspecified.
     """
     if not isinstance(quantities, str):
         raise TypeError("quantities must be a string")
@@ -74,9 +75,20 @@ def neighbor_list(
     except ImportError:  # pragma: no cover - numpy ships with torch
         np = None
     if np is not None and isinstance(positions, np.ndarray):
-        raise RuntimeError(
-            "the NumPy CPU provider is unavailable: tonari_amd runs the neighbor search on "
-            "ROCm (HIP) devices; pass PyTorch tensors on a GPU"
+        from ._numpy_frontend import neighbor_list_numpy
+
+        return neighbor_list_numpy(
+            quantities,
+            positions,
+            cell,
+            pbc,
+            cutoff,
+            batch_ptr,
+            algorithm=algorithm,
+            cpu_threads=cpu_threads,
+            sorted=sorted,
+            half_list=half_list,
+            include_self=include_self,
         )
     try:
         import torch

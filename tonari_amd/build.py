@@ -1,4 +1,5 @@
-"""Compile libtonari_hip.so for gfx950 with hipcc (in-tree, no JIT cache).
+"""Compile libtonari_hip.so for gfx950 with hipcc and the host provider
+libtonari_cpu.so with g++ (in-tree, no JIT cache).
 
 Flags that matter for parity and safety:
   -ffp-contract=off                      no implicit FMA contraction; the
@@ -20,6 +21,8 @@ ROOT = os.path.dirname(HERE)
 SOURCES = [os.path.join(HERE, "csrc", "tonari_hip.hip")]
 HEADERS = [os.path.join(HERE, "csrc", "nl_device.h"), os.path.join(ROOT, "include", "tonari_hip.h")]
 OUTPUT = os.path.join(HERE, "_lib", "libtonari_hip.so")
+CPU_SOURCES = [os.path.join(HERE, "csrc", "cpu", "nl_cpu.cpp")]
+CPU_OUTPUT = os.path.join(HERE, "_lib", "libtonari_cpu.so")
 ARCH = "gfx950"
 
 
@@ -49,19 +52,45 @@ def command(output: str = OUTPUT, extra: list[str] | None = None) -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(os.path.dirname(OUTPUT), exist_ok=True)
-    tmp = OUTPUT + ".tmp"
-    cmd = command(tmp)
+def cpu_command(output: str = CPU_OUTPUT) -> list[str]:
+    """The host provider: plain C++17 with threads; -ffp-contract=off keeps
+    every operation of the predicate rounded on its own (x86-64 arithmetic
+    is SSE, no extended precision)."""
+    cxx = shutil.which("g++") or "g++"
+    return [
+        cxx, "-O3", "-std=c++17", "-fPIC", "-shared", "-pthread", "-ffp-contract=off",
+        "-fno-fast-math", "-Wall", "-Wextra",
+        "-I", os.path.join(ROOT, "include"),
+        *CPU_SOURCES,
+        "-o", output,
+    ]
+
+
+def _run(cmd: list[str], output: str, verbose: bool, what: str) -> None:
+    tmp = output + ".tmp"
+    cmd = [tmp if c == output else c for c in cmd]
     if verbose:
         print(" ".join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         sys.stderr.write(result.stdout + result.stderr)
-        raise RuntimeError("hipcc failed to build libtonari_hip.so")
-    os.replace(tmp, OUTPUT)
+        raise RuntimeError(f"failed to build {what}")
+    os.replace(tmp, output)
+
+
+def build_cpu(verbose: bool = False) -> str:
+    os.makedirs(os.path.dirname(CPU_OUTPUT), exist_ok=True)
+    _run(cpu_command(), CPU_OUTPUT, verbose, "libtonari_cpu.so")
+    return CPU_OUTPUT
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(os.path.dirname(OUTPUT), exist_ok=True)
+    _run(command(OUTPUT), OUTPUT, verbose, "libtonari_hip.so")
+    build_cpu(verbose)
     return OUTPUT
 
 
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(CPU_OUTPUT)
