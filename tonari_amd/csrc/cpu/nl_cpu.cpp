@@ -46,7 +46,7 @@ constexpr int kAuto = 0, kBruteForce = 1, kCellList = 2;
 constexpr int64_t kImageCap = int64_t{1} << 24;        // geometry.cpp:12
 constexpr double kLayoutCap = 67108864.0;              // neighbors_cpu.cpp:379-430
 constexpr int64_t kAutoCandidates = 4096;              // this provider's brute/cell crossover
-constexpr int64_t kSourcesPerTask = 256;
+constexpr int64_t kSourcesPerTask = 256;  // at most; fewer when that leaves threads idle
 
 // Error bits, decoded in the reference's priority order (kMessages).
 enum Err : uint32_t {
@@ -764,12 +764,15 @@ int search(const T* pos, int64_t n_atoms, const int64_t* bp, int64_t nb, const T
         first_flag_message(flags, &code, &text);
         return put_error(err, err_len, code, text);
     }
-    // tasks: runs of sources, in structure and source order
+    // tasks: runs of sources, in structure and source order; about eight
+    // per thread, of 16 to kSourcesPerTask sources
+    const int64_t per_task =
+        std::max<int64_t>(16, std::min<int64_t>(kSourcesPerTask, n_atoms / (8 * threads)));
     std::vector<Task> tasks;
     for (int64_t b = 0; b < nb; ++b) {
         const Structure& r = st[(size_t)b];
-        for (int64_t s = 0; s < r.n; s += kSourcesPerTask)
-            tasks.push_back({b, r.atom0 + s, r.atom0 + std::min(r.n, s + kSourcesPerTask)});
+        for (int64_t s = 0; s < r.n; s += per_task)
+            tasks.push_back({b, r.atom0 + s, r.atom0 + std::min(r.n, s + per_task)});
     }
     res->parts.assign(tasks.size(), Pairs());
     const T cut2 = (T)(cutoff * cutoff);
