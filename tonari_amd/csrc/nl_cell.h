@@ -1,25 +1,16 @@
-// Cell-list query kernels: the stencil walk over the bins of a structure in
-// a counting flavour (k_cell_count: pairs per source and hit masks, in a
-// persistent grid) and an
-// emitting flavour (k_cell_emit: writes i/j/P/S/d/D at the scanned offsets).
+// Cell-list query: the stencil of a bin, its pieces and exact decisions,
+// shared by the counting pass (k_cell_count, nl_count.h), and the emitting
+// pass (k_cell_emit: writes i/j/P/S/d/D at the scanned offsets).
 //
-// Work unit: one source bin per workgroup.  The four waves build the bin's
-// stencil once in LDS: the neighbouring bins with their periodic images,
-// cut into pieces (runs of consecutive z-bins of one (x, y) row with one
-// image k), flattened into candidates.  When the stencil holds at most
-// StageCap<T> candidates, their records (wrapped position and atom index) are
-// staged in LDS as well, so the distance tests and the pair writes read
-// candidates from LDS only; larger stencils read them from the binned array.
-// The waves then split the bin's sources.
-//
-//   counting: up to CH chunks of 64 candidates at a time are gathered into
-//             registers as image positions plus a 32-bit identity key, and
-//             the wave's sources are broadcast one at a time against them;
-//             one 64-bit hit mask per (source, chunk) is stored.
-//   emitting: no distance tests; the hit masks are decoded into an LDS list
-//             of (source, candidate) entries that are written 64 pairs per
-//             round, every lane busy and consecutive lanes writing
-//             consecutive pairs.
+// A bin's stencil is the neighbouring bins with their periodic images, cut
+// into pieces (runs of consecutive z-bins of one (x, y) row with one image
+// k) and flattened into candidates.  The emitting pass takes one source bin
+// per workgroup: the four waves build the stencil once in LDS and, when it
+// holds at most EmitStageCap<T> candidates, stage their records (wrapped
+// position and atom index) in LDS too.  It runs no distance tests: the hit
+// masks of the counting pass are decoded into an LDS list of (source,
+// candidate) entries that are written 64 pairs per round, every lane busy
+// and consecutive lanes writing consecutive pairs.
 //
 // Stencils with more than kMapCap candidates take a slow path that decides
 // every candidate in both passes.
@@ -29,7 +20,7 @@
 // 515-584; both apply the public predicate of neighbors_cpu.cpp:247-261.
 // Here a fused broad-phase distance classifies a candidate as inside
 // (d2 < inner2), outside (d2 >= outer2) or in the thin band between, which
-// the public predicate decides (cell_decide).
+// the public predicate decides (cell_decide, cell_band).
 #pragma once
 
 #include "nl_query.h"
@@ -38,32 +29,6 @@ namespace tnr {
 
 constexpr int kMapCap = kMaskWords * kWave;  // candidates whose piece is mapped in LDS
 constexpr int kListCap = 512;                // emit: compacted hits per flush
-
-// Chunks of 64 candidates held in registers per pass (at most).
-template <typename T>
-struct RegChunks;
-template <>
-struct RegChunks<float> {
-    // six chunks keep the float count within 80 VGPRs, six waves per SIMD
-    // (its LDS allows six workgroups per CU); twelve needed 128 VGPRs
-    static constexpr int value = 6;
-};
-template <>
-struct RegChunks<double> {
-    static constexpr int value = 4;
-};
-
-// Candidates of a stencil staged in LDS (at most); a multiple of kBlock.
-template <typename T>
-struct StageCap;
-template <>
-struct StageCap<float> {
-    static constexpr int value = 1024;
-};
-template <>
-struct StageCap<double> {
-    static constexpr int value = 768;
-};
 
 // Stencil of the workgroup's current bin in LDS.
 struct StencilLds {
@@ -233,15 +198,13 @@ __device__ __forceinline__ bool stencil_piece_rows(const BinGeom& G, int p, int&
 
 // Builds the stencil of global bin g with the whole workgroup (every thread
 // calls it; it holds workgroup barriers), one thread per piece
-// (stencil_piece_rows).  Fills the piece tables of st (and, when tr is given, the
-// broad-phase translation of every piece) and, when C <= kMapCap, the piece
+// (stencil_piece_rows).  Fills the piece tables of st and, when C <= kMapCap, the piece
 // of every candidate in st.piece (a workgroup running maximum of the marks
 // left at every piece start).  Returns false, before any barrier, when the
 // bin holds no source.  The caller separates two calls with a barrier.
 template <typename T>
 __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, StructCache& sc,
                                           CellBin<T>& cb, StencilLds& st,
-                                          T (*tr)[kPieceCap] = nullptr,
                                           Vec4<T>* src_pre = nullptr) {
     const int tid = threadIdx.x;
     const int lane = lane_id();
@@ -306,7 +269,6 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
         st.kfl[p] = (unsigned char)((kx == 0 && ky == 0 && kz == 0 ? 1 : 0) |
                                     (lex_negative(kx, ky, kz) ? 2 : 0));
         if (len > 0 && ex < kMapCap) st.piece[ex] = (unsigned char)p;
-        if (tr) image_translation(kk, cb.c, tr[0][p], tr[1][p], tr[2][p]);
     }
     if (tid == 0) st.pre[npieces] = total;
     cb.C = uniform(total);
@@ -430,8 +392,9 @@ __device__ __forceinline__ void shift_check(const QueryArgs<T>& a, int tid, int 
 // at (sx, sy, sz) with index si: broad phase, identity and band.  Used by the
 // rare paths; its broad phase is the register path's, operation for operation.
 // The candidate's record comes from `cand` (the LDS staging) when given.
-template <typename T, int MODE>
-__device__ __forceinline__ bool cell_decide(const QueryArgs<T>& a, const StencilLds& st,
+// ST: any stencil table with pre, delta and kid (StencilLds, WaveStencil).
+template <typename T, int MODE, typename ST>
+__device__ __forceinline__ bool cell_decide(const QueryArgs<T>& a, const ST& st,
                                             const CellBin<T>& cb, int p, int v, T sx, T sy,
                                             T sz, int si, int* tid_out, int* kk_out,
                                             Vec4<T>* rec_out, const Vec4<T>* cand = nullptr) {
@@ -457,9 +420,10 @@ __device__ __forceinline__ bool cell_decide(const QueryArgs<T>& a, const Stencil
     return ok;
 }
 
-// Candidate v of a stencil too large for the piece map: its piece by binary
+// Piece of candidate v: the last piece whose start is at most v, by binary
 // search over the piece starts.
-__device__ __forceinline__ int stencil_piece(const StencilLds& st, int v, int npieces) {
+template <typename ST>
+__device__ __forceinline__ int stencil_piece(const ST& st, int v, int npieces) {
     int top = 1;
     while (top * 2 <= npieces) top *= 2;
     int p = 0;
@@ -513,8 +477,8 @@ __device__ __forceinline__ void cell_write(const QueryArgs<T>& a, long long o, i
 
 // Stencils with more than kMapCap candidates (coarse grids): one chunk at a
 // time, the piece of each candidate found by binary search.
-template <typename T, int MODE, bool EMIT>
-__device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLds& st,
+template <typename T, int MODE, bool EMIT, typename ST>
+__device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const ST& st,
                                        const CellBin<T>& cb) {
     const int lane = lane_id();
     for (int sg = cb.sb; sg < cb.se; sg += kWave) {
@@ -558,183 +522,6 @@ __device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const StencilLd
             }
         }
         if (!EMIT && lane < ns) a.counts[cb.by_bin ? sg + lane : sidx] = acc;
-    }
-}
-
-// Candidates of one register pass: chunks c0 .. c0 + NC - 1 of the stencil,
-// lane l of chunk j holding candidate (c0 + j) * 64 + l.  Slots past the
-// last candidate hold a far position that fails every test.
-template <typename T, int NC>
-struct Chunks {
-    T x[NC], y[NC], z[NC];  // image positions (broad phase)
-    unsigned key[NC];       // identity keys
-};
-
-template <typename T, int MODE, int NC>
-__device__ __forceinline__ void gather_pass(const QueryArgs<T>& a, const StencilLds& st,
-                                            const Vec4<T>* cand, bool staged,
-                                            const T (*tr)[kPieceCap], const CellBin<T>& cb,
-                                            int c0, Chunks<T, NC>& cd) {
-    using O = Ops<T>;
-    const int lane = lane_id();
-    const T far = T(1e18);
-#pragma unroll
-    for (int j = 0; j < NC; ++j) {
-        cd.x[j] = cd.y[j] = cd.z[j] = far;
-        cd.key[j] = MODE == 0 ? ~0u : 0u;
-        if (c0 + j < cb.nch) {
-            const int v = chunk_cand(c0 + j, lane, cb.nch);
-            if (v < cb.C) {
-                const int p = st.piece[v];
-                const Vec4<T> rec = staged ? cand[v] : a.binned[v + st.delta[p]];
-                const int f = st.kfl[p];
-                if constexpr (MODE >= 2)
-                    cd.key[j] = identity_key<MODE>(as_idx(rec.w), (f & 1) != 0, (f & 2) != 0);
-                cd.x[j] = O::add(rec.x, tr[0][p]);
-                cd.y[j] = O::add(rec.y, tr[1][p]);
-                cd.z[j] = O::add(rec.z, tr[2][p]);
-            }
-        }
-    }
-}
-
-// Full decisions for chunk jc of the stencil against one source: used when
-// the broad phase left a candidate of the chunk in the band.  Rare: the band
-// is about 1e-3 of the cutoff wide.
-template <typename T, int MODE>
-__device__ __forceinline__ unsigned long long band_chunk(const QueryArgs<T>& a,
-                                                         const StencilLds& st,
-                                                         const CellBin<T>& cb, int jc, T sx,
-                                                         T sy, T sz, int si,
-                                                         const Vec4<T>* cand) {
-    const int v = chunk_cand(jc, lane_id(), cb.nch);
-    bool ok = false;
-    if (v < cb.C) {
-        int tid, kk;
-        Vec4<T> rec;
-        ok = cell_decide<T, MODE>(a, st, cb, st.piece[v], v, sx, sy, sz, si, &tid, &kk, &rec,
-                                  cand);
-    }
-    return __builtin_amdgcn_ballot_w64(ok);
-}
-
-// Hit masks of one source (sx, sy, sz, si) against the NC chunks of a pass:
-// lane j of mv receives the mask of chunk c0 + j; returns the hit count.  The
-// fused broad phase gives the inside and band masks of every chunk without
-// branches; the rare chunks with band candidates are then decided in full.
-template <typename T, int MODE, int NC>
-__device__ __forceinline__ int pass_masks(const QueryArgs<T>& a, const StencilLds& st,
-                                          const CellBin<T>& cb, const Chunks<T, NC>& cd, int c0,
-                                          T sx, T sy, T sz, int si, unsigned long long& mv,
-                                          const Vec4<T>* cand) {
-    using O = Ops<T>;
-    const int lane = lane_id();
-    unsigned band = 0;
-    int cnt = 0;
-    int mlo = 0, mhi = 0;  // lane j: the two halves of the mask of chunk c0 + j
-    static_for<NC>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        const T dx = O::sub(cd.x[j], sx), dy = O::sub(cd.y[j], sy), dz = O::sub(cd.z[j], sz);
-        const T d2 = O::fma_(dz, dz, O::fma_(dy, dy, O::mul(dx, dx)));
-        unsigned long long mk = __builtin_amdgcn_ballot_w64(d2 < cb.outer2);
-        // the full list's only identity exclusion, the source itself with
-        // k = 0, is removed once per source afterwards (count_bin)
-        if constexpr (MODE >= 2) mk &= __builtin_amdgcn_ballot_w64(identity_pass<MODE>(cd.key[j], si));
-        const unsigned long long mi = __builtin_amdgcn_ballot_w64(d2 < cb.inner2);
-        const unsigned long long m = mk & mi;
-        band |= (mk & ~mi) ? (1u << j) : 0u;
-        cnt += __popcll(m);
-        mlo = write_lane<j>(mlo, (int)(unsigned)m);
-        mhi = write_lane<j>(mhi, (int)(unsigned)(m >> 32));
-    });
-    mv = ((unsigned long long)(unsigned)mhi << 32) | (unsigned)mlo;
-    if (band) {
-        for (int j = 0; j < NC; ++j) {
-            if (!((band >> j) & 1u)) continue;
-            const unsigned long long full =
-                band_chunk<T, MODE>(a, st, cb, c0 + j, sx, sy, sz, si, cand);
-            const unsigned long long old = (unsigned long long)read_lane((long long)mv, j);
-            cnt += __popcll(full) - __popcll(old);
-            if (lane == j) mv = full;
-        }
-    }
-    return cnt;
-}
-
-// Counting, register path of the wave's sources: source groups of 64,
-// register passes of NC chunks.  Writes counts[s] and, per source, the hit
-// mask of every chunk (masks[binned index][chunk]) for the emitting pass.
-template <typename T, int MODE, int NC>
-__device__ __forceinline__ void count_bin(const QueryArgs<T>& a, const StencilLds& st,
-                                          const Vec4<T>* cand, bool staged,
-                                          const T (*tr)[kPieceCap], const CellBin<T>& cb) {
-    const int lane = lane_id();
-    const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
-    for (int sg = cb.sb; sg < cb.se; sg += kWave) {
-        const int ns = min(kWave, cb.se - sg);
-        Vec4<T> sq = zero4;
-        if (lane < ns) sq = a.binned[sg + lane];
-        const int sidx = as_idx(sq.w);
-        long long acc = 0;  // lane gi: pairs of source gi so far
-        for (int c0 = 0; c0 < cb.nch; c0 += NC) {
-            Chunks<T, NC> cd;
-            gather_pass<T, MODE, NC>(a, st, cand, staged, tr, cb, c0, cd);
-            const bool store = lane < NC && c0 + lane < cb.nch;
-#pragma unroll 1
-            for (int gi = 0; gi < ns; ++gi) {
-                const T sx = read_lane(sq.x, gi), sy = read_lane(sq.y, gi),
-                        sz = read_lane(sq.z, gi);
-                const int si = read_lane(sidx, gi);
-                unsigned long long mv;  // lane j: hit mask of chunk c0 + j
-                int cnt = pass_masks<T, MODE, NC>(a, st, cb, cd, c0, sx, sy, sz, si, mv,
-                                                  staged ? cand : nullptr);
-                if constexpr (MODE == 0) {
-                    // drop the source itself (candidate vs, at distance 0): lane
-                    // vs / nch of chunk vs % nch
-                    const int vs = sg + gi - cb.dself;
-                    const int ls = (int)(((float)vs + 0.5f) / (float)cb.nch);
-                    const int jc = vs - ls * cb.nch - c0;
-                    if (jc >= 0 && jc < NC) {
-                        const unsigned long long mj = (unsigned long long)read_lane((long long)mv, jc);
-                        cnt -= (int)((mj >> ls) & 1ull);
-                        if (lane == jc) mv &= ~(1ull << ls);
-                    }
-                }
-                if (cb.shiftcheck) {
-                    for (int j = 0; j < NC && c0 + j < cb.nch; ++j) {
-                        const unsigned long long m = (unsigned long long)read_lane((long long)mv, j);
-                        if ((m >> lane) & 1ull) {
-                            const int v = chunk_cand(c0 + j, lane, cb.nch);
-                            const int p = st.piece[v];
-                            shift_check(a, as_idx(a.binned[v + st.delta[p]].w), st.kid[p], si);
-                        }
-                    }
-                }
-                if (store) a.masks[(int64_t)(sg + gi) * kMaskWords + c0 + lane] = mv;
-                if (lane == gi) acc += cnt;
-            }
-        }
-        if (lane < ns) a.counts[cb.by_bin ? sg + lane : sidx] = acc;
-    }
-}
-
-// The register path with exactly as many chunks per pass as the bin's
-// stencil holds (passes of RegChunks<T> chunks beyond that).
-template <typename T, int MODE>
-__device__ __forceinline__ void count_bin_any(const QueryArgs<T>& a, const StencilLds& st,
-                                              const Vec4<T>* cand, bool staged,
-                                              const T (*tr)[kPieceCap], const CellBin<T>& cb) {
-    constexpr int CH = RegChunks<T>::value;
-    switch (cb.nch < CH ? cb.nch : CH) {
-#define TNR_COUNT_NC(n) \
-    case n:             \
-        if constexpr (n <= CH) count_bin<T, MODE, n>(a, st, cand, staged, tr, cb); \
-        break;
-        TNR_COUNT_NC(1) TNR_COUNT_NC(2) TNR_COUNT_NC(3) TNR_COUNT_NC(4) TNR_COUNT_NC(5)
-        TNR_COUNT_NC(6) TNR_COUNT_NC(7) TNR_COUNT_NC(8) TNR_COUNT_NC(9) TNR_COUNT_NC(10)
-        TNR_COUNT_NC(11) TNR_COUNT_NC(12)
-#undef TNR_COUNT_NC
-        default: break;
     }
 }
 
@@ -1114,70 +901,7 @@ __device__ __forceinline__ ItemRange xcd_block_range(int64_t W) {
     return r;
 }
 
-// Counting pass, persistent grid: every workgroup walks its share of the
-// bins of the cell-list structures (one bin at a time, stencil built and
-// staged once, sources split over the four waves); writes counts[s] for each
-// source s of a cell-list structure.  The status word is read once: abort
-// bits only come from earlier kernels.
-template <typename T, int MODE>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 ? 6 : 4))) void
-k_cell_count(
-    QueryArgs<T> a) {
-    __shared__ StencilLds s_st;
-    __shared__ T s_tr[3][kPieceCap];
-    __shared__ Vec4<T> s_cand[StageCap<T>::value];
-
-    if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
-    const unsigned long long plan = load_status(a.status + SS_PLAN);
-
-    if (plan & 2) {
-        // Static interleaved split: bins come in chunks of 8 consecutive
-        // bins, chunk c belongs to XCD c % 8 (workgroups with blockIdx % 8 ==
-        // x run on XCD x), and the workgroups of an XCD take its bins round
-        // robin.  Every XCD and workgroup thus sees a mix of the batch's
-        // structures (balanced load) while neighbouring bins share an L2.
-        const int64_t W = a.struct_bin_off[a.nb];
-        const int64_t nxb = (int64_t)(gridDim.x / 8);  // workgroups per XCD (grid is a multiple of 8)
-        const int64_t x = (int64_t)(blockIdx.x & 7u);
-        StructCache sc{0, 0, 0};
-        for (int64_t j = (int64_t)(blockIdx.x >> 3);; j += nxb) {
-            const int64_t g = ((j >> 3) * 8 + x) * 8 + (j & 7);
-            if ((j >> 3) * 64 >= W) break;  // uniform: this XCD has no bins from here on
-            if (g < W) {
-                CellBin<T> cb;
-                if (block_bin<T>(a, g, sc, cb, s_st, s_tr)) {
-                    const bool staged = cb.C <= StageCap<T>::value;
-                    if (staged) stage_candidates<T, StageCap<T>::value>(a, s_st, cb.C, s_cand);
-                    wave_sources(cb);
-                    if (cb.C <= kMapCap)
-                        count_bin_any<T, MODE>(a, s_st, s_cand, staged, s_tr, cb);
-                    else
-                        cell_slow<T, MODE, false>(a, s_st, cb);
-                }
-                __syncthreads();  // the bin's LDS is free
-            }
-        }
-    }
-    if ((plan & 1) && a.brute_in_cell) {
-        // brute-force structures of an explicit cell_list request (no bin
-        // grid fits them): one wave per work unit, atoms read from global
-        // memory, the per-source cursors in the candidate staging area
-        static_assert(sizeof(s_cand) >= kWavesPerBlock * sizeof(BruteCursor),
-                      "brute-force cursors fit the staging area");
-        BruteCursor* cur = reinterpret_cast<BruteCursor*>(s_cand);
-        const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
-        const int wv = uniform(threadIdx.x / kWave);
-        const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-        for (int64_t u = (int64_t)blockIdx.x * kWavesPerBlock + wv; u < units; u += nwaves)
-            brute_unit<T, MODE, false, false>(a, u, nullptr, cur[wv]);
-    }
-}
-
 static_assert(kMapCap == kMaskWords * kWave, "one mask word per chunk of the piece map");
-static_assert(StageCap<float>::value % kBlock == 0 && StageCap<double>::value % kBlock == 0,
-              "staging copies whole workgroup strides");
-static_assert(StageCap<float>::value <= kMapCap && StageCap<double>::value <= kMapCap,
-              "staged stencils have a piece map");
 
 // Emitting pass for one bin whose stencil block_bin has built: the fast
 // path (staged candidates, no wrapped representative, at most 64 sources),
@@ -1255,7 +979,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
         if (g >= br.end) return;
         CellBin<T> cb;
         Vec4<T> src_all;
-        if (block_bin<T>(a, g, sc, cb, s_st, nullptr, &src_all))
+        if (block_bin<T>(a, g, sc, cb, s_st, &src_all))
             emit_one_bin<T, MODE>(a, s_st, s_cand, s_list[wv], cb, src_all, wv, lane);
     } else {
         // a grid of any size strides over the bins (a launch that does not
@@ -1263,7 +987,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
         for (int64_t g = br.first; g < br.end; g += br.step) {
             CellBin<T> cb;
             Vec4<T> src_all;
-            if (block_bin<T>(a, g, sc, cb, s_st, nullptr, &src_all))
+            if (block_bin<T>(a, g, sc, cb, s_st, &src_all))
                 emit_one_bin<T, MODE>(a, s_st, s_cand, s_list[wv], cb, src_all, wv, lane);
             __syncthreads();  // the bin's LDS is free
         }

@@ -35,7 +35,7 @@
 // fused multiply-adds explicitly, the exact predicate uses the _rn
 // intrinsics so that its rounding sequence is the reference's.
 
-#include "nl_cell.h"
+#include "nl_count.h"
 #include "nl_prologue.h"
 #include "nl_query.h"
 #include "nl_scan.h"
