@@ -590,14 +590,31 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
     }
     const double rc = cutoff;
     const double pad = 64.0 * Ops<T>::eps * fmax(scale, rc);
-    const double inner = rc - pad;
+    // Half-width of the band the public predicate decides.  With wrapped
+    // atoms, the padding above.  Without (every wrap zero, so the wrapped
+    // positions are the positions): per component, the broad-phase D of the
+    // cell-list walk (p_t + k.cell, minus p_s) and of the brute-force walk
+    // ((p_t - p_s) + k.cell, fused) differ from the exact value by at most
+    // u (5 |D| + |p| + 4 B) and u (4 |D| + 7 B), the public D by u (4 |D| +
+    // 8 B), with u = eps / 2 and B = max_c sum_a R_a |cell_ac| the largest
+    // image translation; over three components and the d2 roundings (at most
+    // 4 u d together), |d_broad - d_public| <= u (17.9 rc + 1.74 max|p| + 26 B)
+    // near the cutoff, first order.  Twice that bound is the band.
+    double bmax = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+        bmax = fmax(bmax, (double)R0 * fabs(cell[c]) + (double)R1 * fabs(cell[3 + c]) +
+                              (double)R2 * fabs(cell[6 + c]));
+    const double band =
+        maxw_u == 0 ? fmin(pad, Ops<T>::eps * (18.0 * rc + 1.75 * maxp + 26.0 * bmax)) : pad;
+    const double inner = rc - band;
     if (writer) {
         r.pad = pad;
         r.maxp = (unsigned long long)__double_as_longlong(maxp);
         r.maxw = maxw_u;
         r.any_wrap = maxw_u != 0;
         r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
-        r.outer2 = (double)Ops<T>::up((rc + pad) * (rc + pad));
+        r.outer2 = (double)Ops<T>::up((rc + band) * (rc + band));
         r.cut2 = (double)(T)(cutoff * cutoff);
     }
     const bool safe = isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Ops<T>::max;
