@@ -403,8 +403,14 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
         wave_lds_fence();
         const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
         const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-        for (int64_t u = (int64_t)blockIdx.x * kWavesPerBlock + wv; u < units; u += nwaves)
-            brute_unit<T, MODE, false, false>(a, u, nullptr, s_lds[wv].cur);
+        for (int64_t u = (int64_t)blockIdx.x * kWavesPerBlock + wv; u < units; u += nwaves) {
+            const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+            const StructRec& r = a.recs[b];
+            if (molecule_path(r.active, r.natoms))
+                molecule_count<T, MODE>(a, r, u);
+            else
+                brute_unit<T, MODE, false, false>(a, u, b, nullptr, s_lds[wv].cur);
+        }
     }
 }
 

@@ -144,7 +144,19 @@ struct Layout {
 
 // Hit masks stored per cell-list source: one 64-bit word per chunk of 64
 // stencil candidates, for stencils of up to kMaskWords * 64 candidates.
+// Molecules (below) store theirs in the same place: one word per chunk of
+// 64 targets.
 constexpr int kMaskWords = 32;
+
+// Molecules: brute-force structures with no periodic axis and at most
+// kMaskWords * 64 atoms.  They take the hit-mask form of the brute-force
+// passes (molecule_unit): work units of bgroup consecutive sources, with
+// bgroup x (chunks of 64 targets) at most kMolUnitWork, so that the
+// emitting pass's list of one unit's hits fits its LDS.
+constexpr int kMolUnitWork = 28;
+__host__ __device__ inline bool molecule_path(int active, int64_t natoms) {
+    return active == 0 && natoms <= (int64_t)kMaskWords * 64;
+}
 
 constexpr int64_t kScanItems = 8;
 constexpr int64_t kScanChunk = kBlock * kScanItems;

@@ -774,7 +774,13 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
         struct_bins[b] = nbins;
         // brute force: work units of bgroup consecutive sources
         int64_t units = 0;
-        if (algo == ALGO_BRUTE) {
+        if (algo == ALGO_BRUTE && molecule_path(r.active, n)) {
+            // a molecule: sources x chunks of 64 targets per unit
+            const int chunks = (int)((n + kWave - 1) / kWave);
+            const int g = (int)min((int64_t)max(kMolUnitWork / chunks, 1), n);
+            r.bgroup = g;
+            units = (n + g - 1) / g;
+        } else if (algo == ALGO_BRUTE) {
             // a round: 64 (source, target) pairs, costing about 1 + images / 4
             const double round = 1.0 + 0.25 * (double)nimages;
             const double rounds = fmax(floor(kBruteUnitWork / round), 1.0);

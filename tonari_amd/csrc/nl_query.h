@@ -435,8 +435,8 @@ __device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G) {
     return x;
 }
 
-// Work unit u of the brute-force structures: sources [first, first + G) of
-// one structure.  Their (source, target) pairs (targets t >= s for a half
+// Work unit u of the brute-force structures, of structure b: sources
+// [first, first + G).  Their (source, target) pairs (targets t >= s for a half
 // list) are taken 64 per round in source order, lane l taking pair 64 r + l;
 // the atoms of a structure of up to kBruteStage atoms are staged in the
 // wave's LDS first.  Counting adds each lane's pairs to its source's count
@@ -447,9 +447,8 @@ __device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G) {
 // LDS: the form the cell-list counting kernel runs for the structures of an
 // explicit cell_list request that no bin grid fits.
 template <typename T, int MODE, bool EMIT, bool STAGE = true>
-__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, BruteLds<T>* L,
-                                           BruteCursor& C) {
-    const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+__device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int b,
+                                           BruteLds<T>* L, BruteCursor& C) {
     const StructRec& r = a.recs[b];
     BruteGeom<T> g;
     brute_geom(a, r, b, g);
@@ -522,6 +521,151 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, Bru
     wave_lds_fence();
 }
 
+// ---------------------------------------------------------------- molecules
+//
+// Brute-force structures with no periodic axis and at most kMaskWords * 64
+// atoms (molecule_path).  They have one image, k = 0, and no wraps, so the
+// output shift is zero and the public predicate is the whole test: with
+// S = 0 every product S_a * cell_ac of the public formula is a signed zero,
+// and adding a signed zero leaves a nonzero value unchanged (a zero
+// component can only change sign), so d2 = ((dx dx + dy dy) + dz dz) with
+// d = p_t - p_s, rounded after every operation, is the public d2 bit for
+// bit.  The wrapped positions equal the positions (every wrap is zero).
+// The identity policy reduces to t != s (full list) or t > s (half list),
+// and include_self keeps t == s.  A work unit holds bgroup consecutive
+// sources, bgroup x chunks <= kMolUnitWork (chunk c: targets 64 c .. 64 c +
+// 63).
+//   Counting: lane l holds target 64 c + l of each chunk c of a register
+//   pass; each source is read from the lane that holds it, and one ballot
+//   per (source, chunk) gives the hit mask, stored where the cell list
+//   stores its masks (kMaskWords words per atom).
+//   Emitting: the unit's masks are decoded into a list of (source, target)
+//   entries in the wave's LDS, in source and target order, and written 64
+//   pairs per round.  The unit's sources are consecutive atoms, so their
+//   pairs form one contiguous output range from offsets[first source].
+
+constexpr int kMolPass = 8;                   // chunks per register pass (counting)
+constexpr int kMolList = kMolUnitWork * kWave;  // hits of one unit, at most
+static_assert(kMaskWords * kWave <= 2048, "molecule list entries: 11 bits of target");
+
+template <typename T, int MODE>
+__device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const StructRec& r,
+                                               int64_t u) {
+    using O = Ops<T>;
+    const int lane = lane_id();
+    const int a0 = (int)r.atom0, n = (int)r.natoms;
+    const int f = (int)(u - r.unit0) * r.bgroup;
+    const int G = min(r.bgroup, n - f);  // <= kMolUnitWork
+    const int nch = (n + kWave - 1) / kWave;
+    const T cut2 = (T)r.cut2;
+    T sx = 0, sy = 0, sz = 0;  // lane g: source f + g
+    if (lane < G) {
+        const Vec4<T> q = a.atom_q[a0 + f + lane];
+        sx = q.x;
+        sy = q.y;
+        sz = q.z;
+    }
+    int cnt = 0;  // lane g: pairs of source f + g
+    for (int c0 = 0; c0 < nch; c0 += kMolPass) {
+        const int np = min(kMolPass, nch - c0);
+        // targets beyond the structure sit at infinity: d2 is never below cut2
+        T tx[kMolPass], ty[kMolPass], tz[kMolPass];
+        static_for<kMolPass>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const int t = (c0 + j) * kWave + lane;
+            tx[j] = ty[j] = tz[j] = (T)__builtin_inf();
+            if (j < np && t < n) {
+                const Vec4<T> q = a.atom_q[a0 + t];
+                tx[j] = q.x;
+                ty[j] = q.y;
+                tz[j] = q.z;
+            }
+        });
+        for (int g = 0; g < G; ++g) {
+            const int s = f + g;
+            const T px = read_lane(sx, g), py = read_lane(sy, g), pz = read_lane(sz, g);
+            int mlo = 0, mhi = 0;  // lane j: the mask of chunk c0 + j
+            int hits = 0;
+            static_for<kMolPass>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                if (j < np) {
+                    unsigned long long m = 0;
+                    // a half list has no target below s
+                    if ((MODE & 2) == 0 || (c0 + j + 1) * kWave > s) {
+                        const int t = (c0 + j) * kWave + lane;
+                        const T dx = O::sub(tx[j], px), dy = O::sub(ty[j], py),
+                                dz = O::sub(tz[j], pz);
+                        const T d2 = O::add(O::add(O::mul(dx, dx), O::mul(dy, dy)), O::mul(dz, dz));
+                        bool keep = d2 < cut2 && ((MODE & 2) != 0 ? t > s : t != s);
+                        if constexpr ((MODE & 1) != 0) keep = keep || t == s;
+                        m = ballot(keep);
+                    }
+                    hits += __popcll(m);
+                    mlo = write_lane<j>(mlo, (int)(unsigned)m);
+                    mhi = write_lane<j>(mhi, (int)(unsigned)(m >> 32));
+                }
+            });
+            if (lane < np)
+                a.masks[(int64_t)(a0 + s) * kMaskWords + c0 + lane] =
+                    ((unsigned long long)(unsigned)mhi << 32) | (unsigned)mlo;
+            cnt += lane == g ? hits : 0;
+        }
+    }
+    if (lane < G) a.counts[a0 + f + lane] = cnt;
+}
+
+template <typename T, int MODE>
+__device__ __forceinline__ void molecule_emit(const QueryArgs<T>& a, const StructRec& r, int b,
+                                              int64_t u, int* list) {
+    const int lane = lane_id();
+    const int a0 = (int)r.atom0, n = (int)r.natoms;
+    const int f = (int)(u - r.unit0) * r.bgroup;
+    const int G = min(r.bgroup, n - f);
+    const int nch = (n + kWave - 1) / kWave;
+    const int nw = G * nch;  // mask words of the unit, <= kMolUnitWork
+    const long long base = a.offsets[a0 + f];
+    unsigned long long mw = 0;  // lane g * nch + j: mask of source f + g, chunk j
+    if (lane < nw) {
+        const int g = lane / nch;
+        mw = a.masks[(int64_t)(a0 + f + g) * kMaskWords + (lane - g * nch)];
+    }
+    const T* cell = a.cells + 9 * b;
+    T c[9];
+#pragma unroll
+    for (int e = 0; e < 9; ++e) c[e] = cell[e];
+    const bool diagonal = r.diagonal != 0;
+    // entries (g << 11) | t in output order
+    int len = 0;
+    for (int g = 0, w = 0; g < G; ++g) {
+        for (int j = 0; j < nch; ++j, ++w) {
+            const unsigned long long m = (unsigned long long)read_lane((long long)mw, w);
+            if ((m >> lane) & 1ull) list[len + lanes_below(m)] = (g << 11) | (j * kWave + lane);
+            len += __popcll(m);
+        }
+    }
+    wave_lds_fence();
+    for (int k = lane; k < len; k += kWave) {
+        const int e = list[k];
+        const int s = a0 + f + (e >> 11), t = a0 + (e & 2047);
+        T ps[3], pt[3];
+#pragma unroll
+        for (int x = 0; x < 3; ++x) {
+            ps[x] = a.pos[3 * (int64_t)s + x];
+            pt[x] = a.pos[3 * (int64_t)t + x];
+        }
+        write_hit(a, base + k, s, t, 0, 0, 0, ps, pt, c, diagonal);
+    }
+    wave_lds_fence();  // the next unit rewrites the list
+}
+
+// Per-wave LDS of the brute-force kernels: the image walk's atoms and
+// cursors, or a molecule unit's hit list.
+template <typename T>
+union BruteWaveLds {
+    BruteLds<T> walk;
+    int mol[kMolList];
+};
+
 // Counting (EMIT false) or emitting pass of the brute-force structures: one
 // wave per work unit (grid-stride).  Exits at once when the request has no
 // brute-force structure.
@@ -531,13 +675,23 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
         !(load_status(a.status + SS_PLAN) & 1))
         return;
     if constexpr (EMIT) place_edge_index(a);
-    __shared__ BruteLds<T> s_lds[kWavesPerBlock];
+    __shared__ BruteWaveLds<T> s_lds[kWavesPerBlock];
     const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
     const int wv = uniform(threadIdx.x / kWave);
     const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
-    for (int64_t u = wave0; u < units; u += nwaves)
-        brute_unit<T, MODE, EMIT>(a, u, &s_lds[wv], s_lds[wv].c);
+    for (int64_t u = wave0; u < units; u += nwaves) {
+        const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+        const StructRec& r = a.recs[b];
+        if (molecule_path(r.active, r.natoms)) {
+            if constexpr (EMIT)
+                molecule_emit<T, MODE>(a, r, b, u, s_lds[wv].mol);
+            else
+                molecule_count<T, MODE>(a, r, u);
+        } else {
+            brute_unit<T, MODE, EMIT>(a, u, b, &s_lds[wv].walk, s_lds[wv].walk.c);
+        }
+    }
 }
 
 }  // namespace tnr
