@@ -148,3 +148,23 @@ def test_molecule_repeated_calls_with_smaller_batch():
         expected = keys_of(*oracle_call(cfg, algorithm="brute_force"))
         pairs, shifts = gpu("PS", cfg)
         assert_same_keys(keys_of(pairs, shifts), expected)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_molecules_beside_cell_list_structures(dtype):
+    # with algorithm 'auto', small molecules take the molecule form and large
+    # ones, and the periodic box, a cell list: both store hit masks in one
+    # buffer, the molecules in slots counted down from the top
+    sizes = [90, 1500, 40, 700, 2500, 120]
+    pbcs = [[0, 0, 0], [0, 0, 0], [0, 0, 0], [1, 1, 1], [1, 1, 1], [0, 0, 0]]
+    for mode, (half_list, include_self) in enumerate(
+            [(False, False), (False, True), (True, False), (True, True)]):
+        cfg = batch(sizes, pbcs, dtype, 1201 + mode, half_list=half_list,
+                    include_self=include_self)
+        print(f"molecules beside cell lists {np.dtype(dtype).name} mode {mode}", flush=True)
+        expected = keys_of(*oracle_call(cfg, algorithm="brute_force"))
+        for sorted_ in (False, True):
+            pairs, shifts, d, D = gpu("PSdD", cfg, algorithm="auto", sorted=sorted_)
+            assert_same_keys(keys_of(pairs, shifts), expected)
+            assert_grouped_by_source(pairs)
+            assert_geometry_close(pairs, shifts, d, D, cfg)

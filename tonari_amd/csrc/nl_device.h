@@ -89,6 +89,7 @@ struct alignas(16) StructRec {
     int64_t bin0;
     int64_t nbins;
     int64_t unit0;       // first brute-force work unit of the structure
+    int64_t mask0;       // molecules: hit-mask slot of the structure's first atom
     double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
     double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
     double lo[3];        // grid origin (inactive axes)
@@ -144,8 +145,10 @@ struct Layout {
 
 // Hit masks stored per cell-list source: one 64-bit word per chunk of 64
 // stencil candidates, for stencils of up to kMaskWords * 64 candidates.
-// Molecules (below) store theirs in the same place: one word per chunk of
-// 64 targets.
+// Molecules (below) store theirs in the same buffer, one word per chunk of
+// 64 targets, in slots counted down from the top: the cell-list sources of
+// a request fill slots [0, cell-list atoms) by binned position, its
+// molecules slots [n - molecule atoms, n), so the two never meet.
 constexpr int kMaskWords = 32;
 
 // Molecules: brute-force structures with no periodic axis and at most

@@ -115,6 +115,7 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     r.bin0 = 0;
     r.nbins = 0;
     r.unit0 = 0;
+    r.mask0 = 0;
     r.bgroup = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
@@ -860,19 +861,21 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
     }
     if (fused_scan) {
         __syncthreads();
-        struct_scan_block(struct_bins, struct_units, nb, bin_off, unit_off, recs, status,
-                          cap_bins);
+        struct_scan_block(struct_bins, struct_units, nb, n_atoms, bin_off, unit_off, recs,
+                          status, cap_bins);
     }
 }
 
 // The batch-wide step of the planner (one workgroup, after k_plan).
 __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
                                                          const long long* struct_units,
-                                                         int64_t nb, long long* bin_off,
-                                                         long long* unit_off, StructRec* recs,
+                                                         int64_t nb, int64_t n_atoms,
+                                                         long long* bin_off, long long* unit_off,
+                                                         StructRec* recs,
                                                          unsigned long long* status,
                                                          int64_t cap_bins) {
-    struct_scan_block(struct_bins, struct_units, nb, bin_off, unit_off, recs, status, cap_bins);
+    struct_scan_block(struct_bins, struct_units, nb, n_atoms, bin_off, unit_off, recs, status,
+                      cap_bins);
 }
 
 template <typename T>

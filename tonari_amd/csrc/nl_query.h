@@ -537,8 +537,8 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
 // 63).
 //   Counting: lane l holds target 64 c + l of each chunk c of a register
 //   pass; each source is read from the lane that holds it, and one ballot
-//   per (source, chunk) gives the hit mask, stored where the cell list
-//   stores its masks (kMaskWords words per atom).
+//   per (source, chunk) gives the hit mask, stored in the hit-mask buffer
+//   from the structure's slot mask0 on (kMaskWords words per atom).
 //   Emitting: the unit's masks are decoded into a list of (source, target)
 //   entries in the wave's LDS, in source and target order, and written 64
 //   pairs per round.  The unit's sources are consecutive atoms, so their
@@ -606,7 +606,7 @@ __device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const Stru
                 }
             });
             if (lane < np)
-                a.masks[(int64_t)(a0 + s) * kMaskWords + c0 + lane] =
+                a.masks[(r.mask0 + s) * kMaskWords + c0 + lane] =
                     ((unsigned long long)(unsigned)mhi << 32) | (unsigned)mlo;
             cnt += lane == g ? hits : 0;
         }
@@ -627,7 +627,7 @@ __device__ __forceinline__ void molecule_emit(const QueryArgs<T>& a, const Struc
     unsigned long long mw = 0;  // lane g * nch + j: mask of source f + g, chunk j
     if (lane < nw) {
         const int g = lane / nch;
-        mw = a.masks[(int64_t)(a0 + f + g) * kMaskWords + (lane - g * nch)];
+        mw = a.masks[(r.mask0 + f + g) * kMaskWords + (lane - g * nch)];
     }
     const T* cell = a.cells + 9 * b;
     T c[9];

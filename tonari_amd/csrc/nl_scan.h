@@ -158,55 +158,66 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
 
 // One workgroup: exclusive scans of the bins and of the brute-force work
 // units per structure into bin_off and unit_off ([0..nb]; each structure's
-// first bin and unit also go to its record), their totals, and the batch
-// checks that need every structure's plan: total periodic images and bin
-// capacity.
+// first bin and unit also go to its record), of the molecule atoms (each
+// molecule's hit-mask slots, counted down from n_atoms, go to its record),
+// their totals, and the batch checks that need every structure's plan:
+// total periodic images and bin capacity.  Every load of a chunk is issued at once (indices clamped to
+// the last structure, values masked), and the batch reductions go through
+// wave reductions and one LDS slot per wave, without atomics.
 __device__ void struct_scan_block(const long long* struct_bins, const long long* struct_units,
-                                  int64_t nb, long long* bin_off, long long* unit_off,
-                                  StructRec* recs, unsigned long long* status,
-                                  int64_t cap_bins) {
-    __shared__ long long s_carry, s_ucarry;
-    __shared__ unsigned long long s_flags, s_plan, s_images, s_wrap;
+                                  int64_t nb, int64_t n_atoms, long long* bin_off,
+                                  long long* unit_off, StructRec* recs,
+                                  unsigned long long* status, int64_t cap_bins) {
+    __shared__ long long s_carry, s_ucarry, s_mcarry;
+    __shared__ unsigned long long s_red[4][kWavesPerBlock];
     if (threadIdx.x == 0) {
         s_carry = 0;
         s_ucarry = 0;
-        s_flags = 0;
-        s_plan = 0;
-        s_images = 0;
-        s_wrap = 0;
+        s_mcarry = 0;
     }
     __syncthreads();
     unsigned long long flags = 0, plan = 0, images = 0, wrap = 0;
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
-        long long v[kScanItems], u[kScanItems];
-        long long sum = 0, usum = 0;
+        long long v[kScanItems], u[kScanItems], m[kScanItems];
+        long long sum = 0, usum = 0, msum = 0;
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
             const int64_t i = i0 + k;
-            v[k] = i < nb ? struct_bins[i] : 0;
-            u[k] = i < nb ? struct_units[i] : 0;
+            const bool in = i < nb;
+            const int64_t ic = in ? i : nb - 1;
+            const StructRec& r = recs[ic];
+            const long long bv = struct_bins[ic], uv = struct_units[ic];
+            const unsigned long long fl = r.flags;
+            const int algo = r.algo, aw = r.any_wrap, active = r.active;
+            const long long img = r.img_total, na = r.natoms;
+            v[k] = in ? bv : 0;
+            u[k] = in ? uv : 0;
+            m[k] = in && algo == ALGO_BRUTE && molecule_path(active, na) ? na : 0;
             sum += v[k];
             usum += u[k];
-            if (i < nb) {
-                const StructRec& r = recs[i];
-                flags |= r.flags;
-                plan |= r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
-                if (r.algo == ALGO_CELL && r.any_wrap) wrap = 1;
-                images += (unsigned long long)r.img_total;
+            msum += m[k];
+            if (in) {
+                flags |= fl;
+                plan |= algo == ALGO_CELL ? 2ull : (algo == ALGO_BRUTE ? 1ull : 0ull);
+                if (algo == ALGO_CELL && aw) wrap = 1;
+                images += (unsigned long long)img;
             }
         }
-        long long tot, utot;
+        long long tot, utot, mtot;
         long long run = block_exclusive_scan(sum, &tot) + s_carry;
         long long urun = block_exclusive_scan(usum, &utot) + s_ucarry;
+        long long mrun = block_exclusive_scan(msum, &mtot) + s_mcarry;
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
             const int64_t i = i0 + k;
+            mrun += m[k];
             if (i < nb) {
                 bin_off[i] = run;
                 recs[i].bin0 = run;
                 unit_off[i] = urun;
                 recs[i].unit0 = urun;
+                recs[i].mask0 = n_atoms - mrun;
             }
             run += v[k];
             urun += u[k];
@@ -215,26 +226,45 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         if (threadIdx.x == 0) {
             s_carry += tot;
             s_ucarry += utot;
+            s_mcarry += mtot;
         }
         __syncthreads();
     }
-    if (flags) atomicOr(&s_flags, flags);
-    if (plan) atomicOr(&s_plan, plan);
-    if (images) atomicAdd(&s_images, images);
-    if (wrap) atomicOr(&s_wrap, wrap);
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        flags |= __shfl_xor(flags, d);
+        plan |= __shfl_xor(plan, d);
+        wrap |= __shfl_xor(wrap, d);
+        images += __shfl_xor(images, d);
+    }
+    const int w = threadIdx.x / kWave;
+    if (lane_id() == 0) {
+        s_red[0][w] = flags;
+        s_red[1][w] = plan;
+        s_red[2][w] = images;
+        s_red[3][w] = wrap;
+    }
     __syncthreads();
     if (threadIdx.x == 0) {
+        unsigned long long all_flags = 0, all_plan = 0, all_images = 0, all_wrap = 0;
+#pragma unroll
+        for (int x = 0; x < kWavesPerBlock; ++x) {
+            all_flags |= s_red[0][x];
+            all_plan |= s_red[1][x];
+            all_images += s_red[2][x];
+            all_wrap |= s_red[3][x];
+        }
         const long long total = s_carry;
         bin_off[nb] = total;
         unit_off[nb] = s_ucarry;
         status[SS_TOTAL_BINS] = (unsigned long long)total;
         status[SS_TOTAL_UNITS] = (unsigned long long)s_ucarry;
-        status[SS_PLAN] = s_plan;
-        status[SS_TOTAL_IMAGES] = s_images;
-        status[SS_ANY_WRAP] = s_wrap;
-        unsigned long long st = s_flags;
+        status[SS_PLAN] = all_plan;
+        status[SS_TOTAL_IMAGES] = all_images;
+        status[SS_ANY_WRAP] = all_wrap;
+        unsigned long long st = all_flags;
         if (total > cap_bins) st |= ST_CAPACITY;
-        if (s_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+        if (all_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
         if (st) atomicOr(status + SS_FLAGS, st);
     }
 }

@@ -285,7 +285,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
             v.block_partials, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
             L.cap_bins, v.status, fused_scan);
         if (!fused_scan)
-            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb,
+            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb, n,
                                                     v.struct_bin_off, v.struct_unit_off, v.recs,
                                                     v.status, L.cap_bins);
         if (n > 0 && req->algorithm != TNR_BRUTE_FORCE)
