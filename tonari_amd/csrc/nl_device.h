@@ -30,8 +30,9 @@ constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
 constexpr int64_t kAutoBrutePeriodic = 2500;
 constexpr int64_t kAutoBruteIsolated = 384;
 // Brute force: a work unit takes about this many rounds of one image walk
-// per lane, a round costing 1 + images / 4 (most images fall outside the
-// cutoff sphere and are never visited).
+// per lane, a round (64 (source, k0, target) triples) costing 1 + (images
+// of one k0 plane) / 4 (most images fall outside the cutoff sphere and are
+// never visited).
 constexpr double kBruteUnitWork = 16.0;
 constexpr int kBruteGroupCap = 256;  // sources per brute-force work unit (at most)
 
@@ -89,7 +90,7 @@ struct alignas(16) StructRec {
     int64_t bin0;
     int64_t nbins;
     int64_t unit0;       // first brute-force work unit of the structure
-    int64_t mask0;       // molecules: hit-mask slot of the structure's first atom
+    int64_t mask0;       // brute force: hit-mask slot of the structure's first atom
     double dual[9];      // [cartesian][axis] pseudo-inverse columns, 0 for inactive axes
     double grid[9];      // [axis][cartesian]: grid coordinate u_a = grid[a] . q
     double lo[3];        // grid origin (inactive axes)
@@ -112,6 +113,8 @@ struct alignas(16) StructRec {
     int32_t any_wrap;
     int32_t diagonal;    // every off-diagonal cell entry is zero
     int32_t bgroup;      // brute force: sources per work unit
+    int32_t bslices;     // brute force: work units per source group (slices of k0)
+    int32_t bwidth;      // brute force: k0 values per slice
 };
 
 // The 14 per-structure reductions over atoms, all kept as maxima of
@@ -145,10 +148,12 @@ struct Layout {
 
 // Hit masks stored per cell-list source: one 64-bit word per chunk of 64
 // stencil candidates, for stencils of up to kMaskWords * 64 candidates.
-// Molecules (below) store theirs in the same buffer, one word per chunk of
-// 64 targets, in slots counted down from the top: the cell-list sources of
-// a request fill slots [0, cell-list atoms) by binned position, its
-// molecules slots [n - molecule atoms, n), so the two never meet.
+// Brute-force structures use the same buffer, in slots counted down from
+// the top: the cell-list sources of a request fill slots [0, cell-list
+// atoms) by binned position, its brute-force atoms slots [n - brute-force
+// atoms, n), so the two never meet.  A molecule (below) stores its hit masks
+// there, one word per chunk of 64 targets; a periodic structure whose
+// sources are split into k0 slices stores each slice's pair count.
 constexpr int kMaskWords = 32;
 
 // Molecules: brute-force structures with no periodic axis and at most

@@ -117,6 +117,8 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     r.unit0 = 0;
     r.mask0 = 0;
     r.bgroup = 1;
+    r.bslices = 1;
+    r.bwidth = 1;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         r.lo[a] = 0.0;
@@ -384,8 +386,9 @@ __device__ __forceinline__ void grid_coords(const StructRec& r, const T q[3], do
 // A block whose atoms all lie in one structure writes one BlockPartial
 // without atomics; a block spanning several structures uses atomics on the
 // structure records (each such structure is small, so contention is low).
-// The grid also zeroes the bin counters and the tile states of the two
-// single-pass scans, which later kernels of the request use.
+// The grid also zeroes the bin counters, the tile states of the two
+// single-pass scans and the per-source pair counts (sliced brute-force
+// sources add theirs), which later kernels of the request use.
 //
 // SINGLE (a request of one structure with atoms): the grid also does the
 // work of k_setup.  Every block derives the structure's record in LDS
@@ -399,12 +402,15 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
                                                    int* atom_struct, int4* atom_wrap,
                                                    Vec4<T>* atom_q, unsigned long long* status,
                                                    int* bin_count, int64_t n_bin_count,
-                                                   unsigned long long* tiles, int64_t n_tiles) {
+                                                   unsigned long long* tiles, int64_t n_tiles,
+                                                   long long* counts) {
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
     __shared__ unsigned long long s_flags, s_atom_flags;
     __shared__ StructRec s_rec;
     {
         const int64_t stride = (int64_t)gridDim.x * kBlock;
+        if ((int64_t)blockIdx.x * kBlock + threadIdx.x < n_atoms)
+            counts[(int64_t)blockIdx.x * kBlock + threadIdx.x] = 0;
         for (int64_t k = (int64_t)blockIdx.x * kBlock + threadIdx.x; k < n_bin_count; k += stride)
             bin_count[k] = 0;
         for (int64_t k = (int64_t)blockIdx.x * kBlock + threadIdx.x; k < n_tiles; k += stride)
@@ -782,13 +788,29 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
             r.bgroup = g;
             units = (n + g - 1) / g;
         } else if (algo == ALGO_BRUTE) {
-            // a round: 64 (source, target) pairs, costing about 1 + images / 4
-            const double round = 1.0 + 0.25 * (double)nimages;
-            const double rounds = fmax(floor(kBruteUnitWork / round), 1.0);
-            double g = fmax(floor(rounds * (double)kWave / (double)n), 1.0);
+            // a round: 64 (source, k0, target) triples, each walking the
+            // K1 x K2 images of its k0 plane, costing about 1 + K1 K2 / 4.
+            // A source whose K0 planes exceed a unit's work is split into
+            // slices of k0 (at most kMaskWords: their counts are kept in the
+            // source's hit-mask slot).
+            const int64_t K0 = 2 * (int64_t)r.reps[0] + 1;
+            const double round = 1.0 + 0.25 * (double)nimages / (double)K0;
+            const double want = fmax(kBruteUnitWork / round, 1.0);       // rounds per unit
+            const double per_source = (double)n * (double)K0 / kWave;    // rounds per source
+            double g = floor(want / per_source);
+            int64_t nsl = 1, width = K0;
+            if (g < 1.0) {
+                g = 1.0;
+                nsl = (int64_t)fmin(ceil(per_source / want),
+                                    (double)(K0 < kMaskWords ? K0 : kMaskWords));
+                width = (K0 + nsl - 1) / nsl;
+                nsl = (K0 + width - 1) / width;
+            }
             g = fmin(fmin(g, (double)n), (double)kBruteGroupCap);
             r.bgroup = (int32_t)g;
-            units = (n + (int64_t)g - 1) / (int64_t)g;
+            r.bslices = (int32_t)nsl;
+            r.bwidth = (int32_t)width;
+            units = (n + (int64_t)g - 1) / (int64_t)g * nsl;
         }
         struct_units[b] = units;
         r.flags |= st;

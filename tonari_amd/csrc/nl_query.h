@@ -182,14 +182,15 @@ __device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb,
 // Brute-force structures (neighbors_cuda.cu:89-279,443-556 and the brute path
 // of neighbors_cpu.cpp): every (source, target) pair of a structure with every
 // periodic image k of the box |k_a| <= R_a.  Here each lane takes one
-// (source, target) pair; the wave walks the rows (k0, k1) of the box, and
+// (source, k0, target) triple; the wave walks the rows k1 of the box, and
 // each lane visits only the k2 of a row whose translate can lie within the
 // padded cutoff (pair_images): a superset of the images the public predicate
 // can keep, widened far beyond its rounding and clipped to the reference's
 // box.  Every visited image is then decided as everywhere else: fused broad
 // phase, identity, and the public predicate in the band.  A wave takes one
-// work unit: bgroup consecutive sources of one structure (the planner sizes
-// units to similar work).
+// work unit: bgroup consecutive sources of one structure and one slice of
+// bwidth consecutive k0 values (the planner sizes units to similar work and
+// slices k0 only where one source's planes exceed a unit).
 
 // The integers k in [-R, R] within c - h .. c + h, each end widened by 1/256
 // plus 2^-16 of the magnitudes (the rounding of the float evaluations that
@@ -295,11 +296,11 @@ __device__ __forceinline__ WalkAtom<T> walk_atom(const QueryArgs<T>& a, int i) {
     return x;
 }
 
-// The images of the lane's (source, target) pair, row by row: the rows
-// (k0, k1) of the box are walked by the whole wave in the reference order
-// (x-major), and each lane restricts k2 to the integers where |e + k2 c2|
-// can fall below the search radius (line_range; k2 = 0 when axis 2 is not
-// periodic), so only the images near the cutoff sphere are decided.
+// The images of the lane's (source, target) pair in the lane's plane k0, row
+// by row: the rows k1 of the box are walked by the whole wave, and each lane
+// restricts k2 to the integers where |e + k2 c2| can fall below the search
+// radius (line_range; k2 = 0 when axis 2 is not periodic), so only the
+// images near the cutoff sphere are decided.
 //   PASS 0 (count): returns the kept pairs, raising the int32 shift-range
 //                   error where a kept shift does not fit.
 //   PASS 1 (write): writes the kept pairs.  Every lane runs every step of a
@@ -310,7 +311,7 @@ __device__ __forceinline__ WalkAtom<T> walk_atom(const QueryArgs<T>& a, int i) {
 //                   output position, advanced here.
 template <typename T, int MODE, int PASS>
 __device__ __forceinline__ int pair_images(const QueryArgs<T>& a, const BruteGeom<T>& g, bool valid,
-                                           int s, int t, const WalkAtom<T>& xs,
+                                           int s, int t, int k0, const WalkAtom<T>& xs,
                                            const WalkAtom<T>& xt, unsigned long long seg,
                                            long long& cursor) {
     using O = Ops<T>;
@@ -319,7 +320,7 @@ __device__ __forceinline__ int pair_images(const QueryArgs<T>& a, const BruteGeo
                           (double)xs.w.z - (double)xt.w.z};
     const unsigned long long below = (1ull << lane_id()) - 1ull;
     int hits = 0;
-    for (int k0 = -g.R0; k0 <= g.R0; ++k0) {
+    {
         const T f0 = (T)k0;
         const T e0x = O::fma_(f0, g.c[0], bx), e0y = O::fma_(f0, g.c[1], by),
                 e0z = O::fma_(f0, g.c[2], bz);
@@ -417,35 +418,38 @@ __device__ __forceinline__ int64_t unit_pairs_before(int x, int n, int f) {
     return (int64_t)x * n;
 }
 
-// Source offset x of pair p within the unit: the largest x with
-// unit_pairs_before(x) <= p, from a double estimate (off by at most one)
-// corrected in integers.
+// Source offset x of triple p within a unit of W k0 values: the largest x
+// with W unit_pairs_before(x) <= p, from a double estimate (off by at most
+// one) corrected in integers.
 template <int MODE>
-__device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G) {
+__device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G, int W) {
     int x;
     if constexpr ((MODE & 2) != 0) {
         const double A = (double)(2 * (int64_t)(n - f) + 1);
-        x = (int)((A - sqrt(fmax(A * A - 8.0 * (double)p, 0.0))) * 0.5);
+        x = (int)((A - sqrt(fmax(A * A - 8.0 * ((double)p / (double)W), 0.0))) * 0.5);
     } else {
-        x = (int)(((double)p + 0.5) / (double)n);
+        x = (int)(((double)p + 0.5) / ((double)n * (double)W));
     }
     x = min(max(x, 0), G - 1);
-    if (x + 1 < G && unit_pairs_before<MODE>(x + 1, n, f) <= p) ++x;
-    if (x > 0 && unit_pairs_before<MODE>(x, n, f) > p) --x;
+    if (x + 1 < G && (int64_t)W * unit_pairs_before<MODE>(x + 1, n, f) <= p) ++x;
+    if (x > 0 && (int64_t)W * unit_pairs_before<MODE>(x, n, f) > p) --x;
     return x;
 }
 
 // Work unit u of the brute-force structures, of structure b: sources
-// [first, first + G).  Their (source, target) pairs (targets t >= s for a half
-// list) are taken 64 per round in source order, lane l taking pair 64 r + l;
+// [first, first + G) and the k0 values of one slice.  Their (source, k0,
+// target) triples (targets t >= s for a half list), in source order, then
+// k0, then target, are taken 64 per round, lane l taking triple 64 r + l;
 // the atoms of a structure of up to kBruteStage atoms are staged in the
 // wave's LDS first.  Counting adds each lane's pairs to its source's count
-// (one LDS add per source run of the round) and stores counts[s] at the end;
-// emitting places a source's pairs from offsets[s] on, carrying its next
-// output position from round to round in LDS.  Without STAGE (L null) the
-// atoms are always read from global memory and only the cursors C live in
-// LDS: the form the cell-list counting kernel runs for the structures of an
-// explicit cell_list request that no bin grid fits.
+// (one LDS add per source run of the round); at the end it stores counts[s],
+// or, for a sliced source, adds it to counts[s] (zeroed by k_atoms) and
+// keeps the slice's count in the source's hit-mask slot.  Emitting places a
+// source's pairs from offsets[s] plus the counts of its earlier slices on,
+// carrying its next output position from round to round in LDS.  Without
+// STAGE (L null) the atoms are always read from global memory and only the
+// cursors C live in LDS: the form the cell-list counting kernel runs for the
+// structures of an explicit cell_list request that no bin grid fits.
 template <typename T, int MODE, bool EMIT, bool STAGE = true>
 __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int b,
                                            BruteLds<T>* L, BruteCursor& C) {
@@ -453,8 +457,15 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
     BruteGeom<T> g;
     brute_geom(a, r, b, g);
     const int a0 = (int)r.atom0, n = (int)r.natoms;
-    const int f = (int)(u - r.unit0) * r.bgroup;
+    const int nsl = r.bslices;
+    const int64_t ul = u - r.unit0;
+    const int grp = (int)(ul / nsl), sl = (int)(ul - (int64_t)grp * nsl);
+    const int f = grp * r.bgroup;
     const int G = min(r.bgroup, n - f);
+    const int k0a = -g.R0 + sl * r.bwidth;
+    const int W = min(r.bwidth, g.R0 - k0a + 1);  // k0 values of the slice
+    // slice counts of the unit's sources: hit-mask slot words
+    unsigned long long* slice_cnt = a.masks + (r.mask0 + f) * kMaskWords;
     const int lane = lane_id();
     const bool staged = STAGE && n <= kBruteStage;
     if (staged) {
@@ -466,10 +477,13 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
         }
     }
     for (int x = lane; x < G; x += kWave) {
-        if (EMIT)
-            C.cur[x] = a.offsets[a0 + f + x];
-        else
+        if (EMIT) {
+            long long o = a.offsets[a0 + f + x];
+            for (int j = 0; j < sl; ++j) o += (long long)slice_cnt[(int64_t)x * kMaskWords + j];
+            C.cur[x] = o;
+        } else {
             C.cnt[x] = 0;
+        }
     }
     wave_lds_fence();
     auto atom = [&](int i) {
@@ -486,38 +500,62 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
         }
         return x;
     };
-    const int64_t total = unit_pairs_before<MODE>(G, n, f);
+    const int64_t total = (int64_t)W * unit_pairs_before<MODE>(G, n, f);
     for (int64_t base = 0; base < total; base += kWave) {
         const int64_t p = base + lane;
         const bool valid = p < total;
         const int64_t pc = min(p, total - 1);
-        const int x = unit_source_of<MODE>(pc, n, f, G);
-        const int64_t q0 = unit_pairs_before<MODE>(x, n, f);
+        const int x = unit_source_of<MODE>(pc, n, f, G, W);
+        const int64_t q0 = (int64_t)W * unit_pairs_before<MODE>(x, n, f);
         const int li = f + x;
-        const int tl = ((MODE & 2) ? li : 0) + (int)(pc - q0);
-        // lanes of this round that hold pairs of the same source
+        // (k0, target) of the triple: q = k0i * len + t, len targets per k0
+        const int len = (MODE & 2) ? n - li : n;
+        const int64_t q = pc - q0;
+        int k0i = (int)((double)q / (double)len);
+        int tr = (int)(q - (int64_t)k0i * len);
+        if (tr < 0) {
+            --k0i;
+            tr += len;
+        } else if (tr >= len) {
+            ++k0i;
+            tr -= len;
+        }
+        const int tl = ((MODE & 2) ? li : 0) + tr;
+        // lanes of this round that hold triples of the same source
         const int seg_lo = (int)max(q0 - base, (int64_t)0);
-        const int seg_hi = (int)min(unit_pairs_before<MODE>(x + 1, n, f) - base, (int64_t)kWave);
+        const int seg_hi =
+            (int)min((int64_t)W * unit_pairs_before<MODE>(x + 1, n, f) - base, (int64_t)kWave);
         const unsigned long long seg =
             (seg_hi >= kWave ? ~0ull : ((1ull << seg_hi) - 1ull)) & ~((1ull << seg_lo) - 1ull);
         const WalkAtom<T> xs = atom(li), xt = atom(tl);
+        const int k0 = k0a + k0i;
         if constexpr (EMIT) {
             long long cursor = C.cur[x];
-            pair_images<T, MODE, 1>(a, g, valid, a0 + li, a0 + tl, xs, xt, seg, cursor);
+            pair_images<T, MODE, 1>(a, g, valid, a0 + li, a0 + tl, k0, xs, xt, seg, cursor);
             wave_lds_fence();
             if (valid && lane == seg_hi - 1) C.cur[x] = cursor;
         } else {
             long long unused = 0;
-            const int h = pair_images<T, MODE, 0>(a, g, valid, a0 + li, a0 + tl, xs, xt, seg,
-                                                  unused);
+            const int h = pair_images<T, MODE, 0>(a, g, valid, a0 + li, a0 + tl, k0, xs, xt,
+                                                  seg, unused);
             const int incl = wave_inclusive_scan_i32(h);
             const int before = __shfl(incl, max(seg_lo - 1, 0));
             if (valid && lane == seg_hi - 1) C.cnt[x] += incl - (seg_lo > 0 ? before : 0);
         }
         wave_lds_fence();
     }
-    if (!EMIT)
-        for (int x = lane; x < G; x += kWave) a.counts[a0 + f + x] = C.cnt[x];
+    if (!EMIT) {
+        for (int x = lane; x < G; x += kWave) {
+            const int c = C.cnt[x];
+            if (nsl == 1) {
+                a.counts[a0 + f + x] = c;
+            } else {
+                slice_cnt[(int64_t)x * kMaskWords + sl] = (unsigned long long)c;
+                atomicAdd(reinterpret_cast<unsigned long long*>(a.counts + a0 + f + x),
+                          (unsigned long long)c);
+            }
+        }
+    }
     wave_lds_fence();
 }
 

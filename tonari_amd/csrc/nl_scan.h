@@ -158,8 +158,9 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
 
 // One workgroup: exclusive scans of the bins and of the brute-force work
 // units per structure into bin_off and unit_off ([0..nb]; each structure's
-// first bin and unit also go to its record), of the molecule atoms (each
-// molecule's hit-mask slots, counted down from n_atoms, go to its record),
+// first bin and unit also go to its record), of the brute-force atoms
+// (each brute-force structure's hit-mask slots, counted down from n_atoms,
+// go to its record),
 // their totals, and the batch checks that need every structure's plan:
 // total periodic images and bin capacity.  Every load of a chunk is issued at once (indices clamped to
 // the last structure, values masked), and the batch reductions go through
@@ -189,11 +190,11 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
             const StructRec& r = recs[ic];
             const long long bv = struct_bins[ic], uv = struct_units[ic];
             const unsigned long long fl = r.flags;
-            const int algo = r.algo, aw = r.any_wrap, active = r.active;
+            const int algo = r.algo, aw = r.any_wrap;
             const long long img = r.img_total, na = r.natoms;
             v[k] = in ? bv : 0;
             u[k] = in ? uv : 0;
-            m[k] = in && algo == ALGO_BRUTE && molecule_path(active, na) ? na : 0;
+            m[k] = in && algo == ALGO_BRUTE ? na : 0;
             sum += v[k];
             usum += u[k];
             msum += m[k];

@@ -262,7 +262,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_atoms<T, true><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc, req->cutoff,
             nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q,
-            v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
+            v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles, v.counts);
         k_single_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->cell, n, req->cutoff, req->algorithm, reach, v.recs, v.block_partials,
             (int64_t)blocks_for(n), (const Vec4<T>*)v.atom_q, v.atom_bin, v.atom_rank,
@@ -277,7 +277,8 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
             k_atoms<T, false><<<blocks_for(n), kBlock, 0, stream>>>(
                 (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc,
                 req->cutoff, nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
-                (Vec4<T>*)v.atom_q, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles);
+                (Vec4<T>*)v.atom_q, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles,
+                v.counts);
         // a single structure is planned and scanned by one workgroup
         const int fused_scan = nb <= 1 ? 1 : 0;
         k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
