@@ -206,7 +206,11 @@ __device__ __forceinline__ void axis_range(T c, T h, int R, int& lo, int& hi) {
 // The integers k in [-R, R] for which |p + k v|^2 < rho2 may hold: the
 // closest approach of the line p + x v lies at x = c = -(p.v)/|v|^2, at
 // distance |q| with q = p + c v, and |p + x v|^2 = |q|^2 + (x - c)^2 |v|^2.
-// rho2 is widened by 2^-20 |p|^2, which covers the cancellation in |q|.
+// rho2 is widened by 2^-20 |p|^2, which covers the cancellation in |q|.  The
+// half-width comes from the hardware square root in float (within an ulp;
+// axis_range widens each end by far more).
+__device__ __forceinline__ float range_sqrt(float x) { return __builtin_amdgcn_sqrtf(x); }
+__device__ __forceinline__ double range_sqrt(double x) { return sqrt(x); }
 template <typename T>
 __device__ __forceinline__ void line_range(T px, T py, T pz, T vx, T vy, T vz, T inv_vv, T rho2,
                                            int R, int& lo, int& hi) {
@@ -219,7 +223,7 @@ __device__ __forceinline__ void line_range(T px, T py, T pz, T vx, T vy, T vz, T
         hi = 0;
         return;
     }
-    axis_range(c, sqrt(h2), R, lo, hi);
+    axis_range(c, range_sqrt(h2), R, lo, hi);
 }
 
 // Wave-uniform geometry of a brute-force structure.
@@ -436,6 +440,23 @@ __device__ __forceinline__ int unit_source_of(int64_t p, int n, int f, int G, in
     return x;
 }
 
+// q / d (returned) and q mod d (rem) for 0 <= q < 2^24 and d >= 1, from a
+// float estimate: (float)q is exact and q * inv_d (inv_d = 1 / d rounded)
+// is within one of q / d, so one correction step gives the quotient.
+__device__ __forceinline__ int div_small(int q, int d, float inv_d, int& rem) {
+    int x = (int)((float)q * inv_d);
+    int r = q - x * d;
+    if (r < 0) {
+        --x;
+        r += d;
+    } else if (r >= d) {
+        ++x;
+        r -= d;
+    }
+    rem = r;
+    return x;
+}
+
 // Work unit u of the brute-force structures, of structure b: sources
 // [first, first + G) and the k0 values of one slice.  Their (source, k0,
 // target) triples (targets t >= s for a half list), in source order, then
@@ -486,9 +507,12 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
         }
     }
     wave_lds_fence();
-    auto atom = [&](int i) {
+    // the atoms of the unit's pairs: from LDS when staged, else from global
+    // memory (two instances of the round loop below, so that each one's
+    // loads keep their own address space)
+    auto atom = [&](auto from_lds, int i) {
         WalkAtom<T> x;
-        if (staged) {
+        if constexpr (decltype(from_lds)::value) {
             x.q = L->q[i];
             x.w = L->w[i];
             const Vec4<T> p = L->p[i];
@@ -501,49 +525,69 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
         return x;
     };
     const int64_t total = (int64_t)W * unit_pairs_before<MODE>(G, n, f);
-    for (int64_t base = 0; base < total; base += kWave) {
-        const int64_t p = base + lane;
-        const bool valid = p < total;
-        const int64_t pc = min(p, total - 1);
-        const int x = unit_source_of<MODE>(pc, n, f, G, W);
-        const int64_t q0 = (int64_t)W * unit_pairs_before<MODE>(x, n, f);
-        const int li = f + x;
-        // (k0, target) of the triple: q = k0i * len + t, len targets per k0
-        const int len = (MODE & 2) ? n - li : n;
-        const int64_t q = pc - q0;
-        int k0i = (int)((double)q / (double)len);
-        int tr = (int)(q - (int64_t)k0i * len);
-        if (tr < 0) {
-            --k0i;
-            tr += len;
-        } else if (tr >= len) {
-            ++k0i;
-            tr -= len;
-        }
-        const int tl = ((MODE & 2) ? li : 0) + tr;
-        // lanes of this round that hold triples of the same source
-        const int seg_lo = (int)max(q0 - base, (int64_t)0);
-        const int seg_hi =
-            (int)min((int64_t)W * unit_pairs_before<MODE>(x + 1, n, f) - base, (int64_t)kWave);
-        const unsigned long long seg =
-            (seg_hi >= kWave ? ~0ull : ((1ull << seg_hi) - 1ull)) & ~((1ull << seg_lo) - 1ull);
-        const WalkAtom<T> xs = atom(li), xt = atom(tl);
-        const int k0 = k0a + k0i;
-        if constexpr (EMIT) {
-            long long cursor = C.cur[x];
-            pair_images<T, MODE, 1>(a, g, valid, a0 + li, a0 + tl, k0, xs, xt, seg, cursor);
+    // a full list of fewer than 2^24 triples: (source, k0, target) by two
+    // small divisions (the unit's triples are source-major blocks of n W)
+    const bool small = (MODE & 2) == 0 && total < (int64_t{1} << 24);
+    const int nW = small ? n * W : 1;
+    const float inv_nW = 1.0f / (float)nW, inv_n = 1.0f / (float)n;
+    auto rounds = [&](auto from_lds) {
+        for (int64_t base = 0; base < total; base += kWave) {
+            const int64_t p = base + lane;
+            const bool valid = p < total;
+            const int64_t pc = min(p, total - 1);
+            int x, k0i, tr;
+            int64_t q0;
+            if (small) {
+                int rem;
+                x = div_small((int)pc, nW, inv_nW, rem);
+                k0i = div_small(rem, n, inv_n, tr);
+                q0 = (int64_t)x * nW;
+            } else {
+                x = unit_source_of<MODE>(pc, n, f, G, W);
+                q0 = (int64_t)W * unit_pairs_before<MODE>(x, n, f);
+                // (k0, target) of the triple: q = k0i * len + t, len targets per k0
+                const int len = (MODE & 2) ? n - (f + x) : n;
+                const int64_t q = pc - q0;
+                k0i = (int)((double)q / (double)len);
+                tr = (int)(q - (int64_t)k0i * len);
+                if (tr < 0) {
+                    --k0i;
+                    tr += len;
+                } else if (tr >= len) {
+                    ++k0i;
+                    tr -= len;
+                }
+            }
+            const int li = f + x;
+            const int tl = ((MODE & 2) ? li : 0) + tr;
+            // lanes of this round that hold triples of the same source
+            const int seg_lo = (int)max(q0 - base, (int64_t)0);
+            const int64_t q1 = small ? q0 + nW : (int64_t)W * unit_pairs_before<MODE>(x + 1, n, f);
+            const int seg_hi = (int)min(q1 - base, (int64_t)kWave);
+            const unsigned long long seg =
+                (seg_hi >= kWave ? ~0ull : ((1ull << seg_hi) - 1ull)) & ~((1ull << seg_lo) - 1ull);
+            const WalkAtom<T> xs = atom(from_lds, li), xt = atom(from_lds, tl);
+            const int k0 = k0a + k0i;
+            if constexpr (EMIT) {
+                long long cursor = C.cur[x];
+                pair_images<T, MODE, 1>(a, g, valid, a0 + li, a0 + tl, k0, xs, xt, seg, cursor);
+                wave_lds_fence();
+                if (valid && lane == seg_hi - 1) C.cur[x] = cursor;
+            } else {
+                long long unused = 0;
+                const int h = pair_images<T, MODE, 0>(a, g, valid, a0 + li, a0 + tl, k0, xs, xt,
+                                                      seg, unused);
+                const int incl = wave_inclusive_scan_i32(h);
+                const int before = __shfl(incl, max(seg_lo - 1, 0));
+                if (valid && lane == seg_hi - 1) C.cnt[x] += incl - (seg_lo > 0 ? before : 0);
+            }
             wave_lds_fence();
-            if (valid && lane == seg_hi - 1) C.cur[x] = cursor;
-        } else {
-            long long unused = 0;
-            const int h = pair_images<T, MODE, 0>(a, g, valid, a0 + li, a0 + tl, k0, xs, xt,
-                                                  seg, unused);
-            const int incl = wave_inclusive_scan_i32(h);
-            const int before = __shfl(incl, max(seg_lo - 1, 0));
-            if (valid && lane == seg_hi - 1) C.cnt[x] += incl - (seg_lo > 0 ? before : 0);
         }
-        wave_lds_fence();
-    }
+    };
+    if (staged)
+        rounds(std::true_type{});
+    else
+        rounds(std::false_type{});
     if (!EMIT) {
         for (int x = lane; x < G; x += kWave) {
             const int c = C.cnt[x];
