@@ -40,12 +40,13 @@
 extern "C" {
 #endif
 
-#define TNR_ABI_VERSION 4
+#define TNR_ABI_VERSION 5
 
 #define TNR_OK 0
 #define TNR_INPUT_ERROR 1
 #define TNR_SEARCH_ERROR 2
 #define TNR_DEVICE_ERROR 3
+#define TNR_RETRY 4 /* tnr_count_finish: a plan hint did not hold; count again without it */
 
 /* Slots of host_result: status flags, E, total periodic images, plan mask,
  * total cell-list bins, two internal tickets, one unused slot. */
@@ -130,6 +131,21 @@ int tnr_count(const tnr_request* req, void* workspace, size_t workspace_bytes,
  * `stream`; `host_result` is valid once the stream has reached this point. */
 int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_bytes,
                     int64_t* host_result, void* stream, char* err, size_t err_len);
+
+/*
+ * No counterpart in the reference (its binding plans on the host and reads
+ * the plan back, bindings_cuda.cpp:96-98,161-185).  tnr_count_async with a
+ * plan hint: host_result[3] (the plan mask) of an earlier count of a
+ * request of the same shape, or -1 for none.  With algorithm TNR_AUTO and
+ * plan_hint 1 (brute-force structures only) the cell-list kernels are not
+ * launched.  The device planner checks the hint: if some structure is
+ * planned as a cell list after all, nothing of this count is valid and
+ * tnr_count_finish returns TNR_RETRY; the caller counts again without the
+ * hint.  Other hints (and other algorithms) launch the full count.
+ */
+int tnr_count_async_hinted(const tnr_request* req, void* workspace, size_t workspace_bytes,
+                           int64_t* host_result, void* stream, int64_t plan_hint, char* err,
+                           size_t err_len);
 
 /* Decodes `host_result` written by a completed tnr_count_async: maps the
  * status flags to the reference's error types and messages, sets *n_pairs. */

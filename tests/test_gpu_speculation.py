@@ -84,3 +84,70 @@ def test_plan_switch():
     box = W.c4(seed=17, n_atoms=n, density=0.1)
     for cfg in (cluster, box, cluster, box):
         check(cfg)
+
+
+def _molecules(sizes, seed):
+    rng = np.random.default_rng(seed)
+    pos = [rng.uniform(0.0, (n / 0.05) ** (1 / 3), (n, 3)) + 40.0 * k for k, n in enumerate(sizes)]
+    return {
+        "positions": np.concatenate(pos).astype(np.float32),
+        "cell": np.zeros((len(sizes), 3, 3), np.float32),
+        "pbc": np.zeros((len(sizes), 3), bool),
+        "batch_ptr": np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64),
+        "cutoff": 4.0,
+    }
+
+
+def test_plan_hint_miss_in_a_batch():
+    # batches of one shape: molecules that auto searches by brute force
+    # (each at most 384 atoms), then the same atom count with one molecule of
+    # 500 atoms (a cell list).  A repeat after a brute-force-only plan counts
+    # without the cell-list kernels; the device finds the cell list and the
+    # count runs again in full.
+    brute = _molecules([200, 300, 100, 250], 18)
+    mixed = _molecules([500, 150, 100, 100], 19)
+    for cfg in (brute, brute, mixed, brute, mixed, mixed):
+        check(cfg)
+
+
+def test_plan_hint_through_the_abi():
+    import ctypes
+
+    from tonari_amd._extensions import (
+        ALGORITHMS, TNR_OK, TNR_RETRY, Request, load_torch_hip,
+    )
+
+    lib = load_torch_hip()
+
+    def count(cfg, hint):
+        t = {k: torch.as_tensor(cfg[k]).to(DEV) for k in ("positions", "cell", "pbc", "batch_ptr")}
+        req = Request(
+            dtype=0, algorithm=ALGORITHMS["auto"], n_atoms=t["positions"].shape[0],
+            n_structures=t["batch_ptr"].numel() - 1, positions=t["positions"].data_ptr(),
+            batch_ptr=t["batch_ptr"].data_ptr(), cell=t["cell"].data_ptr(),
+            pbc=t["pbc"].data_ptr(), cutoff=cfg["cutoff"], half_list=0, include_self=0,
+            sorted=0, stencil_reach=0,
+        )
+        ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+        host = torch.zeros(8, dtype=torch.int64, pin_memory=True)
+        err = ctypes.create_string_buffer(256)
+        stream = torch.cuda.current_stream().cuda_stream
+        assert lib.tnr_count_async_hinted(ctypes.byref(req), ws.data_ptr(), ws_bytes,
+                                          host.data_ptr(), stream, hint, err, len(err)) == TNR_OK
+        torch.cuda.synchronize()
+        n = ctypes.c_int64(-1)
+        code = lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err))
+        return code, int(n.value), int(host[3]), err.value.decode()
+
+    brute = _molecules([200, 300, 100, 250], 18)
+    mixed = _molecules([500, 150, 100, 100], 19)
+    for cfg, plan in ((brute, 1), (mixed, 3)):
+        expected = len(keys_of(*oracle_call(cfg, algorithm="brute_force")))
+        code, n, got_plan, _ = count(cfg, -1)
+        assert code == TNR_OK and n == expected and (got_plan & 3) == plan
+        code, n, _, msg = count(cfg, 1)
+        if plan == 1:
+            assert code == TNR_OK and n == expected
+        else:
+            assert code == TNR_RETRY and "plan hint" in msg

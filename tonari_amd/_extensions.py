@@ -14,10 +14,10 @@ from functools import lru_cache
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 HOST_RESULT_SLOTS = 8
 
-TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR = 0, 1, 2, 3
+TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR, TNR_RETRY = 0, 1, 2, 3, 4
 ALGORITHMS = {"auto": 0, "brute_force": 1, "cell_list": 2}
 EXPORTS = (
     "tnr_abi_version",
@@ -26,6 +26,7 @@ EXPORTS = (
     "tnr_workspace_size",
     "tnr_count",
     "tnr_count_async",
+    "tnr_count_async_hinted",
     "tnr_count_finish",
     "tnr_geometry_backward",
     "tnr_emit",
@@ -112,6 +113,11 @@ def open_library(path: str = LIBRARY) -> ctypes.CDLL:
     lib.tnr_count_async.argtypes = [
         ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+    ]
+    lib.tnr_count_async_hinted.restype = ctypes.c_int
+    lib.tnr_count_async_hinted.argtypes = [
+        ctypes.POINTER(Request), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_int64, ctypes.c_char_p, ctypes.c_size_t,
     ]
     lib.tnr_count_finish.restype = ctypes.c_int
     lib.tnr_count_finish.argtypes = [

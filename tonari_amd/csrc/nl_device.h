@@ -57,11 +57,16 @@ enum StatusBit : unsigned long long {
     // (outputs sized for another pair count); not an abort bit, so the pass
     // can run again on the same workspace with larger outputs
     ST_OUTPUT_RANGE = 1ull << 15,
+    // a count launched with a brute-force-only plan hint (no cell-list
+    // kernels) met a structure planned as a cell list: nothing of the count
+    // is valid, the caller counts again without the hint
+    ST_PLAN_HINT = 1ull << 16,
 };
 // Bits that make every later kernel skip its work (inputs are unusable).
 constexpr unsigned long long kAbortBits =
     ST_BP_START | ST_BP_END | ST_BP_ORDER | ST_CELL_NONFINITE | ST_CELL_RANK | ST_DUAL_RANGE |
-    ST_REPEAT_RANGE | ST_IMAGE_CAP | ST_POS_NONFINITE | ST_WRAP_RANGE | ST_CAPACITY;
+    ST_REPEAT_RANGE | ST_IMAGE_CAP | ST_POS_NONFINITE | ST_WRAP_RANGE | ST_CAPACITY |
+    ST_PLAN_HINT;
 
 // Slots of the status block (int64 each).
 enum StatusSlot : int {

@@ -884,7 +884,7 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
     if (fused_scan) {
         __syncthreads();
         struct_scan_block(struct_bins, struct_units, nb, n_atoms, bin_off, unit_off, recs,
-                          status, cap_bins);
+                          status, cap_bins, 0);
     }
 }
 
@@ -895,9 +895,9 @@ __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_
                                                          long long* bin_off, long long* unit_off,
                                                          StructRec* recs,
                                                          unsigned long long* status,
-                                                         int64_t cap_bins) {
+                                                         int64_t cap_bins, int brute_hint) {
     struct_scan_block(struct_bins, struct_units, nb, n_atoms, bin_off, unit_off, recs, status,
-                      cap_bins);
+                      cap_bins, brute_hint);
 }
 
 template <typename T>
@@ -952,7 +952,8 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
     const T* cells, int64_t n_atoms, double cutoff, int requested, int reach_target,
     StructRec* recs, const BlockPartial* partials, int64_t n_partials, const Vec4<T>* atom_q,
     int* atom_bin, int* atom_rank, int* bin_count, long long* struct_bins, long long* bin_off,
-    long long* struct_units, long long* unit_off, int64_t cap_bins, unsigned long long* status) {
+    long long* struct_units, long long* unit_off, int64_t cap_bins, unsigned long long* status,
+    int brute_hint) {
     using K = RedKeys<T>;
     __shared__ StructRec s_rec;
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
@@ -1030,6 +1031,7 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
             unsigned long long st = r.flags;
             if (s_bins > cap_bins) st |= ST_CAPACITY;
             if (images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+            if (brute_hint && r.algo == ALGO_CELL) st |= ST_PLAN_HINT;
             status[SS_TOTAL_BINS] = (unsigned long long)s_bins;
             status[SS_TOTAL_UNITS] = (unsigned long long)s_units;
             status[SS_ANY_WRAP] = r.algo == ALGO_CELL && r.any_wrap ? 1ull : 0ull;

@@ -162,13 +162,16 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
 // (each brute-force structure's hit-mask slots, counted down from n_atoms,
 // go to its record),
 // their totals, and the batch checks that need every structure's plan:
-// total periodic images and bin capacity.  Every load of a chunk is issued at once (indices clamped to
-// the last structure, values masked), and the batch reductions go through
-// wave reductions and one LDS slot per wave, without atomics.
+// total periodic images, bin capacity and, for a count launched without the
+// cell-list kernels (brute_hint), the absence of cell-list structures.
+// Every load of a chunk is issued at once (indices clamped to the last
+// structure, values masked), and the batch reductions go through wave
+// reductions and one LDS slot per wave, without atomics.
 __device__ void struct_scan_block(const long long* struct_bins, const long long* struct_units,
                                   int64_t nb, int64_t n_atoms, long long* bin_off,
                                   long long* unit_off, StructRec* recs,
-                                  unsigned long long* status, int64_t cap_bins) {
+                                  unsigned long long* status, int64_t cap_bins,
+                                  int brute_hint) {
     __shared__ long long s_carry, s_ucarry, s_mcarry;
     __shared__ unsigned long long s_red[4][kWavesPerBlock];
     if (threadIdx.x == 0) {
@@ -266,6 +269,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         unsigned long long st = all_flags;
         if (total > cap_bins) st |= ST_CAPACITY;
         if (all_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+        if (brute_hint && (all_plan & 2ull)) st |= ST_PLAN_HINT;
         if (st) atomicOr(status + SS_FLAGS, st);
     }
 }

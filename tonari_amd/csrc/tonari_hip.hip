@@ -199,7 +199,8 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
 
 // Counting: the plan is only known on the device, so with auto both
 // families are launched and each exits at once when the plan has none of
-// its structures.  An explicit brute_force request launches the brute-force
+// its structures, unless plan is 1 (a hint that there is no cell-list
+// structure, checked by the planner).  An explicit brute_force request launches the brute-force
 // kernel only, an explicit cell_list request the cell-list kernel only,
 // which also counts the structures that no bin grid fits (brute force,
 // QueryArgs::brute_in_cell).  Emitting: plan bit 0 launches the
@@ -211,9 +212,9 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
     const int64_t n = req->n_atoms;
     if (n == 0) return;
     if constexpr (!EMIT) {
-        (void)plan;
+        // plan 1: brute force only (an explicit request or a plan hint)
         (void)n_tasks;
-        if (req->algorithm != TNR_BRUTE_FORCE)
+        if (req->algorithm != TNR_BRUTE_FORCE && plan != 1)
             k_cell_count<T, MODE><<<count_blocks<T, MODE>(2 * (L.cap_bins > n ? L.cap_bins : n)),
                                     kBlock, 0, stream>>>(q);
         if (req->algorithm != TNR_CELL_LIST)
@@ -248,9 +249,14 @@ static void dispatch_queries(const tnr_request* req, const Layout& L, const Quer
 // The count pipeline.  Its last kernel copies the status words into
 // host_out (a device-visible pointer to the caller's pinned buffer) when
 // given.
+// brute_hint: the caller expects no cell-list structure (an earlier count
+// of the same request shape planned brute force only), so the cell-list
+// kernels are not launched; the planner raises ST_PLAN_HINT if a structure
+// is planned as a cell list after all.
 template <typename T>
 static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
-                            hipStream_t stream, long long* host_out) {
+                            hipStream_t stream, long long* host_out, bool brute_hint) {
+    const bool cell_kernels = req->algorithm != TNR_BRUTE_FORCE && !brute_hint;
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
     const int reach = req->stencil_reach;  // 0: chosen per structure
@@ -267,7 +273,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
             (const T*)req->cell, n, req->cutoff, req->algorithm, reach, v.recs, v.block_partials,
             (int64_t)blocks_for(n), (const Vec4<T>*)v.atom_q, v.atom_bin, v.atom_rank,
             v.bin_count, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
-            L.cap_bins, v.status);
+            L.cap_bins, v.status, brute_hint ? 1 : 0);
     } else {
         // k_setup zeroes the status words; k_atoms zeroes the bin counters and
         // the tile states of both single-pass scans.
@@ -288,13 +294,13 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         if (!fused_scan)
             k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb, n,
                                                     v.struct_bin_off, v.struct_unit_off, v.recs,
-                                                    v.status, L.cap_bins);
-        if (n > 0 && req->algorithm != TNR_BRUTE_FORCE)
+                                                    v.status, L.cap_bins, brute_hint ? 1 : 0);
+        if (n > 0 && cell_kernels)
             k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
                                                            (const Vec4<T>*)v.atom_q, v.atom_bin,
                                                            v.atom_rank, v.bin_count, v.status);
     }
-    if (n > 0 && req->algorithm != TNR_BRUTE_FORCE) {
+    if (n > 0 && cell_kernels) {
         k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
             v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
             v.status + SS_TICKET_BINS, v.status, nullptr);
@@ -306,7 +312,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                                                            v.status);
     }
     const QueryArgs<T> q = query_args<T>(req, v);
-    dispatch_queries<T, false>(req, L, q, 0, 0, stream);
+    dispatch_queries<T, false>(req, L, q, cell_kernels ? 0 : 1, 0, stream);
     // pairs per source -> offsets; the total (E) goes to the status words
     k_scan_lookback<long long, long long>
         <<<(unsigned)((n + kScanTile - 1) / kScanTile > 0 ? (n + kScanTile - 1) / kScanTile : 1),
@@ -341,8 +347,11 @@ struct StatusMessage {
 };
 
 // Priority follows the order in which the reference raises: host-side
-// batch_ptr checks, periodic metadata, then device status words.
+// batch_ptr checks, periodic metadata, then device status words; a plan
+// hint that did not hold comes first (the count is retried without it).
 static const StatusMessage kMessages[] = {
+    {ST_PLAN_HINT, TNR_RETRY,
+     "the plan hint does not hold for this request; count again without it"},
     {ST_BP_START, TNR_INPUT_ERROR, "batch_ptr must start at zero"},
     {ST_BP_END, TNR_INPUT_ERROR, "batch_ptr must end at N_total"},
     {ST_BP_ORDER, TNR_INPUT_ERROR, "batch_ptr must be nondecreasing"},
@@ -711,6 +720,13 @@ size_t tnr_workspace_size(const tnr_request* req) {
 
 int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_bytes,
                     int64_t* host_result, void* stream, char* err, size_t err_len) {
+    return tnr_count_async_hinted(req, workspace, workspace_bytes, host_result, stream, -1, err,
+                                  err_len);
+}
+
+int tnr_count_async_hinted(const tnr_request* req, void* workspace, size_t workspace_bytes,
+                           int64_t* host_result, void* stream, int64_t plan_hint, char* err,
+                           size_t err_len) {
     tnr::Layout L;
     const int rc = tnr::check_request(req, workspace_bytes, workspace, err, err_len, &L);
     if (rc != TNR_OK) return rc;
@@ -723,10 +739,11 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
         mapped = nullptr;
         (void)hipGetLastError();
     }
+    const bool brute_hint = plan_hint == 1 && req->algorithm == TNR_AUTO;
     hipError_t e =
         req->dtype == TNR_FLOAT32
-            ? tnr::run_count<float>(req, workspace, L, s, (long long*)mapped)
-            : tnr::run_count<double>(req, workspace, L, s, (long long*)mapped);
+            ? tnr::run_count<float>(req, workspace, L, s, (long long*)mapped, brute_hint)
+            : tnr::run_count<double>(req, workspace, L, s, (long long*)mapped, brute_hint);
     if (e == hipSuccess && !mapped) {
         const tnr::Views v = tnr::views(workspace, L);
         e = hipMemcpyAsync(host_result, v.status, TNR_HOST_RESULT_SLOTS * sizeof(int64_t),
