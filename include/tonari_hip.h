@@ -135,13 +135,17 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
 /*
  * No counterpart in the reference (its binding plans on the host and reads
  * the plan back, bindings_cuda.cpp:96-98,161-185).  tnr_count_async with a
- * plan hint: host_result[3] (the plan mask) of an earlier count of a
- * request of the same shape, or -1 for none.  With algorithm TNR_AUTO and
- * plan_hint 1 (brute-force structures only) the cell-list kernels are not
- * launched.  The device planner checks the hint: if some structure is
- * planned as a cell list after all, nothing of this count is valid and
- * tnr_count_finish returns TNR_RETRY; the caller counts again without the
- * hint.  Other hints (and other algorithms) launch the full count.
+ * plan hint: host_result[3] (the plan mask: bit 0 brute-force structures,
+ * bit 1 cell-list structures, bit 2 every brute-force structure a
+ * molecule, i.e. without periodic axes and of at most 2,048 atoms) of an
+ * earlier count of a request of the same shape, or -1 for none.  Hint 1
+ * (brute force only) with algorithm TNR_AUTO: the cell-list kernels are not
+ * launched.  Hint 5 (molecules only) with TNR_AUTO or TNR_BRUTE_FORCE: one
+ * kernel plans the whole batch in place of the set-up, atom and planning
+ * kernels.  The device checks the hint: if a structure does not fit it,
+ * nothing of this count is valid and tnr_count_finish returns TNR_RETRY;
+ * the caller counts again without the hint.  Other hints launch the full
+ * count.
  */
 int tnr_count_async_hinted(const tnr_request* req, void* workspace, size_t workspace_bytes,
                            int64_t* host_result, void* stream, int64_t plan_hint, char* err,

@@ -101,13 +101,22 @@ def _molecules(sizes, seed):
 def test_plan_hint_miss_in_a_batch():
     # batches of one shape: molecules that auto searches by brute force
     # (each at most 384 atoms), then the same atom count with one molecule of
-    # 500 atoms (a cell list).  A repeat after a brute-force-only plan counts
-    # without the cell-list kernels; the device finds the cell list and the
-    # count runs again in full.
-    brute = _molecules([200, 300, 100, 250], 18)
+    # 500 atoms (a cell list), and with a periodic structure (brute force,
+    # not a molecule).  A repeat after a molecules-only plan runs the
+    # molecule prologue; the device finds the other structure and the count
+    # runs again in full.
+    brute = _molecules([200, 300, 90, 260], 18)
     mixed = _molecules([500, 150, 100, 100], 19)
-    for cfg in (brute, brute, mixed, brute, mixed, mixed):
+    periodic = _molecules([200, 300, 90, 260], 20)
+    periodic["pbc"][2] = True  # 90 atoms x 27 images: brute force under auto
+    periodic["cell"][2] = np.eye(3, dtype=np.float32) * 25.0
+    for cfg in (brute, brute, mixed, brute, mixed, mixed, brute, periodic, periodic, brute):
         check(cfg)
+    for half_list in (False, True):
+        for include_self in (False, True):
+            cfg = dict(brute, half_list=half_list, include_self=include_self)
+            for _ in range(2):
+                check(cfg, half_list=half_list, include_self=include_self)
 
 
 def test_plan_hint_through_the_abi():
@@ -140,14 +149,26 @@ def test_plan_hint_through_the_abi():
         code = lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err))
         return code, int(n.value), int(host[3]), err.value.decode()
 
-    brute = _molecules([200, 300, 100, 250], 18)
+    brute = _molecules([200, 300, 90, 260], 18)
     mixed = _molecules([500, 150, 100, 100], 19)
-    for cfg, plan in ((brute, 1), (mixed, 3)):
+    periodic = _molecules([200, 300, 90, 260], 20)
+    periodic["pbc"][2] = True
+    periodic["cell"][2] = np.eye(3, dtype=np.float32) * 25.0
+    # hint 1: brute force only; hint 5: every structure a molecule
+    for cfg, plan in ((brute, 5), (mixed, 3 | 4), (periodic, 1)):
         expected = len(keys_of(*oracle_call(cfg, algorithm="brute_force")))
         code, n, got_plan, _ = count(cfg, -1)
-        assert code == TNR_OK and n == expected and (got_plan & 3) == plan
-        code, n, _, msg = count(cfg, 1)
-        if plan == 1:
-            assert code == TNR_OK and n == expected
-        else:
-            assert code == TNR_RETRY and "plan hint" in msg
+        assert code == TNR_OK and n == expected and got_plan == plan
+        for hint in (1, 5):
+            code, n, _, msg = count(cfg, hint)
+            holds = (plan & 3) == 1 and (hint == 1 or plan & 4)
+            if holds:
+                assert code == TNR_OK and n == expected, (plan, hint)
+            else:
+                assert code == TNR_RETRY and "plan hint" in msg, (plan, hint)
+    # the molecule prologue skips the atom pass: the molecule count checks
+    # the positions
+    bad = _molecules([200, 300, 90, 260], 21)
+    bad["positions"][350, 1] = np.nan
+    code, _, _, msg = count(bad, 5)
+    assert code != TNR_OK and "finite" in msg

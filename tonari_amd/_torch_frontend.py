@@ -353,7 +353,8 @@ def neighbor_list_hip(
         arrived.synchronize()
         n_pairs = ctypes.c_int64(0)
         code = lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n_pairs), err, len(err))
-        if code == TNR_RETRY:
+        retried = code == TNR_RETRY
+        if retried:
             # the hint did not hold (a structure is planned as a cell list):
             # count again in full; the speculative emit wrote nothing
             code = lib.tnr_count_async(
@@ -370,8 +371,10 @@ def neighbor_list_hip(
         count = int(n_pairs.value)
         plan, bins = int(host_view[3]), int(host_view[4])
         if guess is not None and want:
+            # after a retried count the speculative emit wrote nothing
             fits = (
-                count <= capacity
+                not retried
+                and count <= capacity
                 and (plan & ~plan_guess) == 0
                 and (not plan & 2 or bins <= bins_guess)
             )

@@ -226,7 +226,7 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     cb.shiftcheck = cb.wrapped && (double)max(max(r.reps[0], r.reps[1]), r.reps[2]) +
                                          2.0 * (double)r.maxw >= 2147483647.0;
     cb.diagonal = r.diagonal != 0;
-    cb.by_bin = a.by_bin && load_status(a.status + SS_PLAN) == 2ull;
+    cb.by_bin = a.by_bin && (load_status(a.status + SS_PLAN) & kPlanFamilies) == 2ull;
     const BinGeom G = bin_geom(r, lbin);
     const int npieces = G.npieces;  // at most kPieceCap < kBlock
     cb.npieces = npieces;

@@ -900,6 +900,56 @@ __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_
                       cap_bins, brute_hint);
 }
 
+// The set-up and plan of a request whose structures are all molecules (a
+// plan hint from an earlier count of the same shape), one thread per
+// structure: the set-up of k_setup (block 0 zeroes the status words and the
+// pair scan's tile states), then the molecule plan (brute force with hit
+// masks needs no wraps, no bounds and no bin grid, so k_atoms, k_plan and
+// the cell-list kernels have nothing to do).  k_struct_scan follows.  A
+// structure that is not a molecule under the request's algorithm raises
+// ST_PLAN_HINT in its record, which the scan folds into the status words.
+template <typename T>
+__global__ void k_molecule_setup(const int64_t* bp, const T* cells, const uint8_t* pbc,
+                                 int64_t nb, int64_t n_atoms, double cutoff, int requested,
+                                 StructRec* recs, long long* struct_bins,
+                                 long long* struct_units, unsigned long long* status,
+                                 unsigned long long* tiles, int64_t n_tiles) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
+        for (int64_t k = threadIdx.x; k < n_tiles; k += blockDim.x) tiles[k] = 0;
+    }
+    if (b >= nb) return;
+    StructRec& r = recs[b];
+    setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, r);
+    const int64_t n = r.natoms;
+    long long units = 0;
+    if (!(r.flags & kAbortBits) && n > 0) {
+        const bool molecule = molecule_path(r.active, n) &&
+                              (requested == TNR_BRUTE_FORCE || n <= kAutoBruteIsolated);
+        if (molecule) {
+            r.algo = ALGO_BRUTE;
+            r.pad = 0.0;
+            r.maxp = 0;
+            r.maxw = 0;
+            r.any_wrap = 0;
+            r.cut2 = (double)(T)(cutoff * cutoff);
+            r.inner2 = 0.0;  // the molecule passes decide by the public predicate
+            r.outer2 = r.cut2;
+            const int chunks = (int)((n + kWave - 1) / kWave);
+            const int g = (int)min((int64_t)max(kMolUnitWork / chunks, 1), n);
+            r.bgroup = g;
+            r.bslices = 1;
+            r.bwidth = 1;
+            units = (n + g - 1) / g;
+        } else {
+            r.flags |= ST_PLAN_HINT;
+        }
+    }
+    struct_bins[b] = 0;
+    struct_units[b] = units;
+}
+
 template <typename T>
 __device__ __forceinline__ int64_t local_bin(const StructRec& r, const T q[3]) {
     double u[3];
@@ -1035,7 +1085,12 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
             status[SS_TOTAL_BINS] = (unsigned long long)s_bins;
             status[SS_TOTAL_UNITS] = (unsigned long long)s_units;
             status[SS_ANY_WRAP] = r.algo == ALGO_CELL && r.any_wrap ? 1ull : 0ull;
-            status[SS_PLAN] = r.algo == ALGO_CELL ? 2ull : (r.algo == ALGO_BRUTE ? 1ull : 0ull);
+            status[SS_PLAN] = r.algo == ALGO_CELL
+                                  ? 2ull
+                                  : (r.algo == ALGO_BRUTE
+                                         ? (molecule_path(r.active, r.natoms) ? 1ull | kPlanMolecules
+                                                                              : 1ull)
+                                         : 0ull);
             status[SS_TOTAL_IMAGES] = images;
             status[SS_FLAGS] = st;
         }

@@ -612,7 +612,7 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
 // and adding a signed zero leaves a nonzero value unchanged (a zero
 // component can only change sign), so d2 = ((dx dx + dy dy) + dz dz) with
 // d = p_t - p_s, rounded after every operation, is the public d2 bit for
-// bit.  The wrapped positions equal the positions (every wrap is zero).
+// bit.  The passes read the positions themselves (every wrap is zero).
 // The identity policy reduces to t != s (full list) or t > s (half list),
 // and include_self keeps t == s.  A work unit holds bgroup consecutive
 // sources, bgroup x chunks <= kMolUnitWork (chunk c: targets 64 c .. 64 c +
@@ -642,10 +642,14 @@ __device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const Stru
     const T cut2 = (T)r.cut2;
     T sx = 0, sy = 0, sz = 0;  // lane g: source f + g
     if (lane < G) {
-        const Vec4<T> q = a.atom_q[a0 + f + lane];
-        sx = q.x;
-        sy = q.y;
-        sz = q.z;
+        const int64_t i = 3 * (int64_t)(a0 + f + lane);
+        sx = a.pos[i];
+        sy = a.pos[i + 1];
+        sz = a.pos[i + 2];
+        // every atom is a source of one unit: the check of the atom pass,
+        // which a request planned by k_molecule_setup does not run
+        if (!(isfinite((double)sx) && isfinite((double)sy) && isfinite((double)sz)))
+            atomicOr(a.status + SS_FLAGS, ST_POS_NONFINITE);
     }
     int cnt = 0;  // lane g: pairs of source f + g
     for (int c0 = 0; c0 < nch; c0 += kMolPass) {
@@ -657,10 +661,10 @@ __device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const Stru
             const int t = (c0 + j) * kWave + lane;
             tx[j] = ty[j] = tz[j] = (T)__builtin_inf();
             if (j < np && t < n) {
-                const Vec4<T> q = a.atom_q[a0 + t];
-                tx[j] = q.x;
-                ty[j] = q.y;
-                tz[j] = q.z;
+                const int64_t i = 3 * (int64_t)(a0 + t);
+                tx[j] = a.pos[i];
+                ty[j] = a.pos[i + 1];
+                tz[j] = a.pos[i + 2];
             }
         });
         for (int g = 0; g < G; ++g) {

@@ -180,7 +180,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         s_mcarry = 0;
     }
     __syncthreads();
-    unsigned long long flags = 0, plan = 0, images = 0, wrap = 0;
+    unsigned long long flags = 0, plan = 0, images = 0, wrap = 0, nonmol = 0;
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
         long long v[kScanItems], u[kScanItems], m[kScanItems];
@@ -193,7 +193,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
             const StructRec& r = recs[ic];
             const long long bv = struct_bins[ic], uv = struct_units[ic];
             const unsigned long long fl = r.flags;
-            const int algo = r.algo, aw = r.any_wrap;
+            const int algo = r.algo, aw = r.any_wrap, active = r.active;
             const long long img = r.img_total, na = r.natoms;
             v[k] = in ? bv : 0;
             u[k] = in ? uv : 0;
@@ -205,6 +205,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
                 flags |= fl;
                 plan |= algo == ALGO_CELL ? 2ull : (algo == ALGO_BRUTE ? 1ull : 0ull);
                 if (algo == ALGO_CELL && aw) wrap = 1;
+                if (algo == ALGO_BRUTE && !molecule_path(active, na)) nonmol = 1;
                 images += (unsigned long long)img;
             }
         }
@@ -239,6 +240,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         flags |= __shfl_xor(flags, d);
         plan |= __shfl_xor(plan, d);
         wrap |= __shfl_xor(wrap, d);
+        nonmol |= __shfl_xor(nonmol, d);
         images += __shfl_xor(images, d);
     }
     const int w = threadIdx.x / kWave;
@@ -246,7 +248,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         s_red[0][w] = flags;
         s_red[1][w] = plan;
         s_red[2][w] = images;
-        s_red[3][w] = wrap;
+        s_red[3][w] = wrap | (nonmol << 1);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -263,9 +265,10 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
         unit_off[nb] = s_ucarry;
         status[SS_TOTAL_BINS] = (unsigned long long)total;
         status[SS_TOTAL_UNITS] = (unsigned long long)s_ucarry;
-        status[SS_PLAN] = all_plan;
+        status[SS_PLAN] =
+            all_plan | ((all_plan & 1ull) && !(all_wrap & 2ull) ? kPlanMolecules : 0ull);
         status[SS_TOTAL_IMAGES] = all_images;
-        status[SS_ANY_WRAP] = all_wrap;
+        status[SS_ANY_WRAP] = all_wrap & 1ull;
         unsigned long long st = all_flags;
         if (total > cap_bins) st |= ST_CAPACITY;
         if (all_images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;

@@ -249,20 +249,33 @@ static void dispatch_queries(const tnr_request* req, const Layout& L, const Quer
 // The count pipeline.  Its last kernel copies the status words into
 // host_out (a device-visible pointer to the caller's pinned buffer) when
 // given.
-// brute_hint: the caller expects no cell-list structure (an earlier count
-// of the same request shape planned brute force only), so the cell-list
-// kernels are not launched; the planner raises ST_PLAN_HINT if a structure
-// is planned as a cell list after all.
+// Plan hints of a count (from an earlier count of the same request shape):
+//   HINT_BRUTE      no cell-list structure: the cell-list kernels are not
+//                   launched, and the planner raises ST_PLAN_HINT if a
+//                   structure is planned as a cell list after all;
+//   HINT_MOLECULES  every structure a molecule: k_molecule_setup and
+//                   k_struct_scan are the whole prologue (ST_PLAN_HINT for
+//                   any other structure).
+enum CountHint : int { HINT_NONE = 0, HINT_BRUTE = 1, HINT_MOLECULES = 2 };
+
 template <typename T>
 static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
-                            hipStream_t stream, long long* host_out, bool brute_hint) {
-    const bool cell_kernels = req->algorithm != TNR_BRUTE_FORCE && !brute_hint;
+                            hipStream_t stream, long long* host_out, int hint) {
+    const bool brute_hint = hint == HINT_BRUTE;
+    const bool cell_kernels = req->algorithm != TNR_BRUTE_FORCE && hint == HINT_NONE;
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
     const int reach = req->stencil_reach;  // 0: chosen per structure
     const int64_t n_tiles =
         (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) + L.n_tiles_pairs;
-    if (nb == 1 && n > 0) {
+    if (hint == HINT_MOLECULES) {
+        k_molecule_setup<T><<<blocks_for(nb, 64), 64, 0, stream>>>(
+            req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, req->algorithm,
+            v.recs, v.struct_bins, v.struct_units, v.status, v.tiles_pairs, L.n_tiles_pairs);
+        k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb, n,
+                                                v.struct_bin_off, v.struct_unit_off, v.recs,
+                                                v.status, L.cap_bins, 0);
+    } else if (nb == 1 && n > 0) {
         // one structure: set-up and atoms, then plan and binning, in two
         // launches; k_single_bin writes the status words
         k_atoms<T, true><<<blocks_for(n), kBlock, 0, stream>>>(
@@ -739,11 +752,20 @@ int tnr_count_async_hinted(const tnr_request* req, void* workspace, size_t works
         mapped = nullptr;
         (void)hipGetLastError();
     }
-    const bool brute_hint = plan_hint == 1 && req->algorithm == TNR_AUTO;
+    // a hint of brute force only (plan bits 0-1 equal to 1) from an earlier
+    // count; with bit 2 every structure was a molecule
+    int hint = tnr::HINT_NONE;
+    if (plan_hint >= 0 && (plan_hint & (int64_t)tnr::kPlanFamilies) == 1 && req->n_structures > 0 &&
+        (req->algorithm == TNR_AUTO || req->algorithm == TNR_BRUTE_FORCE)) {
+        if (plan_hint & (int64_t)tnr::kPlanMolecules)
+            hint = tnr::HINT_MOLECULES;
+        else if (req->algorithm == TNR_AUTO)
+            hint = tnr::HINT_BRUTE;
+    }
     hipError_t e =
         req->dtype == TNR_FLOAT32
-            ? tnr::run_count<float>(req, workspace, L, s, (long long*)mapped, brute_hint)
-            : tnr::run_count<double>(req, workspace, L, s, (long long*)mapped, brute_hint);
+            ? tnr::run_count<float>(req, workspace, L, s, (long long*)mapped, hint)
+            : tnr::run_count<double>(req, workspace, L, s, (long long*)mapped, hint);
     if (e == hipSuccess && !mapped) {
         const tnr::Views v = tnr::views(workspace, L);
         e = hipMemcpyAsync(host_result, v.status, TNR_HOST_RESULT_SLOTS * sizeof(int64_t),
