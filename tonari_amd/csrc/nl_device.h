@@ -144,13 +144,23 @@ struct alignas(16) BlockPartial {
     unsigned long long flags;
 };
 
+// What the batch scan of the plans reads of a structure's record, in one
+// 32-byte line per structure (records are several hundred bytes apart).
+// Written by whoever plans the structure, right after its record.
+struct alignas(32) PlanSummary {
+    unsigned long long flags;
+    long long img_total;
+    long long natoms;
+    long long kind;  // algo | any_wrap << 8 | molecule << 9
+};
+
 // Workspace layout.  Sub-buffers are 256-byte aligned from a 256-byte
 // aligned base.  Depends only on N, B and the scalar size.
 struct Layout {
     size_t status, structs, struct_bins, struct_bin_off, struct_units, struct_unit_off,
         atom_struct, atom_wrap, atom_q, binned_w, binned_p,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets,
-        block_partials, masks, tiles_bins, tiles_pairs, total;
+        block_partials, masks, tiles_bins, tiles_pairs, struct_meta, total;
     int64_t cap_bins, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
 };
 
@@ -216,6 +226,7 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.n_tiles_pairs = (n + kScanTile - 1) / kScanTile + 1;
     L.tiles_bins = take(sizeof(unsigned long long) * (size_t)L.n_tiles_bins);
     L.tiles_pairs = take(sizeof(unsigned long long) * (size_t)L.n_tiles_pairs);
+    L.struct_meta = take(sizeof(PlanSummary) * (size_t)(b + 1));
     L.total = o;
     return L;
 }

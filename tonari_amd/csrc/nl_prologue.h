@@ -829,7 +829,7 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
                                                   long long* struct_bins, long long* bin_off,
                                                   long long* struct_units, long long* unit_off,
                                                   int64_t cap_bins, unsigned long long* status,
-                                                  int fused_scan) {
+                                                  int fused_scan, PlanSummary* meta) {
     using K = RedKeys<T>;
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
     const int64_t b = blockIdx.x;
@@ -880,24 +880,28 @@ __global__ __launch_bounds__(kBlock) void k_plan(const T* cells, int64_t nb, int
                                   struct_units);
             }
         }
+        // thread 0 wrote the record's plan (or k_setup did, for an aborted
+        // structure), so it reads it back in program order
+        if (tid == 0) write_summary(meta + b, recs[b]);
     }
     if (fused_scan) {
         __syncthreads();
-        struct_scan_block(struct_bins, struct_units, nb, n_atoms, bin_off, unit_off, recs,
-                          status, cap_bins, 0);
+        struct_scan_block(struct_bins, struct_units, meta, nb, n_atoms, bin_off, unit_off,
+                          recs, status, cap_bins, 0);
     }
 }
 
 // The batch-wide step of the planner (one workgroup, after k_plan).
 __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_bins,
                                                          const long long* struct_units,
+                                                         const PlanSummary* meta,
                                                          int64_t nb, int64_t n_atoms,
                                                          long long* bin_off, long long* unit_off,
                                                          StructRec* recs,
                                                          unsigned long long* status,
                                                          int64_t cap_bins, int brute_hint) {
-    struct_scan_block(struct_bins, struct_units, nb, n_atoms, bin_off, unit_off, recs, status,
-                      cap_bins, brute_hint);
+    struct_scan_block(struct_bins, struct_units, meta, nb, n_atoms, bin_off, unit_off, recs,
+                      status, cap_bins, brute_hint);
 }
 
 // The set-up and plan of a request whose structures are all molecules (a
@@ -912,8 +916,9 @@ template <typename T>
 __global__ void k_molecule_setup(const int64_t* bp, const T* cells, const uint8_t* pbc,
                                  int64_t nb, int64_t n_atoms, double cutoff, int requested,
                                  StructRec* recs, long long* struct_bins,
-                                 long long* struct_units, unsigned long long* status,
-                                 unsigned long long* tiles, int64_t n_tiles) {
+                                 long long* struct_units, PlanSummary* meta,
+                                 unsigned long long* status, unsigned long long* tiles,
+                                 int64_t n_tiles) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
@@ -948,6 +953,7 @@ __global__ void k_molecule_setup(const int64_t* bp, const T* cells, const uint8_
     }
     struct_bins[b] = 0;
     struct_units[b] = units;
+    write_summary(meta + b, r);
 }
 
 template <typename T>

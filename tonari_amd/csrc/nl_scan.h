@@ -156,18 +156,30 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     }
 }
 
-// One workgroup: exclusive scans of the bins and of the brute-force work
-// units per structure into bin_off and unit_off ([0..nb]; each structure's
-// first bin and unit also go to its record), of the brute-force atoms
-// (each brute-force structure's hit-mask slots, counted down from n_atoms,
-// go to its record),
-// their totals, and the batch checks that need every structure's plan:
-// total periodic images, bin capacity and, for a count launched without the
-// cell-list kernels (brute_hint), the absence of cell-list structures.
-// Every load of a chunk is issued at once (indices clamped to the last
-// structure, values masked), and the batch reductions go through wave
-// reductions and one LDS slot per wave, without atomics.
+// The summary of record r for the batch scan.
+__device__ __forceinline__ void write_summary(PlanSummary* s, const StructRec& r) {
+    PlanSummary x;
+    x.flags = r.flags;
+    x.img_total = r.img_total;
+    x.natoms = r.natoms;
+    x.kind = (long long)r.algo | (r.any_wrap ? 1ll << 8 : 0ll) |
+             (molecule_path(r.active, r.natoms) ? 1ll << 9 : 0ll);
+    *s = x;
+}
+
+// One workgroup, from the plans' summaries (meta): exclusive scans of the
+// bins and of the brute-force work units per structure into bin_off and
+// unit_off ([0..nb]; each structure's first bin and unit also go to its
+// record), of the brute-force atoms (each brute-force structure's hit-mask
+// slots, counted down from n_atoms, go to its record), their totals, and
+// the batch checks that need every structure's plan: total periodic images,
+// bin capacity and, for a count launched without the cell-list kernels
+// (brute_hint), the absence of cell-list structures.  Every load of a chunk
+// is issued at once (indices clamped to the last structure, values masked),
+// and the batch reductions go through wave reductions and one LDS slot per
+// wave, without atomics.
 __device__ void struct_scan_block(const long long* struct_bins, const long long* struct_units,
+                                  const PlanSummary* meta,
                                   int64_t nb, int64_t n_atoms, long long* bin_off,
                                   long long* unit_off, StructRec* recs,
                                   unsigned long long* status, int64_t cap_bins,
@@ -190,11 +202,12 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
             const int64_t i = i0 + k;
             const bool in = i < nb;
             const int64_t ic = in ? i : nb - 1;
-            const StructRec& r = recs[ic];
+            const PlanSummary sm = meta[ic];
             const long long bv = struct_bins[ic], uv = struct_units[ic];
-            const unsigned long long fl = r.flags;
-            const int algo = r.algo, aw = r.any_wrap, active = r.active;
-            const long long img = r.img_total, na = r.natoms;
+            const unsigned long long fl = sm.flags;
+            const int algo = (int)(sm.kind & 0xff);
+            const bool aw = (sm.kind >> 8) & 1, mol = (sm.kind >> 9) & 1;
+            const long long img = sm.img_total, na = sm.natoms;
             v[k] = in ? bv : 0;
             u[k] = in ? uv : 0;
             m[k] = in && algo == ALGO_BRUTE ? na : 0;
@@ -205,7 +218,7 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
                 flags |= fl;
                 plan |= algo == ALGO_CELL ? 2ull : (algo == ALGO_BRUTE ? 1ull : 0ull);
                 if (algo == ALGO_CELL && aw) wrap = 1;
-                if (algo == ALGO_BRUTE && !molecule_path(active, na)) nonmol = 1;
+                if (algo == ALGO_BRUTE && !mol) nonmol = 1;
                 images += (unsigned long long)img;
             }
         }

@@ -83,6 +83,7 @@ struct Views {
     unsigned long long* masks;
     unsigned long long* tiles_bins;
     unsigned long long* tiles_pairs;
+    PlanSummary* struct_meta;
 };
 
 static Views views(void* ws, const Layout& L) {
@@ -110,6 +111,7 @@ static Views views(void* ws, const Layout& L) {
     v.masks = (unsigned long long*)(base + L.masks);
     v.tiles_bins = (unsigned long long*)(base + L.tiles_bins);
     v.tiles_pairs = (unsigned long long*)(base + L.tiles_pairs);
+    v.struct_meta = (PlanSummary*)(base + L.struct_meta);
     return v;
 }
 
@@ -271,10 +273,11 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     if (hint == HINT_MOLECULES) {
         k_molecule_setup<T><<<blocks_for(nb, 64), 64, 0, stream>>>(
             req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, req->algorithm,
-            v.recs, v.struct_bins, v.struct_units, v.status, v.tiles_pairs, L.n_tiles_pairs);
-        k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb, n,
-                                                v.struct_bin_off, v.struct_unit_off, v.recs,
-                                                v.status, L.cap_bins, 0);
+            v.recs, v.struct_bins, v.struct_units, v.struct_meta, v.status, v.tiles_pairs,
+            L.n_tiles_pairs);
+        k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, v.struct_meta,
+                                                nb, n, v.struct_bin_off, v.struct_unit_off,
+                                                v.recs, v.status, L.cap_bins, 0);
     } else if (nb == 1 && n > 0) {
         // one structure: set-up and atoms, then plan and binning, in two
         // launches; k_single_bin writes the status words
@@ -303,11 +306,11 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_plan<T><<<(unsigned)(nb > 0 ? nb : 1), kBlock, 0, stream>>>(
             (const T*)req->cell, nb, n, req->cutoff, req->algorithm, reach, v.recs,
             v.block_partials, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
-            L.cap_bins, v.status, fused_scan);
+            L.cap_bins, v.status, fused_scan, v.struct_meta);
         if (!fused_scan)
-            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, nb, n,
-                                                    v.struct_bin_off, v.struct_unit_off, v.recs,
-                                                    v.status, L.cap_bins, brute_hint ? 1 : 0);
+            k_struct_scan<<<1, kBlock, 0, stream>>>(
+                v.struct_bins, v.struct_units, v.struct_meta, nb, n, v.struct_bin_off,
+                v.struct_unit_off, v.recs, v.status, L.cap_bins, brute_hint ? 1 : 0);
         if (n > 0 && cell_kernels)
             k_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(n, v.recs, v.atom_struct,
                                                            (const Vec4<T>*)v.atom_q, v.atom_bin,
