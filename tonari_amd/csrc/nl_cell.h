@@ -103,6 +103,7 @@ struct CellBin {
     T outer2, inner2, cut2;
     bool wrapped, diagonal;
     bool shiftcheck;  // wrapped, and R + 2 max|wrap| may exceed int32: check kept shifts
+    bool kwpack;      // wrapped, and every k - w_t packs (max_a R_a + max|wrap| <= 511)
 };
 
 // Geometry of the stencil of one bin, decoded from its structure record.
@@ -209,11 +210,11 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wv = tid / kWave;
+    // the bin's sources load with the structure search
+    const int sb_raw = a.bin_start[g], se_raw = a.bin_start[g + 1];
     cb.b = structure_of_item(a.struct_bin_off, a.nb, g, sc);
     const StructRec& r = a.recs[cb.b];
     const unsigned lbin = (unsigned)(g - r.bin0);  // bins of a structure fit in 32 bits
-    // the bin's sources and the piece bounds below load in one round trip
-    const int sb_raw = a.bin_start[g], se_raw = a.bin_start[g + 1];
     const T* cell = a.cells + 9 * cb.b;
 #pragma unroll
     for (int e = 0; e < 9; ++e) cb.c[e] = cell[e];
@@ -225,6 +226,8 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     // structure can leave int32 unless that bound does
     cb.shiftcheck = cb.wrapped && (double)max(max(r.reps[0], r.reps[1]), r.reps[2]) +
                                          2.0 * (double)r.maxw >= 2147483647.0;
+    cb.kwpack = cb.wrapped && (double)max(max(r.reps[0], r.reps[1]), r.reps[2]) +
+                                      (double)r.maxw <= 511.0;
     cb.diagonal = r.diagonal != 0;
     cb.by_bin = a.by_bin && (load_status(a.status + SS_PLAN) & kPlanFamilies) == 2ull;
     const BinGeom G = bin_geom(r, lbin);
@@ -325,6 +328,79 @@ __device__ __forceinline__ void stage_candidates(const QueryArgs<T>& a, const St
     for (int k = 0; k < NS; ++k) {
         const int v = tid + k * kBlock;
         if (v < C) cand[v] = rec[k];
+    }
+    __syncthreads();
+}
+
+// Staged candidates of a wrapped structure: the original position, the atom
+// index and the image shift k of the candidate's piece minus its wraps w_t,
+// packed (pack_k).  Float64 keeps the index in the low and k - w_t in the
+// high half of the fourth word; float32 keeps the index in the fourth word
+// and k - w_t in an array behind WrapStageCap<float> records, inside the
+// same staging area.  Taken when max_a R_a + max|w| <= 511 (every k - w_t
+// packs).
+template <typename T>
+struct WrapStageCap;
+template <>
+struct WrapStageCap<float> {
+    static constexpr int value = 512;
+};
+template <>
+struct WrapStageCap<double> {
+    static constexpr int value = 1280;
+};
+static_assert(WrapStageCap<float>::value * (16 + 4) <= EmitStageCap<float>::value * 16 &&
+                  WrapStageCap<double>::value <= EmitStageCap<double>::value,
+              "the wrapped staging fits the staging area");
+
+__device__ __forceinline__ void wstage_put(Vec4<float>* cand, int v, const Vec4<float>& p,
+                                           int kw) {
+    cand[v] = p;
+    reinterpret_cast<int*>(cand + WrapStageCap<float>::value)[v] = kw;
+}
+__device__ __forceinline__ void wstage_put(Vec4<double>* cand, int v, Vec4<double> p, int kw) {
+    p.w = __hiloint2double(kw, as_idx(p.w));
+    cand[v] = p;
+}
+__device__ __forceinline__ int wstage_kw(const Vec4<float>* cand, int v, const Vec4<float>&) {
+    return reinterpret_cast<const int*>(cand + WrapStageCap<float>::value)[v];
+}
+__device__ __forceinline__ int wstage_kw(const Vec4<double>*, int, const Vec4<double>& rec) {
+    return __double2hiint(rec.w);
+}
+__device__ __forceinline__ int wstage_idx(const Vec4<float>& rec) { return as_idx(rec.w); }
+__device__ __forceinline__ int wstage_idx(const Vec4<double>& rec) {
+    return __double2loint(rec.w);
+}
+
+// Stages the C <= WrapStageCap<T> candidates of a wrapped structure (every
+// thread calls it; ends with a workgroup barrier): original positions (whose
+// fourth word holds the atom index) and wraps in binned order.
+template <typename T>
+__device__ __forceinline__ void stage_wrapped(const QueryArgs<T>& a, const StencilLds& st, int C,
+                                              Vec4<T>* cand) {
+    constexpr int NS = WrapStageCap<T>::value / kBlock;
+    static_assert(WrapStageCap<T>::value % kBlock == 0, "whole rounds");
+    const int tid = threadIdx.x;
+    Vec4<T> rp[NS];
+    int4 rw[NS];
+    int kk[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const int v0 = tid + k * kBlock;
+        const int v = v0 < C ? v0 : 0;
+        const int p = st.piece[v];
+        const int at = v + st.delta[p];
+        kk[k] = st.kid[p];
+        rp[k] = a.binned_p[at];
+        rw[k] = a.binned_w[at];
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const int v = tid + k * kBlock;
+        int kx, ky, kz;
+        unpack_k(kk[k], kx, ky, kz);
+        if (v < C) wstage_put(cand, v, rp[k], pack_k(kx - rw[k].x, ky - rw[k].y, kz - rw[k].z));
     }
     __syncthreads();
 }
@@ -530,10 +606,12 @@ __device__ __forceinline__ void cell_slow(const QueryArgs<T>& a, const ST& st,
 // a time, lane (s, j) holding the mask of chunk j of source s; a wave scan of
 // the mask popcounts places every hit in the wave's LDS list (entry = owner
 // lane << 6 | bit), which is written out in rounds of 64 consecutive pairs.
-// With STAGED the candidate records come from LDS; without WRAPPED the
-// source and target positions are the records themselves.  Both together
-// leave a round with no global load, so the pair stores stream without
-// waits (a wait for a load also waits for every earlier store).
+// With STAGED the candidates come from LDS: the records (unwrapped) or the
+// wrapped staging (stage_wrapped), so that a round holds no global load and
+// the pair stores stream without waits (a wait for a load also waits for
+// every earlier store).  With WRAPPED and not STAGED each candidate's
+// original position (carrying its index) and wraps are loaded in binned
+// order.
 template <typename T, bool STAGED, bool WRAPPED>
 __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds& st,
                                          const Vec4<T>* cand, const CellBin<T>& cb,
@@ -610,12 +688,18 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                     x.tg = __shfl(tag, x.e >> 6);
                     if (r < L) {
                         const int v = chunk_cand(x.tg & 63, x.e & 63, nch);
-                        const int p = st.piece[v];
-                        x.kk = st.kid[p];
-                        x.rec = cand_record<T, STAGED>(a, st, cand, p, v);
-                        if (WRAPPED) {
-                            x.rw = a.binned_w[v + st.delta[p]];
-                            x.rp = a.binned_p[v + st.delta[p]];
+                        if (STAGED && WRAPPED) {
+                            x.rp = cand[v];
+                            x.kk = wstage_kw(cand, v, x.rp);
+                        } else {
+                            const int p = st.piece[v];
+                            x.kk = st.kid[p];
+                            if (WRAPPED) {
+                                x.rw = a.binned_w[v + st.delta[p]];
+                                x.rp = a.binned_p[v + st.delta[p]];
+                            } else {
+                                x.rec = cand_record<T, STAGED>(a, st, cand, p, v);
+                            }
                         }
                     }
                     return x;
@@ -632,9 +716,19 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
                         const int4 ws = make_int4(__shfl(sw.x, g), __shfl(sw.y, g),
                                                   __shfl(sw.z, g), 0);
                         const T pt[3] = {cur.rp.x, cur.rp.y, cur.rp.z};
-                        if (r0 + lane < L)
-                            cell_write_regs<T>(a, o, si, as_idx(cur.rec.w), cur.kk, ps, pt, ws,
-                                               cur.rw, cb);
+                        if (r0 + lane < L) {
+                            if (STAGED) {
+                                // kk holds k - w_t: S = kk + w_s
+                                int kx, ky, kz;
+                                unpack_k(cur.kk, kx, ky, kz);
+                                write_hit(a, o, si, wstage_idx(cur.rp), shift_i32(kx, 0, ws.x),
+                                          shift_i32(ky, 0, ws.y), shift_i32(kz, 0, ws.z), ps, pt,
+                                          cb.c, cb.diagonal);
+                            } else {
+                                cell_write_regs<T>(a, o, si, as_idx(cur.rp.w), cur.kk, ps, pt,
+                                                   ws, cur.rw, cb);
+                            }
+                        }
                     } else {
                         const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                         if (r0 + lane < L)
@@ -675,12 +769,13 @@ __device__ __forceinline__ int64_t off32_limit(const QueryArgs<T>& a) {
 // evaluates D with the public formula's operation order.  Each source's output range
 // [offsets[s], offsets[s] + hits) is checked against E once; a source that
 // does not fit raises ST_OUTPUT_RANGE and writes nothing.
-template <typename T, bool OFF32>
+template <typename T, bool OFF32, bool WRAPPED>
 __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLds& st,
                                           const Vec4<T>* cand,
                                           const CellBin<T>& cb, unsigned short* list,
-                                          const Vec4<T>& src_all, long long cur_all,
-                                          unsigned long long m_pre0, unsigned long long m_pre1) {
+                                          const Vec4<T>& src_all, const int4& sw_all,
+                                          long long cur_all, unsigned long long m_pre0,
+                                          unsigned long long m_pre1) {
     using O = Ops<T>;
     const int lane = lane_id();
     const Vec4<T> zero4 = {T(0), T(0), T(0), T(0)};
@@ -708,6 +803,12 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
         sq.z = __shfl(src_all.z, from);
         sq.w = __shfl(src_all.w, from);
         const int sidx = as_idx(sq.w);
+        int4 sw = make_int4(0, 0, 0, 0);
+        if (WRAPPED) {
+            sw.x = __shfl(sw_all.x, from);
+            sw.y = __shfl(sw_all.y, from);
+            sw.z = __shfl(sw_all.z, from);
+        }
         const long long cur = __shfl(cur_all, from);
         {
             const int s0 = 0;
@@ -784,13 +885,22 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                     g_ = (int)(e_ >> vb);
                     const int v = (int)(e_ & vmask);
                     rec_ = cand[v];
-                    unpack_k(st.kid[st.piece[v]], k_.x, k_.y, k_.z);
+                    if (WRAPPED)
+                        unpack_k(wstage_kw(cand, v, rec_), k_.x, k_.y, k_.z);  // k - w_t
+                    else
+                        unpack_k(st.kid[st.piece[v]], k_.x, k_.y, k_.z);
                 };
                 // pair r0 + lane of the list; byte offsets of output o in 32
                 // bits when OFF32 (every offset below 2^32)
-                auto put = [&](int r0, int g, const Vec4<T>& rec, const int4& k) {
+                auto put = [&](int r0, int g, const Vec4<T>& rec, int4 k) {
                     const T sx = __shfl(sq.x, g), sy = __shfl(sq.y, g), sz = __shfl(sq.z, g);
                     const int si = __shfl(sidx, g);
+                    if (WRAPPED) {
+                        // S = (k - w_t) + w_s
+                        k.x = shift_i32(k.x, 0, __shfl(sw.x, g));
+                        k.y = shift_i32(k.y, 0, __shfl(sw.y, g));
+                        k.z = shift_i32(k.z, 0, __shfl(sw.z, g));
+                    }
                     long long o;
                     if constexpr (OFF32)
                         o = (long long)(unsigned)(__shfl(ob32, g) + (unsigned)(base + r0 + lane));
@@ -811,7 +921,7 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
                                                         (size_t)o * width);
                     };
                     if (r0 + lane >= L) return;
-                    const int t = as_idx(rec.w);
+                    const int t = WRAPPED ? wstage_idx(rec) : as_idx(rec.w);
                     if (a.pairs) {
                         long2 v;
                         v.x = (long long)(unsigned)si;
@@ -877,68 +987,122 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
     }
 }
 
-// Static XCD-aware split of W work items over the workgroups of a grid:
-// workgroup b runs on XCD b % 8 (the hardware deals workgroups round-robin),
-// items are cut into 8 contiguous ranges and the workgroups of XCD x stride
-// over range x, so neighbouring bins share one L2.
+// XCD-aware deal of work items: workgroup b runs on XCD b % 8 (the hardware
+// deals workgroups round-robin).  Items go to the XCDs in chunks of K
+// consecutive items, chunk c to XCD c % 8, so the bins of one region mostly
+// share an L2 while a region of heavy bins (a dense, skewed or large
+// structure of a batch) spreads over every XCD instead of holding up one.
+constexpr int64_t kXcdChunk = 64;
+
+// Chunk length for n items: kXcdChunk, or n / 8 rounded up for fewer than
+// 8 kXcdChunk items (so that a grid of 8 ceil(n / 8) workgroups covers them).
+__device__ __host__ __forceinline__ int64_t xcd_chunk(int64_t n) {
+    return n >= 8 * kXcdChunk ? kXcdChunk : (n + 7) / 8 > 0 ? (n + 7) / 8 : 1;
+}
+// Items of XCD x among W, in chunks of K.
+__device__ __forceinline__ int64_t xcd_items(int64_t W, int64_t K, int64_t x) {
+    const int64_t nc = W / K, rem = W - nc * K;
+    const int64_t full = nc / 8 + (x < nc % 8 ? 1 : 0);
+    return full * K + (x == nc % 8 ? rem : 0);
+}
+// The j-th item of XCD x, in chunks of K.
+__device__ __forceinline__ int64_t xcd_item(int64_t x, int64_t j, int64_t K) {
+    const int64_t c = j / K;
+    return (c * 8 + x) * K + (j - c * K);
+}
+
+// The items of the calling workgroup: j = first, first + step, ... < end,
+// item(j) the j-th.  A grid whose size is not a multiple of 8 strides over
+// the items in order.
 struct ItemRange {
-    int64_t first, end, step;
+    int64_t x, first, end, step, K;
+    bool dealt;
+    __device__ __forceinline__ int64_t item(int64_t j) const {
+        return dealt ? xcd_item(x, j, K) : j;
+    }
 };
-__device__ __forceinline__ ItemRange xcd_block_range(int64_t W) {
+// W items, chunks of K (xcd_chunk of the count the grid was sized for).
+__device__ __forceinline__ ItemRange xcd_block_range(int64_t W, int64_t K) {
     const unsigned nblk = gridDim.x;
     ItemRange r;
+    r.K = K;
     if ((nblk & 7u) != 0) {
+        r.dealt = false;
+        r.x = 0;
         r.first = blockIdx.x;
         r.end = W;
         r.step = nblk;
         return r;
     }
-    const int64_t per = (W + 7) / 8;
-    const int64_t x = blockIdx.x & 7u;
-    r.first = x * per + (int64_t)(blockIdx.x >> 3);
-    r.end = min(W, (x + 1) * per);
+    r.dealt = true;
+    r.x = blockIdx.x & 7u;
+    r.first = (int64_t)(blockIdx.x >> 3);
+    r.end = xcd_items(W, K, r.x);
     r.step = (int64_t)(nblk >> 3);
     return r;
 }
 
 static_assert(kMapCap == kMaskWords * kWave, "one mask word per chunk of the piece map");
 
-// Emitting pass for one bin whose stencil block_bin has built: the fast
-// path (staged candidates, no wrapped representative, at most 64 sources),
-// the decode path (emit_bin) or, beyond the piece map, the slow path.
+// Emitting pass for one bin with staged candidates: the fast path (at most
+// 64 sources) or the decode path.  WRAPPED: the wrapped staging
+// (stage_wrapped), and the sources' original positions and wraps.
+template <typename T, bool WRAPPED>
+__device__ __forceinline__ void emit_staged(const QueryArgs<T>& a, StencilLds& s_st,
+                                            Vec4<T>* s_cand, unsigned short* list,
+                                            CellBin<T>& cb, Vec4<T> src_all, int wv, int lane) {
+    const int nsrc = cb.se - cb.sb;
+    const bool fast = nsrc <= kWave;
+    long long cur_all = 0;
+    unsigned long long m0 = 0, m1 = 0;
+    int4 sw_all = make_int4(0, 0, 0, 0);
+    if (fast) {
+        // sources, offsets and the masks of the wave's first two groups load
+        // with the staging
+        if (WRAPPED && lane < nsrc) {
+            src_all = a.binned_p[cb.sb + lane];
+            sw_all = a.binned_w[cb.sb + lane];
+        }
+        cur_all = lane < nsrc ? a.offsets[cb.by_bin ? cb.sb + lane : as_idx(src_all.w)] : 0;
+        const int S = emit_group_size(nsrc, cb.nch);
+        const int sl = (int)(((float)lane + 0.5f) / (float)cb.nch);
+        const int j = lane - sl * cb.nch;
+        const int s0 = wv * S + sl, s1 = (wv + kWavesPerBlock) * S + sl;
+        if (sl < S && s0 < min(nsrc, wv * S + S))
+            m0 = a.masks[(int64_t)(cb.sb + s0) * kMaskWords + j];
+        if (sl < S && s1 < min(nsrc, (wv + kWavesPerBlock) * S + S))
+            m1 = a.masks[(int64_t)(cb.sb + s1) * kMaskWords + j];
+    }
+    if (WRAPPED)
+        stage_wrapped<T>(a, s_st, cb.C, s_cand);
+    else
+        stage_candidates<T, EmitStageCap<T>::value>(a, s_st, cb.C, s_cand);
+    if (fast) {
+        // every output's byte offset below 2^32: 32-bit offsets
+        if (a.limit <= off32_limit(a))
+            emit_fast<T, true, WRAPPED>(a, s_st, s_cand, cb, list, src_all, sw_all, cur_all, m0,
+                                        m1);
+        else
+            emit_fast<T, false, WRAPPED>(a, s_st, s_cand, cb, list, src_all, sw_all, cur_all,
+                                         m0, m1);
+    } else {
+        wave_sources(cb);
+        emit_bin<T, true, WRAPPED>(a, s_st, s_cand, cb, list);
+    }
+}
+
+// Emitting pass for one bin whose stencil block_bin has built: staged
+// candidates (emit_staged), the decode path with candidates loaded from
+// global memory (emit_bin) or, beyond the piece map, the slow path.
 template <typename T, int MODE>
 __device__ __forceinline__ void emit_one_bin(const QueryArgs<T>& a, StencilLds& s_st,
                                              Vec4<T>* s_cand, unsigned short* list,
                                              CellBin<T>& cb, const Vec4<T>& src_all, int wv,
                                              int lane) {
-    if (cb.C <= EmitStageCap<T>::value && !cb.wrapped) {
-        const int nsrc = cb.se - cb.sb;
-        const bool fast = nsrc <= kWave;
-        long long cur_all = 0;
-        unsigned long long m0 = 0, m1 = 0;
-        if (fast) {
-            // offsets and the masks of the wave's first two groups load with the staging
-            cur_all = lane < nsrc ? a.offsets[cb.by_bin ? cb.sb + lane : as_idx(src_all.w)] : 0;
-            const int S = emit_group_size(nsrc, cb.nch);
-            const int sl = (int)(((float)lane + 0.5f) / (float)cb.nch);
-            const int j = lane - sl * cb.nch;
-            const int s0 = wv * S + sl, s1 = (wv + kWavesPerBlock) * S + sl;
-            if (sl < S && s0 < min(nsrc, wv * S + S))
-                m0 = a.masks[(int64_t)(cb.sb + s0) * kMaskWords + j];
-            if (sl < S && s1 < min(nsrc, (wv + kWavesPerBlock) * S + S))
-                m1 = a.masks[(int64_t)(cb.sb + s1) * kMaskWords + j];
-        }
-        stage_candidates<T, EmitStageCap<T>::value>(a, s_st, cb.C, s_cand);
-        if (fast) {
-            // every output's byte offset below 2^32: 32-bit offsets
-            if (a.limit <= off32_limit(a))
-                emit_fast<T, true>(a, s_st, s_cand, cb, list, src_all, cur_all, m0, m1);
-            else
-                emit_fast<T, false>(a, s_st, s_cand, cb, list, src_all, cur_all, m0, m1);
-        } else {
-            wave_sources(cb);
-            emit_bin<T, true, false>(a, s_st, s_cand, cb, list);
-        }
+    if (!cb.wrapped && cb.C <= EmitStageCap<T>::value) {
+        emit_staged<T, false>(a, s_st, s_cand, list, cb, src_all, wv, lane);
+    } else if (cb.kwpack && cb.C <= WrapStageCap<T>::value) {
+        emit_staged<T, true>(a, s_st, s_cand, list, cb, src_all, wv, lane);
     } else if (cb.C <= kMapCap) {
         wave_sources(cb);
         if (cb.wrapped)
@@ -951,8 +1115,8 @@ __device__ __forceinline__ void emit_one_bin(const QueryArgs<T>& a, StencilLds& 
     }
 }
 
-// Emitting pass: one workgroup per bin, mapped XCD-aware (workgroup b runs
-// on XCD b % 8; XCD x takes the x-th eighth of the bins).  The grid is sized
+// Emitting pass: one workgroup per bin, dealt to the XCDs in chunks of bins
+// (xcd_block_range).  The grid is sized
 // for out->n_tasks bins; the kernel reads the batch's bin count from the
 // status words and only trusts the smaller of the two, and it can run again
 // on the same workspace.  STRIDED: the workgroups of a grid of any size
@@ -969,14 +1133,14 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     // the batch's bins from the count's status words; the grid may cover
     // more (a launch sized before the count finished)
     const int64_t bins = (int64_t)load_status(a.status + SS_TOTAL_BINS);
-    const ItemRange br = xcd_block_range(min(a.n_bins, bins));
+    const ItemRange br = xcd_block_range(min(a.n_bins, bins), xcd_chunk(a.n_bins));
     StructCache sc{0, 0, 0};
     const int wv = uniform(threadIdx.x / kWave);
     const int lane = lane_id();
     if constexpr (!STRIDED) {
         // one bin per workgroup (the grid covers the bins)
-        const int64_t g = br.first;
-        if (g >= br.end) return;
+        if (br.first >= br.end) return;
+        const int64_t g = br.item(br.first);
         CellBin<T> cb;
         Vec4<T> src_all;
         if (block_bin<T>(a, g, sc, cb, s_st, &src_all))
@@ -984,7 +1148,8 @@ __global__ __launch_bounds__(kBlock) void k_cell_emit(
     } else {
         // a grid of any size strides over the bins (a launch that does not
         // know the bin count)
-        for (int64_t g = br.first; g < br.end; g += br.step) {
+        for (int64_t j = br.first; j < br.end; j += br.step) {
+            const int64_t g = br.item(j);
             CellBin<T> cb;
             Vec4<T> src_all;
             if (block_bin<T>(a, g, sc, cb, s_st, &src_all))

@@ -67,11 +67,13 @@ template <typename T>
 __device__ __forceinline__ bool wave_bin(const QueryArgs<T>& a, int64_t g, StructCache& sc,
                                          CellBin<T>& cb, WaveStencil<T>& st) {
     const int lane = lane_id();
+    // the bin's sources load with the structure search
+    const int sb_raw = a.bin_start[g], se_raw = a.bin_start[g + 1];
     cb.b = structure_of_item(a.struct_bin_off, a.nb, g, sc);
     const StructRec& r = a.recs[cb.b];
     const unsigned lbin = (unsigned)(g - r.bin0);  // bins of a structure fit in 32 bits
-    cb.sb = uniform(a.bin_start[g]);
-    cb.se = uniform(a.bin_start[g + 1]);
+    cb.sb = uniform(sb_raw);
+    cb.se = uniform(se_raw);
     if (cb.sb >= cb.se) return false;
     const T* cell = a.cells + 9 * cb.b;
 #pragma unroll
@@ -359,10 +361,11 @@ __device__ __forceinline__ void count_wave_bin(const QueryArgs<T>& a, const Wave
 }
 
 // Counting pass, persistent grid of waves.  A task is one of the
-// kCountParts equal parts of a bin's sources; the tasks are cut into 8
-// contiguous ranges, one per XCD (workgroup b runs on XCD b % 8), and the
-// waves of an XCD take its tasks round robin, the four waves of a workgroup
-// four consecutive tasks.  Each task builds its bin's stencil itself.
+// kCountParts equal parts of a bin's sources; the tasks are dealt to the
+// XCDs (workgroup b runs on XCD b % 8) in chunks of kXcdChunk bins' tasks,
+// chunk c to XCD c % 8, and the waves of an XCD take its tasks round robin,
+// the four waves of a workgroup four consecutive tasks.  Each task builds
+// its bin's stencil itself.
 // Writes counts[s] for each source s of a cell-list structure.  The status
 // word is read once: abort bits only come from earlier kernels.
 template <typename T, int MODE>
@@ -374,13 +377,13 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
     const int wv = uniform(threadIdx.x / kWave);
     if (plan & 2) {
         const int64_t W = a.struct_bin_off[a.nb] * kCountParts;
-        const int64_t per = (W + 7) / 8;
+        const int64_t K = kXcdChunk * kCountParts;
         const int64_t x = (int64_t)(blockIdx.x & 7u);
         const int64_t nw = (int64_t)(gridDim.x / 8) * kWavesPerBlock;  // grid: a multiple of 8
-        const int64_t end = min(W, (x + 1) * per);
+        const int64_t end = xcd_items(W, K, x);
         StructCache sc{0, 0, 0};
-        for (int64_t t = x * per + (int64_t)(blockIdx.x >> 3) * kWavesPerBlock + wv; t < end;
-             t += nw) {
+        for (int64_t j = (int64_t)(blockIdx.x >> 3) * kWavesPerBlock + wv; j < end; j += nw) {
+            const int64_t t = xcd_item(x, j, K);
             CellBin<T> cb;
             if (!wave_bin<T>(a, t / kCountParts, sc, cb, s_lds[wv].st)) continue;
             const int part = (int)(t % kCountParts);

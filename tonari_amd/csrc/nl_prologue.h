@@ -1131,12 +1131,14 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
     const int g = atom_bin[i];
     if (g < 0) return;
     const int at = bin_start[g] + atom_rank[i];
-    binned[at] = atom_q[i];
+    const Vec4<T> q = atom_q[i];
+    binned[at] = q;
     if (wrapped) {
         // the emitting pass of a wrapped structure reads each candidate's
-        // wraps and original position at its binned position
+        // wraps and original position (with the atom index of the record) at
+        // its binned position
         binned_w[at] = atom_wrap[i];
-        binned_p[at] = Vec4<T>{pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], T(0)};
+        binned_p[at] = Vec4<T>{pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], q.w};
     }
 }
 

@@ -26,7 +26,7 @@ struct QueryArgs {
     const int* bin_start;
     const Vec4<T>* binned;
     const int4* binned_w;       // wraps in binned order (status SS_ANY_WRAP)
-    const Vec4<T>* binned_p;    // original positions in binned order (likewise)
+    const Vec4<T>* binned_p;    // original positions (and the records' atom index) in binned order
     long long* counts;
     const long long* offsets;
     unsigned long long* status;
@@ -162,18 +162,34 @@ struct StructCache {
     int64_t lo, hi;
 };
 
+// Structure of unit u: the largest b with off[b] <= u, found by the whole
+// wave (every lane with the same u), 64 candidates per step (one load per
+// lane): one round trip for up to 64 structures, two up to 4,096.
+__device__ __forceinline__ int unit_structure(const int64_t* off, int64_t nb, int64_t u) {
+    const int lane = lane_id();
+    int64_t lo = 0, len = nb;
+    while (len > 1) {
+        const int64_t step = (len + kWave - 1) / kWave;
+        const int64_t at = (int64_t)lane * step;
+        const bool le = at < len && off[lo + at] <= u;
+        const unsigned long long m = ballot(le) | 1ull;
+        const int64_t last = 63 - __builtin_clzll(m);
+        lo += last * step;
+        len = min(step, len - last * step);
+    }
+    return (int)lo;
+}
+
+// Structure of item g (the whole wave calls it with the same g): the wave
+// search of unit_structure, unless g lies in the item range cached in sc
+// by the previous call (callers that walk consecutive items).
 __device__ __forceinline__ int structure_of_item(const int64_t* off, int64_t nb, int64_t g,
                                                  StructCache& sc) {
     if (nb == 1) return 0;  // every item belongs to the only structure
     if (g >= sc.lo && g < sc.hi) return sc.b;
-    int64_t lo = 0, hi = nb;
-    while (hi - lo > 1) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (off[mid] <= g) lo = mid; else hi = mid;
-    }
-    sc.b = (int)lo;
-    sc.lo = off[lo];
-    sc.hi = off[lo + 1];
+    sc.b = uniform(unit_structure(off, nb, g));
+    sc.lo = off[sc.b];
+    sc.hi = off[sc.b + 1];
     return sc.b;
 }
 
@@ -364,23 +380,6 @@ __device__ __forceinline__ int pair_images(const QueryArgs<T>& a, const BruteGeo
         }
     }
     return hits;
-}
-
-// Structure of brute-force unit u: the largest b with off[b] <= u, found by
-// the whole wave, 64 candidates per step (one load per lane).
-__device__ __forceinline__ int unit_structure(const int64_t* off, int64_t nb, int64_t u) {
-    const int lane = lane_id();
-    int64_t lo = 0, len = nb;
-    while (len > 1) {
-        const int64_t step = (len + kWave - 1) / kWave;
-        const int64_t at = (int64_t)lane * step;
-        const bool le = at < len && off[lo + at] <= u;
-        const unsigned long long m = ballot(le) | 1ull;
-        const int64_t last = 63 - __builtin_clzll(m);
-        lo += last * step;
-        len = min(step, len - last * step);
-    }
-    return (int)lo;
 }
 
 // Atoms of a structure staged in LDS per wave (structures up to this size).

@@ -155,10 +155,12 @@ static unsigned count_blocks(int64_t work_waves) {
     return (unsigned)(b > 0 ? b : 8);
 }
 
-// Workgroups of the emitting cell-list kernel: one per bin, 8 equal XCD
-// ranges of ceil(bins / 8) bins.
+// Workgroups of the emitting cell-list kernel: one per bin, the bins dealt
+// to the XCDs in chunks of K = xcd_chunk(bins) (every XCD gets the same
+// number of workgroups, enough for its share of whole chunks).
 static unsigned emit_blocks(int64_t bins) {
-    const int64_t b = 8 * ((bins + 7) / 8);
+    const int64_t K = xcd_chunk(bins);
+    const int64_t b = 8 * K * ((bins + 8 * K - 1) / (8 * K));
     return (unsigned)(b > 0 ? b : 8);
 }
 
