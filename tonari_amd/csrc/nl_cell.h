@@ -992,12 +992,18 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
 // consecutive items, chunk c to XCD c % 8, so the bins of one region mostly
 // share an L2 while a region of heavy bins (a dense, skewed or large
 // structure of a batch) spreads over every XCD instead of holding up one.
-constexpr int64_t kXcdChunk = 64;
+// Chunks of bins: 16 for the emitting pass (one workgroup per bin: on C5,
+// 2.83 ms against 3.05 ms at 64 and 3.68 ms at 256), 64 for the counting
+// pass (its waves stride over their XCD's tasks: 1.12 ms against 1.15 ms
+// at 16).
+constexpr int64_t kEmitChunk = 16;
+constexpr int64_t kCountChunk = 64;
 
-// Chunk length for n items: kXcdChunk, or n / 8 rounded up for fewer than
-// 8 kXcdChunk items (so that a grid of 8 ceil(n / 8) workgroups covers them).
+// Chunk length of the emitting pass for n bins: kEmitChunk, or n / 8
+// rounded up for fewer than 8 kEmitChunk bins (so that a grid of
+// 8 ceil(n / 8) workgroups covers them).
 __device__ __host__ __forceinline__ int64_t xcd_chunk(int64_t n) {
-    return n >= 8 * kXcdChunk ? kXcdChunk : (n + 7) / 8 > 0 ? (n + 7) / 8 : 1;
+    return n >= 8 * kEmitChunk ? kEmitChunk : (n + 7) / 8 > 0 ? (n + 7) / 8 : 1;
 }
 // Items of XCD x among W, in chunks of K.
 __device__ __forceinline__ int64_t xcd_items(int64_t W, int64_t K, int64_t x) {
@@ -1052,7 +1058,10 @@ __device__ __forceinline__ void emit_staged(const QueryArgs<T>& a, StencilLds& s
                                             Vec4<T>* s_cand, unsigned short* list,
                                             CellBin<T>& cb, Vec4<T> src_all, int wv, int lane) {
     const int nsrc = cb.se - cb.sb;
-    const bool fast = nsrc <= kWave;
+    // the wrapped fast path needs six more VGPRs than the kernel's other
+    // paths: float32 (seven workgroups per CU, at most 72 VGPRs) leaves it
+    // to the decode path
+    const bool fast = nsrc <= kWave && (!WRAPPED || sizeof(T) == 8);
     long long cur_all = 0;
     unsigned long long m0 = 0, m1 = 0;
     int4 sw_all = make_int4(0, 0, 0, 0);

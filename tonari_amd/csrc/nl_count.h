@@ -362,7 +362,7 @@ __device__ __forceinline__ void count_wave_bin(const QueryArgs<T>& a, const Wave
 
 // Counting pass, persistent grid of waves.  A task is one of the
 // kCountParts equal parts of a bin's sources; the tasks are dealt to the
-// XCDs (workgroup b runs on XCD b % 8) in chunks of kXcdChunk bins' tasks,
+// XCDs (workgroup b runs on XCD b % 8) in chunks of kCountChunk bins' tasks,
 // chunk c to XCD c % 8, and the waves of an XCD take its tasks round robin,
 // the four waves of a workgroup four consecutive tasks.  Each task builds
 // its bin's stencil itself.
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
     const int wv = uniform(threadIdx.x / kWave);
     if (plan & 2) {
         const int64_t W = a.struct_bin_off[a.nb] * kCountParts;
-        const int64_t K = kXcdChunk * kCountParts;
+        const int64_t K = kCountChunk * kCountParts;
         const int64_t x = (int64_t)(blockIdx.x & 7u);
         const int64_t nw = (int64_t)(gridDim.x / 8) * kWavesPerBlock;  // grid: a multiple of 8
         const int64_t end = xcd_items(W, K, x);
