@@ -28,6 +28,7 @@
 namespace tnr {
 
 constexpr int kMapCap = kMaskWords * kWave;  // candidates whose piece is mapped in LDS
+constexpr int kMarkWords = kMapCap / (8 * kBlock);  // 8-byte words of the piece map per thread
 constexpr int kListCap = 512;                // emit: compacted hits per flush
 
 // Stencil of the workgroup's current bin in LDS.
@@ -243,8 +244,10 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     cb.se = uniform(se_raw);
     if (cb.sb >= cb.se) return false;
     // clear the piece marks (the previous bin's users passed a barrier)
-    reinterpret_cast<unsigned long long*>(st.piece)[tid] = 0ull;
-    static_assert(kMapCap == 8 * kBlock, "one 8-byte word of piece marks per thread");
+    static_assert(kMapCap == kMarkWords * 8 * kBlock, "kMarkWords 8-byte words of marks per thread");
+#pragma unroll
+    for (int k = 0; k < kMarkWords; ++k)
+        reinterpret_cast<unsigned long long*>(st.piece)[kMarkWords * tid + k] = 0ull;
     // workgroup exclusive scan of the piece lengths
     const int inc = wave_inclusive_scan_i32(len);
     if (src_pre) {
@@ -280,14 +283,17 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
     // the bin itself with image 0: row (Kx, Ky), the z segment with kz = 0
     cb.dself = st.delta[(G.Kx * G.RY + (G.RY >> 1)) * G.zs + (G.perz ? -G.kz0 : 0)];
     if (cb.C <= kMapCap) {
-        // piece of candidate v: running maximum of the marks up to v, eight
-        // candidates per thread
-        unsigned long long w8 = reinterpret_cast<const unsigned long long*>(st.piece)[tid];
-        int run = 0;
-        int m[8];
+        // piece of candidate v: running maximum of the marks up to v,
+        // 8 kMarkWords consecutive candidates per thread
+        unsigned long long w8[kMarkWords];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            run = max(run, (int)((w8 >> (8 * k)) & 0xffull));
+        for (int k = 0; k < kMarkWords; ++k)
+            w8[k] = reinterpret_cast<const unsigned long long*>(st.piece)[kMarkWords * tid + k];
+        int run = 0;
+        int m[8 * kMarkWords];
+#pragma unroll
+        for (int k = 0; k < 8 * kMarkWords; ++k) {
+            run = max(run, (int)((w8[k / 8] >> (8 * (k % 8))) & 0xffull));
             m[k] = run;
         }
         const int incm = wave_inclusive_max_i32(run);
@@ -299,10 +305,14 @@ __device__ __forceinline__ bool block_bin(const QueryArgs<T>& a, int64_t g, Stru
 #pragma unroll
         for (int w = 0; w < kWavesPerBlock; ++w)
             if (w < wv) carry = max(carry, st.wmax[w]);
-        w8 = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) w8 |= (unsigned long long)max(carry, m[k]) << (8 * k);
-        reinterpret_cast<unsigned long long*>(st.piece)[tid] = w8;
+        for (int k = 0; k < kMarkWords; ++k) {
+            unsigned long long w = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                w |= (unsigned long long)max(carry, m[8 * k + e]) << (8 * e);
+            reinterpret_cast<unsigned long long*>(st.piece)[kMarkWords * tid + k] = w;
+        }
         __syncthreads();
     }
     return true;

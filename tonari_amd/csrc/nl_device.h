@@ -172,17 +172,22 @@ struct Layout {
 // atoms, n), so the two never meet.  A molecule (below) stores its hit masks
 // there, one word per chunk of 64 targets; a periodic structure whose
 // sources are split into k0 slices stores each slice's pair count.
-constexpr int kMaskWords = 32;
+constexpr int kMaskWords = 64;
 
 // Molecules: brute-force structures with no periodic axis and at most
-// kMaskWords * 64 atoms.  They take the hit-mask form of the brute-force
+// kMoleculeCap atoms.  They take the hit-mask form of the brute-force
 // passes (molecule_unit): work units of bgroup consecutive sources, with
 // bgroup x (chunks of 64 targets) at most kMolUnitWork, so that the
 // emitting pass's list of one unit's hits fits its LDS.
+constexpr int kMoleculeCap = 2048;
 constexpr int kMolUnitWork = 28;
 __host__ __device__ inline bool molecule_path(int active, int64_t natoms) {
-    return active == 0 && natoms <= (int64_t)kMaskWords * 64;
+    return active == 0 && natoms <= (int64_t)kMoleculeCap;
 }
+
+// k0 slices of a periodic brute-force structure, at most (each source's
+// slice pair counts fill the first words of its hit-mask slot).
+constexpr int kMaxSlices = 32;
 
 constexpr int64_t kScanItems = 8;
 constexpr int64_t kScanChunk = kBlock * kScanItems;

@@ -802,7 +802,7 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
             if (g < 1.0) {
                 g = 1.0;
                 nsl = (int64_t)fmin(ceil(per_source / want),
-                                    (double)(K0 < kMaskWords ? K0 : kMaskWords));
+                                    (double)(K0 < kMaxSlices ? K0 : kMaxSlices));
                 width = (K0 + nsl - 1) / nsl;
                 nsl = (K0 + width - 1) / width;
             }

@@ -604,7 +604,7 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
 
 // ---------------------------------------------------------------- molecules
 //
-// Brute-force structures with no periodic axis and at most kMaskWords * 64
+// Brute-force structures with no periodic axis and at most kMoleculeCap
 // atoms (molecule_path).  They have one image, k = 0, and no wraps, so the
 // output shift is zero and the public predicate is the whole test: with
 // S = 0 every product S_a * cell_ac of the public formula is a signed zero,
@@ -627,7 +627,8 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
 
 constexpr int kMolPass = 8;                   // chunks per register pass (counting)
 constexpr int kMolList = kMolUnitWork * kWave;  // hits of one unit, at most
-static_assert(kMaskWords * kWave <= 2048, "molecule list entries: 11 bits of target");
+static_assert(kMoleculeCap <= 2048 && kMoleculeCap <= kMaskWords * kWave,
+              "molecule list entries: 11 bits of target; one mask word per chunk");
 
 template <typename T, int MODE>
 __device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const StructRec& r,
