@@ -175,7 +175,7 @@ int tnr_emit(const tnr_request* req, void* workspace, size_t workspace_bytes,
  * tnr_count_finish(host_result) reports errors and E; when E exceeds the
  * capacity, the rows beyond it were not written and the call must be
  * repeated with larger outputs.  Requests whose tnr_workspace_size exceeds
- * 64 MiB (one structure of more than about 176,000 float32 or 156,000
+ * 64 MiB (one structure of more than about 105,000 float32 or 98,000
  * float64 atoms) are rejected with TNR_INPUT_ERROR before any device work.
  * Every call on one GPU uses that GPU's one array: calls that overlap on a
  * GPU (two streams, two threads) race and must be serialised by the caller.
