@@ -39,8 +39,20 @@ struct CountChunks<double> {
 };
 
 // Counting tasks per bin: the bin's sources are split into this many equal
-// parts, one wave each, so the device holds twice as many waves as bins.
-constexpr int kCountParts = 2;
+// parts, one wave each, and each part builds the bin's stencil.  Measured:
+// C4 (float32, bins of about 24 sources) 94 us with two parts against
+// 97.5 us with one; C5 (float64, bins of 12 to 16 sources, a float64
+// stencil costing more to build) 0.66 ms with one against 0.72 ms with two.
+template <typename T>
+struct CountParts;
+template <>
+struct CountParts<float> {
+    static constexpr int value = 2;
+};
+template <>
+struct CountParts<double> {
+    static constexpr int value = 1;
+};
 
 // Stencil tables of one counting wave's bin.
 template <typename T>
@@ -361,7 +373,7 @@ __device__ __forceinline__ void count_wave_bin(const QueryArgs<T>& a, const Wave
 }
 
 // Counting pass, persistent grid of waves.  A task is one of the
-// kCountParts equal parts of a bin's sources; the tasks are dealt to the
+// CountParts<T> equal parts of a bin's sources; the tasks are dealt to the
 // XCDs (workgroup b runs on XCD b % 8) in chunks of kCountChunk bins' tasks,
 // chunk c to XCD c % 8, and the waves of an XCD take its tasks round robin,
 // the four waves of a workgroup four consecutive tasks.  Each task builds
@@ -376,6 +388,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
     const unsigned long long plan = load_status(a.status + SS_PLAN);
     const int wv = uniform(threadIdx.x / kWave);
     if (plan & 2) {
+        constexpr int kCountParts = CountParts<T>::value;
         const int64_t W = a.struct_bin_off[a.nb] * kCountParts;
         const int64_t K = kCountChunk * kCountParts;
         const int64_t x = (int64_t)(blockIdx.x & 7u);
