@@ -19,6 +19,7 @@ namespace tnr {
 __device__ __forceinline__ bool active_pinv(double w[3][3], int k, double dual[3][3]) {
     double v[3][3] = {{1, 0, 0}, {0, 1, 0}, {0, 0, 1}};
     const double eps = 2.220446049250313e-16;
+    bool any_rotation = false;
     for (int sweep = 0; sweep < 64; ++sweep) {
         bool rotated = false;
 #pragma unroll
@@ -35,10 +36,14 @@ __device__ __forceinline__ bool active_pinv(double w[3][3], int k, double dual[3
                 }
                 if (fabs(apq) <= 8 * eps * sqrt(app * aqq)) continue;
                 rotated = true;
+                any_rotation = true;
                 const double zeta = (aqq - app) / (2 * apq);
-                const double t =
-                    zeta == 0.0 ? 1.0 : copysign(1.0, zeta) / (fabs(zeta) + hypot(1.0, zeta));
-                const double cs = 1.0 / hypot(1.0, t);
+                // hypot(1, x) as sqrt(fma(x, x, 1)) (one rounding before the
+                // root) wherever x^2 cannot overflow; |t| <= 1 always
+                const double az = fabs(zeta);
+                const double hz = az < 1e150 ? sqrt(fma(zeta, zeta, 1.0)) : hypot(1.0, zeta);
+                const double t = zeta == 0.0 ? 1.0 : copysign(1.0, zeta) / (az + hz);
+                const double cs = 1.0 / sqrt(fma(t, t, 1.0));
                 const double sn = cs * t;
 #pragma unroll
                 for (int c = 0; c < 3; ++c) {
@@ -67,6 +72,16 @@ __device__ __forceinline__ bool active_pinv(double w[3][3], int k, double dual[3
         }
     }
     if (!(smin > eps * 3 * fmax(smax, 1.0))) return false;
+    if (!any_rotation) {
+        // Orthogonal active rows (a diagonal cell among them): v is the
+        // identity, so every term of the sum below but j = a is a signed
+        // zero and the sum is 0 + w[c][a] / sig2[a], bit for bit.
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+#pragma unroll
+            for (int a = 0; a < 3; ++a) dual[c][a] = a < k ? 0.0 + w[c][a] / sig2[a] : 0.0;
+        return true;
+    }
 #pragma unroll
     for (int c = 0; c < 3; ++c)
 #pragma unroll
@@ -212,7 +227,9 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
             for (int a = 0; a < 3; ++a) {
                 const int64_t f = 2 * rep_axis[a] + 1;
                 if (!(st & ST_IMAGE_CAP)) {
-                    if (count > kImageCap / f)
+                    // count > floor(cap / f) without an integer division
+                    // (count <= 2^24 and f <= 2^32 + 1, so the product fits)
+                    if (count * f > kImageCap)
                         st |= ST_IMAGE_CAP;
                     else
                         count *= f;
@@ -627,7 +644,8 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
     const bool safe = isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Ops<T>::max;
 
     const int64_t nimages = r.nimages;
-    const bool large = r.active != 0 ? n > kAutoBrutePeriodic / nimages : n > kAutoBruteIsolated;
+    // n > floor(limit / nimages), as a product (nimages <= 2^24)
+    const bool large = r.active != 0 ? n * nimages > kAutoBrutePeriodic : n > kAutoBruteIsolated;
     bool want_cell = requested == TNR_CELL_LIST || (requested == TNR_AUTO && large);
     unsigned long long st = 0;
     if (requested == TNR_CELL_LIST) {
