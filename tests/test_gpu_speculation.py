@@ -172,3 +172,15 @@ def test_plan_hint_through_the_abi():
     bad["positions"][350, 1] = np.nan
     code, _, _, msg = count(bad, 5)
     assert code != TNR_OK and "finite" in msg
+
+
+def test_cutoff_change_between_calls():
+    # one shape at three cutoffs in turn: each call's pairs are its own
+    # cutoff's, whether the call follows one at the same cutoff or not
+    base = W.c4(seed=14, n_atoms=8000)
+    counts = {}
+    for rc in (6.0, 4.5, 6.0, 7.0, 4.5):
+        cfg = dict(base, cutoff=rc)
+        counts.setdefault(rc, set()).add(len(check(cfg)))
+    assert all(len(v) == 1 for v in counts.values())
+    assert len({next(iter(v)) for v in counts.values()}) == 3

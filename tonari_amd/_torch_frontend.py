@@ -331,8 +331,12 @@ def neighbor_list_hip(
         ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
         host, host_view, arrived = _host_result(device)
+        # the cutoff is part of the shape: a call at another cutoff takes the
+        # plain count -> emit path instead of a speculative emit sized for the
+        # old one (the cell is not: it drifts a little on every step of NPT
+        # dynamics, and a miss only re-runs the emit)
         key = (device, req.dtype, req.n_atoms, req.n_structures, req.half_list,
-               req.include_self, req.algorithm, frozenset(want))
+               req.include_self, req.algorithm, float(req.cutoff), frozenset(want))
         table = _speculation()
         guess = table.get(key)
         # the previous call of this shape planned brute force only: count
