@@ -1142,14 +1142,17 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
                                                      const T* pos, const int4* atom_wrap,
                                                      int4* binned_w, Vec4<T>* binned_p,
                                                      const unsigned long long* status) {
-    if (load_status(status + SS_FLAGS) & kAbortBits) return;
-    const bool wrapped = load_status(status + SS_ANY_WRAP) != 0;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n_atoms) return;
+    // the atom's own words load alongside the status words (in bounds for
+    // every i < n_atoms); the bin is used only once the request is known good
     const int g = atom_bin[i];
-    if (g < 0) return;
-    const int at = bin_start[g] + atom_rank[i];
+    const int rank = atom_rank[i];
     const Vec4<T> q = atom_q[i];
+    if (load_status(status + SS_FLAGS) & kAbortBits) return;
+    const bool wrapped = load_status(status + SS_ANY_WRAP) != 0;
+    if (g < 0) return;
+    const int at = bin_start[g] + rank;
     binned[at] = q;
     if (wrapped) {
         // the emitting pass of a wrapped structure reads each candidate's
