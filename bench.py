@@ -162,6 +162,55 @@ def time_phases(cfg, t, reps: int):
     return statistics.mean(count_ms), statistics.mean(emit_ms), E, plan
 
 
+def measured_peak(nbytes: int, reps: int = 20):
+    """Measured write and copy bandwidth of plain device kernels.
+
+    A fill of `nbytes` (torch's fill kernel: writes only, the emit's traffic
+    pattern) into two buffers in turn, as the bench's emit alternates two
+    output sets (the previous fill's dirty lines are still being written back
+    from the memory-attached last-level cache while the next one runs), and a
+    device-to-device copy of `nbytes` (reads and writes, 2 * nbytes moved).
+    HIP events on the current stream; mean over `reps` launches after one
+    warm-up launch of each buffer.
+    """
+    import torch
+
+    dev = torch.device("cuda:0")
+    words = nbytes // 4
+    bufs = [torch.empty(words, dtype=torch.int32, device=dev) for _ in range(2)]
+    src = torch.ones(words, dtype=torch.int32, device=dev)
+
+    def timed(fn):
+        for k in range(2):
+            fn(k)
+        torch.cuda.synchronize()
+        ts = []
+        for k in range(reps):
+            ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            ev[0].record()
+            fn(k)
+            ev[1].record()
+            torch.cuda.synchronize()
+            ts.append(ev[0].elapsed_time(ev[1]) * 1e-3)
+        return statistics.mean(ts), min(ts)
+
+    fill_mean, fill_min = timed(lambda k: bufs[k % 2].fill_(k))
+    same_mean, _ = timed(lambda k: bufs[0].fill_(k))
+    copy_mean, _ = timed(lambda k: bufs[k % 2].copy_(src))
+    del bufs, src
+    nb = words * 4
+    return {
+        "fill_alternating_GBps": round(nb / fill_mean / 1e9, 1),
+        "fill_alternating_best_GBps": round(nb / fill_min / 1e9, 1),
+        "fill_same_buffer_GBps": round(nb / same_mean / 1e9, 1),
+        "copy_GBps": round(2 * nb / copy_mean / 1e9, 1),
+        "bytes": nb,
+        "method": "torch fill_ of int32 into two buffers in turn (writes only), the same into "
+                  "one buffer, and copy_ between buffers (read + write); HIP events, mean of "
+                  f"{reps} launches",
+    }
+
+
 def load_traffic(name: str):
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
     if not os.path.exists(path):
@@ -172,37 +221,102 @@ def load_traffic(name: str):
 
 
 def time_backward(cfg, t, reps: int):
-    """HIP-event durations of the gradient of sum(w * D) for positions and cell.
+    """The gradient of sum(w * D) for positions and cell, three ways.
 
-    D comes from the public call with positions and cell requiring grad; its
-    backward is tnr_geometry_backward (fused).  For comparison, the same
-    gradient through the reference's Torch expression for D over the same
-    pairs (autograd of gathers, einsum and their scatter-adds).
+    - fused_us: the autograd backward of the public call's D (positions and
+      cell requiring grad), which runs tnr_geometry_backward, with torch's
+      allocations and zero fills around it;
+    - kernel_us: tnr_geometry_backward alone, HIP events on the stream it
+      runs on, with its algorithmic bytes and roofline fraction
+      (per pair: P 16 B, S 12 B and dL/dD 3s read; per atom: the position
+      gradient 3s written);
+    - torch_index_add_us: a fair Torch restatement of the same gradient:
+      index_add_ of dL/dD into the targets and of -dL/dD into the sources
+      (sources come sorted), and the cell gradient as S^T @ dL/dD (one
+      structure);
+    - torch_expression_us: autograd of the reference's Torch expression for D
+      (``_torch_frontend.py:92-104``), whose scatter-adds of the cell
+      gradient all land in the one cell.
     """
     import torch
 
+    from tonari_amd._extensions import load_torch_hip
     from tonari_amd._torch_frontend import _torch_geometry
 
     positions = t["positions"].clone().requires_grad_()
     cell = t["cell"].clone().requires_grad_()
     P, S, D = public_call(dict(cfg, quantities="PSD"), dict(t, positions=positions, cell=cell))
     w = torch.randn(D.shape, dtype=D.dtype, device=D.device)
-    D_torch = _torch_geometry(positions, cell, t["batch_ptr"], P, S)
     result = {}
-    # the Torch expression takes seconds on C4 (its scatter-adds into the one
-    # cell contend): one timed repetition after the warm-up
-    for name, values, n_rep in (("fused_us", D, reps), ("torch_expression_us", D_torch, 1)):
-        loss = (w * values).sum()
+
+    def events(fn, n_rep):
         times = []
         for rep in range(n_rep + 1):
             ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
             ev[0].record()
-            torch.autograd.grad(loss, (positions, cell), retain_graph=True)
+            fn()
             ev[1].record()
             torch.cuda.synchronize()
             if rep > 0:
                 times.append(ev[0].elapsed_time(ev[1]) * 1e3)
-        result[name] = round(statistics.median(times), 2)
+        return round(statistics.median(times), 2)
+
+    loss = (w * D).sum()
+    result["fused_us"] = events(
+        lambda: torch.autograd.grad(loss, (positions, cell), retain_graph=True), reps)
+
+    lib = load_torch_hip()
+    pos_d, cell_d = positions.detach(), cell.detach()
+    gp = torch.zeros_like(pos_d)
+    gc = torch.zeros_like(cell_d)
+    Dd = D.detach()
+    err = ctypes.create_string_buffer(512)
+    stream = torch.cuda.current_stream(pos_d.device).cuda_stream
+    nb = t["batch_ptr"].numel() - 1
+
+    def kernel():
+        rc = lib.tnr_geometry_backward(
+            0 if pos_d.dtype == torch.float32 else 1, P.shape[0], pos_d.shape[0], nb,
+            t["batch_ptr"].data_ptr(), P.data_ptr(), S.data_ptr(), Dd.data_ptr(), None,
+            w.data_ptr(), None, gp.data_ptr(), gc.data_ptr(), stream, err, len(err))
+        if rc != 0:
+            raise RuntimeError(err.value.decode())
+
+    result["kernel_us"] = events(kernel, reps)
+    s = pos_d.element_size()
+    b_alg = P.shape[0] * (16 + 12 + 3 * s) + pos_d.shape[0] * 3 * s + nb * 9 * s
+    result["algorithmic_bytes"] = int(b_alg)
+    result["kernel_GBps"] = round(b_alg / (result["kernel_us"] * 1e-6) / 1e9, 1)
+    result["kernel_frac"] = round(result["kernel_GBps"] / HBM_PEAK_GBPS, 4)
+
+    src, dst = P[:, 0], P[:, 1]
+    Sf = S.to(pos_d.dtype)
+
+    def index_add():
+        g_pos = torch.zeros_like(pos_d)
+        g_pos.index_add_(0, dst, w)
+        g_pos.index_add_(0, src, w, alpha=-1)
+        g_cell = (Sf.t() @ w).unsqueeze(0)
+        return g_pos, g_cell
+
+    result["torch_index_add_us"] = events(index_add, reps)
+    # both restatements agree with the fused kernel (checked once, loosely:
+    # float atomics sum in varying order)
+    g_pos, g_cell = index_add()
+    gp.zero_()
+    gc.zero_()
+    kernel()
+    torch.cuda.synchronize()
+    scale = float(g_pos.abs().max()) + 1.0
+    result["index_add_matches"] = bool(torch.allclose(gp, g_pos, rtol=1e-3, atol=1e-4 * scale)
+                                       and torch.allclose(gc, g_cell, rtol=1e-3,
+                                                          atol=1e-4 * float(g_cell.abs().max())))
+    # the Torch expression takes seconds on C4 (its scatter-adds into the one
+    # cell contend): one timed repetition after the warm-up
+    D_torch = _torch_geometry(positions, cell, t["batch_ptr"], P, S)
+    loss_t = (w * D_torch).sum()
+    result["torch_expression_us"] = events(
+        lambda: torch.autograd.grad(loss_t, (positions, cell), retain_graph=True), 1)
     result["n_pairs"] = int(P.shape[0])
     return result
 
@@ -559,8 +673,12 @@ def main() -> int:
                                                            args.cpu_baseline, args.cpu_budget)
             log(f"cpu baseline {name}: {secondary[name]['cpu_baseline']}")
 
+    log("measured peak: fill and copy")
+    peak = measured_peak(head["algorithmic_bytes"])
+    log(f"measured peak: {peak}")
     emit_s = head["emit_us"] * 1e-6
     achieved = head["algorithmic_bytes"] / emit_s / 1e9
+    peak_fill = peak["fill_alternating_GBps"]
     line = {
         "metric": METRIC,
         "value": head["M_pairs_per_s"],
@@ -594,6 +712,12 @@ def main() -> int:
             # host gaps) against the same algorithmic bytes
             "call_kernel_sum_us": head["kernel_sum_us"],
             "call_frac": head["frac_kernel_sum"],
+            # the second denominator: a plain fill of the same bytes into
+            # alternating buffers on this GPU
+            "peak_measured": peak_fill,
+            "frac_measured": round(achieved / peak_fill, 4),
+            "call_frac_measured": round(head["GBps_kernel_sum"] / peak_fill, 4),
+            "peak_measured_detail": peak,
         },
         "cpu_baseline": base,
         "M_atoms_per_s": head["M_atoms_per_s"],
