@@ -137,12 +137,17 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
  * the plan back, bindings_cuda.cpp:96-98,161-185).  tnr_count_async with a
  * plan hint: host_result[3] (the plan mask: bit 0 brute-force structures,
  * bit 1 cell-list structures, bit 2 every brute-force structure a
- * molecule, i.e. without periodic axes and of at most 2,048 atoms) of an
- * earlier count of a request of the same shape, or -1 for none.  Hint 1
- * (brute force only) with algorithm TNR_AUTO: the cell-list kernels are not
- * launched.  Hint 5 (molecules only) with TNR_AUTO or TNR_BRUTE_FORCE: one
- * kernel plans the whole batch in place of the set-up, atom and planning
- * kernels.  The device checks the hint: if a structure does not fit it,
+ * molecule, i.e. without periodic axes and of at most 2,048 atoms, bit 3
+ * one fully periodic structure whose bin grid follows from its cell and
+ * cutoff) of an earlier count of a request of the same shape, or -1 for
+ * none.  Hint 1 (brute force only) with algorithm TNR_AUTO: the cell-list
+ * kernels are not launched.  Hint 5 (molecules only) with TNR_AUTO or
+ * TNR_BRUTE_FORCE: one kernel plans the whole batch in place of the set-up,
+ * atom and planning kernels.  Hint 10 (one periodic cell-list structure)
+ * with TNR_AUTO or TNR_CELL_LIST: the bin grid is chosen before the atoms
+ * are reduced and the prologue takes three launches instead of four, none
+ * of them a device-wide scan.  The device checks the hint: if a structure
+ * does not fit it,
  * nothing of this count is valid and tnr_count_finish returns TNR_RETRY;
  * the caller counts again without the hint.  Other hints launch the full
  * count.

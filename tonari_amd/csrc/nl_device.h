@@ -74,7 +74,8 @@ enum StatusSlot : int {
     SS_PAIRS = 1,
     SS_TOTAL_IMAGES = 2,
     SS_PLAN = 3,          // bit 0: some brute-force structure, bit 1: some cell-list one,
-                          // bit 2: every brute-force structure is a molecule
+                          // bit 2: every brute-force structure is a molecule,
+                          // bit 3: the periodic fast prologue applies
     SS_TOTAL_BINS = 4,
     SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
@@ -87,6 +88,9 @@ enum StatusSlot : int {
 enum Algo : int { ALGO_NONE = 0, ALGO_BRUTE = 1, ALGO_CELL = 2 };
 constexpr unsigned long long kPlanFamilies = 3;   // plan bits 0-1: the kernel families
 constexpr unsigned long long kPlanMolecules = 4;  // plan bit 2
+// plan bit 3: one fully periodic cell-list structure whose grid the periodic
+// fast prologue chooses (periodic_grid holds), a hint for the next count
+constexpr unsigned long long kPlanPeriodicGrid = 8;
 
 // One record per structure.  Filled by k_setup (geometry), k_atoms
 // (reductions of atoms in blocks that span several structures) and k_plan

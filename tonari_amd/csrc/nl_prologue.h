@@ -571,14 +571,257 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
 }
 
 
+// Margins of a structure from the reductions of its atoms (max |p|, max
+// |wrap|): the broad-phase margin pad = 64 eps_T max(scale, rc), with scale =
+// 2 max|p| + sum_a (R_a + 2 max|w|) max_c |cell_ac| the operation scale of
+// neighbors_cpu.cpp:156-219, which sizes the bins, and the half-width of the
+// band the public predicate decides.  With wrapped atoms the band is the
+// padding above.  Without (every wrap zero, so the wrapped positions are the
+// positions): per component, the broad-phase D of the cell-list walk (p_t +
+// k.cell, minus p_s) and of the brute-force walk ((p_t - p_s) + k.cell,
+// fused) differ from the exact value by at most u (5 |D| + |p| + 4 B) and u
+// (4 |D| + 7 B), the public D by u (4 |D| + 8 B), with u = eps / 2 and B =
+// max_c sum_a R_a |cell_ac| the largest image translation; over three
+// components and the d2 roundings (at most 4 u d together), |d_broad -
+// d_public| <= u (17.9 rc + 1.74 max|p| + 26 B) near the cutoff, first
+// order.  Twice that bound is the band.
+struct Margins {
+    double pad, band, maxp;
+    unsigned maxw;
+    bool safe;  // the padded cutoff is finite and at most 2 rc (bins of it are usable)
+};
+
+template <typename T>
+__device__ __forceinline__ Margins plan_margins(const double cell[9], const StructRec& r,
+                                                double maxp, unsigned maxw_u, double rc) {
+    Margins m;
+    const double maxw = (double)maxw_u;
+    const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
+    double scale = 0, bmax = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const double sc = 2 * maxp + ((double)R0 + 2 * maxw) * fabs(cell[c]) +
+                          ((double)R1 + 2 * maxw) * fabs(cell[3 + c]) +
+                          ((double)R2 + 2 * maxw) * fabs(cell[6 + c]);
+        scale = fmax(scale, sc);
+        bmax = fmax(bmax, (double)R0 * fabs(cell[c]) + (double)R1 * fabs(cell[3 + c]) +
+                              (double)R2 * fabs(cell[6 + c]));
+    }
+    m.pad = 64.0 * Ops<T>::eps * fmax(scale, rc);
+    m.band = maxw_u == 0 ? fmin(m.pad, Ops<T>::eps * (18.0 * rc + 1.75 * maxp + 26.0 * bmax))
+                         : m.pad;
+    m.maxp = maxp;
+    m.maxw = maxw_u;
+    m.safe = isfinite(rc + m.pad) && rc + m.pad <= 2 * rc && rc + m.pad <= Ops<T>::max;
+    return m;
+}
+
+// The record's thresholds from the margins (one writer).
+template <typename T>
+__device__ __forceinline__ void write_margins(StructRec& r, const Margins& m, double cutoff) {
+    const double rc = cutoff;
+    const double inner = rc - m.band;
+    r.pad = m.pad;
+    r.maxp = (unsigned long long)__double_as_longlong(m.maxp);
+    r.maxw = m.maxw;
+    r.any_wrap = m.maxw != 0;
+    r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
+    r.outer2 = (double)Ops<T>::up((rc + m.band) * (rc + m.band));
+    r.cut2 = (double)(T)(cutoff * cutoff);
+}
+
+// The reference CPU layout rule for an explicit cell_list
+// (neighbors_cpu.cpp:379-430): bins of the padded cutoff over the bounding
+// box of the wrapped positions.  True when the structure is refused.
+template <typename T>
+__device__ __forceinline__ bool cell_unsafe(const unsigned long long red[kRedCount], double rc,
+                                            const Margins& m, int64_t n, int64_t nimages) {
+    using K = RedKeys<T>;
+    const double size = rc + m.pad;
+    double count = 1;
+    bool ok = m.safe;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const double span =
+            K::upper_value(red[kRedChi + c]) - K::lower_value(red[kRedClo + c]) + 2 * size;
+        const double dim = span / size;
+        if (!isfinite(dim) || dim > 67108864.0) ok = false;
+        count *= fmax(1.0, ceil(dim));
+    }
+    return !ok || count > 67108864.0 || ceil(count / 64.0) > (double)n * (double)nimages;
+}
+
+// A bin grid of a cell-list structure: bins per axis, bins per grid unit,
+// origin, stencil reach and z segments per stencil row.
+struct GridPlan {
+    double inv_w[3], lo[3];
+    int nb[3], reach[3];
+    int zs;
+    int64_t nbins;
+};
+
+// z segments per stencil row for a z reach of Kz bins over nz bins.
+__device__ __forceinline__ int stencil_zseg(bool perz, int Kz, int nz) {
+    if (!perz) return 1;
+    const int span = 2 * Kz + 1;
+    return min(span, (span + nz - 1) / nz + 1);
+}
+
+// Bin grid for a stencil reach of kt bins per padded cutoff, run by all lanes
+// of one wave.  With reach_target 0 the reach is chosen per structure by an
+// estimated cost per source: the stencil candidates (distance tests) times
+// 1 + kBinOverhead / (sources per bin), since every bin builds and stages its
+// stencil once for all of its sources; stencils beyond the mask capacity take
+// the slow path and count four times.  The candidate reaches are evaluated
+// one per lane.  red (the reduced bounds) is read for non-periodic axes only.
+// Returns false, in every lane, when no grid fits (the structure then stays
+// with brute force, whose pairs are the same set): where the cutoff spans two
+// or more cell widths on every periodic axis (one bin per axis, a reach of
+// three bins: 7^3 stencil pieces, beyond kPieceCap), or beyond about 2^24
+// atoms.
+template <typename T>
+__device__ __forceinline__ bool choose_grid(const StructRec& r, const unsigned long long* red,
+                                            double rc, double pad, int64_t n, int reach_target,
+                                            GridPlan& gp) {
+    using K = RedKeys<T>;
+    const int active = r.active;
+    const double rcu0 = rc + 2 * pad;
+    const int k_lo = reach_target > 0 ? reach_target : 1;
+    const int k_hi = reach_target > 0 ? reach_target : 4;
+    const int lane = lane_id();
+    const int kt_i = min(k_lo + lane, k_hi);
+    const double kt = (double)kt_i;
+    double ext[3], wdt[3], nbf[3], rcu[3], lo[3];
+    bool ok = k_lo + lane <= k_hi;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const double gn = sqrt(r.grid[3 * a] * r.grid[3 * a] + r.grid[3 * a + 1] * r.grid[3 * a + 1] +
+                               r.grid[3 * a + 2] * r.grid[3 * a + 2]);
+        rcu[a] = rcu0 * gn;
+        lo[a] = 0.0;
+        if (active >> a & 1) {
+            ext[a] = 1.0;
+            nbf[a] = fmin(fmax(ceil(kt / rcu[a]) - 1.0, 1.0), 1048576.0);
+            wdt[a] = 1.0 / nbf[a];
+        } else {
+            lo[a] = K::lower_value(red[kRedUlo + a]);
+            const double hi = K::upper_value(red[kRedUhi + a]);
+            ext[a] = fmax(hi - lo[a], 0.0);
+            if (!isfinite(ext[a]) || !isfinite(lo[a])) ok = false;
+            wdt[a] = rcu[a] / kt * (1.0 + 1e-9);
+            if (ext[a] / wdt[a] > 1048575.0) wdt[a] = ext[a] / 1048575.0 * (1.0 + 1e-9);
+            if (!(wdt[a] > 0) || !isfinite(wdt[a])) wdt[a] = 1.0;
+            nbf[a] = fmin(floor(ext[a] / wdt[a]) + 1.0, 1048576.0);
+        }
+    }
+    const double capb = 2.0 * (double)n + 64.0;
+    for (int it = 0; it < 200 && nbf[0] * nbf[1] * nbf[2] > capb; ++it) {
+        const int a = (nbf[0] >= nbf[1] && nbf[0] >= nbf[2]) ? 0 : (nbf[1] >= nbf[2] ? 1 : 2);
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            if (c != a) continue;
+            if (active >> c & 1) {
+                nbf[c] = ceil(nbf[c] / 2.0);
+                wdt[c] = 1.0 / nbf[c];
+            } else {
+                wdt[c] *= 2.0;
+                nbf[c] = fmin(floor(ext[c] / wdt[c]) + 1.0, 1048576.0);
+            }
+        }
+    }
+    int reach[3];
+    bool reach_ok = true;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const double rd = floor(rcu[a] / wdt[a] * (1.0 + 1e-12)) + 1.0;
+        reach_ok = reach_ok && rd < 256.0;
+        reach[a] = rd < 256.0 ? (int)rd : 1;
+    }
+    const int rows = (2 * reach[0] + 1) * (2 * reach[1] + 1);
+    const int zs = stencil_zseg(active >> 2 & 1, reach[2], (int)nbf[2]);
+    const bool fits = ok && reach_ok && nbf[0] * nbf[1] * nbf[2] <= capb &&
+                      (long long)rows * zs <= kPieceCap &&
+                      (double)n * (double)(rows * zs) < 2147483647.0;
+    // estimated candidates of a stencil and sources of a bin
+    const double bins_f = nbf[0] * nbf[1] * nbf[2];
+    const double per_bin = (double)n / bins_f;
+    double span_bins = 1.0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const double w = 2.0 * reach[a] + 1.0;
+        span_bins *= (active >> a & 1) ? w : fmin(w, nbf[a]);
+    }
+    const double cand = span_bins * per_bin;
+    double cost = cand * (1.0 + kBinOverhead / fmax(per_bin, 1e-9)) *
+                  (cand > (double)(kMaskWords * kWave) ? 4.0 : 1.0);
+    // the cheapest fitting reach, the smallest on ties
+    cost = fits ? fmin(cost, 1.7976931348623157e308) : INFINITY;
+    int best = lane;
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        const double oc = __shfl_xor(cost, d);
+        const int ob = __shfl_xor(best, d);
+        if (oc < cost || (oc == cost && ob < best)) {
+            cost = oc;
+            best = ob;
+        }
+    }
+    best = __builtin_amdgcn_readfirstlane(best);
+    if (!(cost < INFINITY)) return false;
+    gp.nbins = (int64_t)__shfl(bins_f, best);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        gp.nb[a] = (int)__shfl(nbf[a], best);
+        gp.inv_w[a] = __shfl((active >> a & 1) ? nbf[a] : 1.0 / wdt[a], best);
+        gp.lo[a] = __shfl(lo[a], best);
+        gp.reach[a] = __shfl(reach[a], best);
+    }
+    gp.zs = __shfl(zs, best);
+    return true;
+}
+
+// Brute-force work units of a structure of n atoms (one writer): units of
+// bgroup consecutive sources, and for periodic structures k0 slices.
+__device__ __forceinline__ int64_t plan_brute_units(StructRec& r, int64_t n) {
+    int64_t units = 0;
+    if (molecule_path(r.active, n)) {
+        // a molecule: sources x chunks of 64 targets per unit
+        const int chunks = (int)((n + kWave - 1) / kWave);
+        const int g = (int)min((int64_t)max(kMolUnitWork / chunks, 1), n);
+        r.bgroup = g;
+        units = (n + g - 1) / g;
+    } else {
+        // a round: 64 (source, k0, target) triples, each walking the
+        // K1 x K2 images of its k0 plane, costing about 1 + K1 K2 / 4.
+        // A source whose K0 planes exceed a unit's work is split into
+        // slices of k0 (at most kMaskWords: their counts are kept in the
+        // source's hit-mask slot).
+        const int64_t K0 = 2 * (int64_t)r.reps[0] + 1;
+        const double round = 1.0 + 0.25 * (double)r.nimages / (double)K0;
+        const double want = fmax(kBruteUnitWork / round, 1.0);     // rounds per unit
+        const double per_source = (double)n * (double)K0 / kWave;  // rounds per source
+        double g = floor(want / per_source);
+        int64_t nsl = 1, width = K0;
+        if (g < 1.0) {
+            g = 1.0;
+            nsl = (int64_t)fmin(ceil(per_source / want),
+                                (double)(K0 < kMaxSlices ? K0 : kMaxSlices));
+            width = (K0 + nsl - 1) / nsl;
+            nsl = (K0 + width - 1) / width;
+        }
+        g = fmin(fmin(g, (double)n), (double)kBruteGroupCap);
+        r.bgroup = (int32_t)g;
+        r.bslices = (int32_t)nsl;
+        r.bwidth = (int32_t)width;
+        units = (n + (int64_t)g - 1) / (int64_t)g * nsl;
+    }
+    return units;
+}
+
 // Planner of one structure, run by all lanes of one wave (lane 0 writes the
 // record and the per-structure arrays): from the reduced bounds red (see
-// k_plan) the broad-phase margin, the algorithm and the bin grid.  The
-// margin pad = 64 eps_T max(scale, rc) bounds the difference between the
-// fused broad-phase distance and the public predicate, with scale = 2 max|p| +
-// sum_a (R_a + 2 max|w|) max_c |cell_ac|, the operation scale of
-// neighbors_cpu.cpp:156-219.  The candidate stencil reaches are evaluated one
-// per lane.
+// k_plan) the margins (plan_margins), the algorithm and the bin grid
+// (choose_grid) or the brute-force work units.
 template <typename T>
 __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, StructRec& r,
                                                const unsigned long long red[kRedCount],
@@ -599,240 +842,67 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
     double cell[9];
 #pragma unroll
     for (int e = 0; e < 9; ++e) cell[e] = (double)cells[9 * b + e];
-    const double maxp = K::magnitude_value(red[kRedP]);
-    const unsigned maxw_u = (unsigned)red[kRedW];
-    const double maxw = (double)maxw_u;
-    const int active = r.active;
-    const int R0 = r.reps[0], R1 = r.reps[1], R2 = r.reps[2];
-    double scale = 0;
-#pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        const double sc = 2 * maxp + ((double)R0 + 2 * maxw) * fabs(cell[c]) +
-                          ((double)R1 + 2 * maxw) * fabs(cell[3 + c]) +
-                          ((double)R2 + 2 * maxw) * fabs(cell[6 + c]);
-        scale = fmax(scale, sc);
-    }
     const double rc = cutoff;
-    const double pad = 64.0 * Ops<T>::eps * fmax(scale, rc);
-    // Half-width of the band the public predicate decides.  With wrapped
-    // atoms, the padding above.  Without (every wrap zero, so the wrapped
-    // positions are the positions): per component, the broad-phase D of the
-    // cell-list walk (p_t + k.cell, minus p_s) and of the brute-force walk
-    // ((p_t - p_s) + k.cell, fused) differ from the exact value by at most
-    // u (5 |D| + |p| + 4 B) and u (4 |D| + 7 B), the public D by u (4 |D| +
-    // 8 B), with u = eps / 2 and B = max_c sum_a R_a |cell_ac| the largest
-    // image translation; over three components and the d2 roundings (at most
-    // 4 u d together), |d_broad - d_public| <= u (17.9 rc + 1.74 max|p| + 26 B)
-    // near the cutoff, first order.  Twice that bound is the band.
-    double bmax = 0;
-#pragma unroll
-    for (int c = 0; c < 3; ++c)
-        bmax = fmax(bmax, (double)R0 * fabs(cell[c]) + (double)R1 * fabs(cell[3 + c]) +
-                              (double)R2 * fabs(cell[6 + c]));
-    const double band =
-        maxw_u == 0 ? fmin(pad, Ops<T>::eps * (18.0 * rc + 1.75 * maxp + 26.0 * bmax)) : pad;
-    const double inner = rc - band;
-    if (writer) {
-        r.pad = pad;
-        r.maxp = (unsigned long long)__double_as_longlong(maxp);
-        r.maxw = maxw_u;
-        r.any_wrap = maxw_u != 0;
-        r.inner2 = inner > 0 ? (double)Ops<T>::down(inner * inner) : 0.0;
-        r.outer2 = (double)Ops<T>::up((rc + band) * (rc + band));
-        r.cut2 = (double)(T)(cutoff * cutoff);
-    }
-    const bool safe = isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Ops<T>::max;
-
+    const Margins m = plan_margins<T>(cell, r, K::magnitude_value(red[kRedP]),
+                                      (unsigned)red[kRedW], rc);
+    if (writer) write_margins<T>(r, m, cutoff);
     const int64_t nimages = r.nimages;
     // n > floor(limit / nimages), as a product (nimages <= 2^24)
     const bool large = r.active != 0 ? n * nimages > kAutoBrutePeriodic : n > kAutoBruteIsolated;
     bool want_cell = requested == TNR_CELL_LIST || (requested == TNR_AUTO && large);
     unsigned long long st = 0;
-    if (requested == TNR_CELL_LIST) {
-        // The reference CPU layout rule (neighbors_cpu.cpp:379-430): bins of
-        // the padded cutoff over the bounding box of the wrapped positions.
-        const double size = rc + pad;
-        double count = 1;
-        bool ok = safe;
-#pragma unroll
-        for (int c = 0; c < 3; ++c) {
-            const double span = K::upper_value(red[kRedChi + c]) -
-                                K::lower_value(red[kRedClo + c]) + 2 * size;
-            const double dim = span / size;
-            if (!isfinite(dim) || dim > 67108864.0) ok = false;
-            count *= fmax(1.0, ceil(dim));
-        }
-        if (!ok || count > 67108864.0 || ceil(count / 64.0) > (double)n * (double)nimages)
-            st |= ST_CELL_UNSAFE;
-    }
-    if (!safe) want_cell = false;
+    if (requested == TNR_CELL_LIST && cell_unsafe<T>(red, rc, m, n, nimages)) st |= ST_CELL_UNSAFE;
+    if (!m.safe) want_cell = false;
     int algo = ALGO_BRUTE;
     int64_t nbins = 0;
-    if (want_cell) {
-        // Bin grid for a stencil reach of kt bins per padded cutoff.  With
-        // reach_target 0 the reach is chosen per structure by an estimated
-        // cost per source: the stencil candidates (distance tests) times
-        // 1 + kBinOverhead / (sources per bin), since every bin builds and
-        // stages its stencil once for all of its sources; stencils beyond
-        // the mask capacity take the slow path and count four times.
-        const double rcu0 = rc + 2 * pad;
-        const int k_lo = reach_target > 0 ? reach_target : 1;
-        const int k_hi = reach_target > 0 ? reach_target : 4;
-        const int lane = lane_id();
-        const int kt_i = min(k_lo + lane, k_hi);
-        const double kt = (double)kt_i;
-        double ext[3], wdt[3], nbf[3], rcu[3], lo[3];
-        bool ok = k_lo + lane <= k_hi;
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            const double gn = sqrt(r.grid[3 * a] * r.grid[3 * a] +
-                                   r.grid[3 * a + 1] * r.grid[3 * a + 1] +
-                                   r.grid[3 * a + 2] * r.grid[3 * a + 2]);
-            rcu[a] = rcu0 * gn;
-            lo[a] = 0.0;
-            if (active >> a & 1) {
-                ext[a] = 1.0;
-                nbf[a] = fmin(fmax(ceil(kt / rcu[a]) - 1.0, 1.0), 1048576.0);
-                wdt[a] = 1.0 / nbf[a];
-            } else {
-                lo[a] = K::lower_value(red[kRedUlo + a]);
-                const double hi = K::upper_value(red[kRedUhi + a]);
-                ext[a] = fmax(hi - lo[a], 0.0);
-                if (!isfinite(ext[a]) || !isfinite(lo[a])) ok = false;
-                wdt[a] = rcu[a] / kt * (1.0 + 1e-9);
-                if (ext[a] / wdt[a] > 1048575.0) wdt[a] = ext[a] / 1048575.0 * (1.0 + 1e-9);
-                if (!(wdt[a] > 0) || !isfinite(wdt[a])) wdt[a] = 1.0;
-                nbf[a] = fmin(floor(ext[a] / wdt[a]) + 1.0, 1048576.0);
-            }
-        }
-        const double capb = 2.0 * (double)n + 64.0;
-        for (int it = 0; it < 200 && nbf[0] * nbf[1] * nbf[2] > capb; ++it) {
-            const int a = (nbf[0] >= nbf[1] && nbf[0] >= nbf[2]) ? 0 : (nbf[1] >= nbf[2] ? 1 : 2);
-#pragma unroll
-            for (int c = 0; c < 3; ++c) {
-                if (c != a) continue;
-                if (active >> c & 1) {
-                    nbf[c] = ceil(nbf[c] / 2.0);
-                    wdt[c] = 1.0 / nbf[c];
-                } else {
-                    wdt[c] *= 2.0;
-                    nbf[c] = fmin(floor(ext[c] / wdt[c]) + 1.0, 1048576.0);
-                }
-            }
-        }
-        int reach[3];
-        bool reach_ok = true;
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            const double rd = floor(rcu[a] / wdt[a] * (1.0 + 1e-12)) + 1.0;
-            reach_ok = reach_ok && rd < 256.0;
-            reach[a] = rd < 256.0 ? (int)rd : 1;
-        }
-        const int rows = (2 * reach[0] + 1) * (2 * reach[1] + 1);
-        int zs = 1;
-        if (active >> 2 & 1) {
-            const int span = 2 * reach[2] + 1;
-            zs = min(span, (span + (int)nbf[2] - 1) / (int)nbf[2] + 1);
-        }
-        const bool fits = ok && reach_ok && nbf[0] * nbf[1] * nbf[2] <= capb &&
-                          (long long)rows * zs <= kPieceCap &&
-                          (double)n * (double)(rows * zs) < 2147483647.0;
-        // estimated candidates of a stencil and sources of a bin
-        const double bins_f = nbf[0] * nbf[1] * nbf[2];
-        const double per_bin = (double)n / bins_f;
-        double span_bins = 1.0;
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            const double w = 2.0 * reach[a] + 1.0;
-            span_bins *= (active >> a & 1) ? w : fmin(w, nbf[a]);
-        }
-        const double cand = span_bins * per_bin;
-        double cost = cand * (1.0 + kBinOverhead / fmax(per_bin, 1e-9)) *
-                      (cand > (double)(kMaskWords * kWave) ? 4.0 : 1.0);
-        // the cheapest fitting reach, the smallest on ties
-        cost = fits ? fmin(cost, 1.7976931348623157e308) : INFINITY;
-        int best = lane;
-#pragma unroll
-        for (int d = kWave / 2; d > 0; d >>= 1) {
-            const double oc = __shfl_xor(cost, d);
-            const int ob = __shfl_xor(best, d);
-            if (oc < cost || (oc == cost && ob < best)) {
-                cost = oc;
-                best = ob;
-            }
-        }
-        best = __builtin_amdgcn_readfirstlane(best);
-        // A structure that no bin grid fits stays with brute force, whose
-        // pairs are the same set.  This happens where the cutoff spans two or
-        // more cell widths on every periodic axis (one bin per axis, a reach
-        // of three bins: 7^3 stencil pieces, beyond kPieceCap), or beyond
-        // about 2^24 atoms.  An explicit cell_list request then has its
-        // brute-force structures counted by the cell-list counting kernel.
-        if (cost < INFINITY) {
-            algo = ALGO_CELL;
-            nbins = (int64_t)__shfl(bins_f, best);
-            double nbw[3], invw[3], low[3];
-            int rch[3];
+    GridPlan gp;
+    // An explicit cell_list request whose structure no grid fits has its
+    // brute-force structures counted by the cell-list counting kernel.
+    if (want_cell && choose_grid<T>(r, red, rc, m.pad, n, reach_target, gp)) {
+        algo = ALGO_CELL;
+        nbins = gp.nbins;
+        if (writer) {
 #pragma unroll
             for (int a = 0; a < 3; ++a) {
-                nbw[a] = __shfl(nbf[a], best);
-                invw[a] = __shfl((active >> a & 1) ? nbf[a] : 1.0 / wdt[a], best);
-                low[a] = __shfl(lo[a], best);
-                rch[a] = __shfl(reach[a], best);
+                r.nb[a] = (int32_t)gp.nb[a];
+                r.inv_w[a] = gp.inv_w[a];
+                r.lo[a] = gp.lo[a];
+                r.reach[a] = gp.reach[a];
             }
-            const int zsb = __shfl(zs, best);
-            if (writer) {
-#pragma unroll
-                for (int a = 0; a < 3; ++a) {
-                    r.nb[a] = (int32_t)nbw[a];
-                    r.inv_w[a] = invw[a];
-                    r.lo[a] = low[a];
-                    r.reach[a] = rch[a];
-                }
-                r.zseg = zsb;
-            }
+            r.zseg = gp.zs;
         }
     }
     if (writer) {
         r.algo = algo;
         r.nbins = nbins;
         struct_bins[b] = nbins;
-        // brute force: work units of bgroup consecutive sources
-        int64_t units = 0;
-        if (algo == ALGO_BRUTE && molecule_path(r.active, n)) {
-            // a molecule: sources x chunks of 64 targets per unit
-            const int chunks = (int)((n + kWave - 1) / kWave);
-            const int g = (int)min((int64_t)max(kMolUnitWork / chunks, 1), n);
-            r.bgroup = g;
-            units = (n + g - 1) / g;
-        } else if (algo == ALGO_BRUTE) {
-            // a round: 64 (source, k0, target) triples, each walking the
-            // K1 x K2 images of its k0 plane, costing about 1 + K1 K2 / 4.
-            // A source whose K0 planes exceed a unit's work is split into
-            // slices of k0 (at most kMaskWords: their counts are kept in the
-            // source's hit-mask slot).
-            const int64_t K0 = 2 * (int64_t)r.reps[0] + 1;
-            const double round = 1.0 + 0.25 * (double)nimages / (double)K0;
-            const double want = fmax(kBruteUnitWork / round, 1.0);       // rounds per unit
-            const double per_source = (double)n * (double)K0 / kWave;    // rounds per source
-            double g = floor(want / per_source);
-            int64_t nsl = 1, width = K0;
-            if (g < 1.0) {
-                g = 1.0;
-                nsl = (int64_t)fmin(ceil(per_source / want),
-                                    (double)(K0 < kMaxSlices ? K0 : kMaxSlices));
-                width = (K0 + nsl - 1) / nsl;
-                nsl = (K0 + width - 1) / width;
-            }
-            g = fmin(fmin(g, (double)n), (double)kBruteGroupCap);
-            r.bgroup = (int32_t)g;
-            r.bslices = (int32_t)nsl;
-            r.bwidth = (int32_t)width;
-            units = (n + (int64_t)g - 1) / (int64_t)g * nsl;
-        }
-        struct_units[b] = units;
+        struct_units[b] = algo == ALGO_BRUTE ? plan_brute_units(r, n) : 0;
         r.flags |= st;
     }
+}
+
+// The grid of the periodic fast prologue, run by all lanes of one wave: for a
+// fully periodic structure planned as a cell list (an explicit cell_list, or
+// auto above the brute-force crossover), the grid choose_grid picks with the
+// margin of atoms inside the cell (max |p_c| <= sum_a |cell_ac|, no wraps).
+// False, in every lane, when the fast prologue does not apply.  k_single_bin
+// runs it too, so that the plan bit it reports is exactly this condition.
+template <typename T>
+__device__ __forceinline__ bool periodic_grid(const StructRec& r, const T* cells, double cutoff,
+                                              int requested, int reach_target, GridPlan& gp) {
+    const int64_t n = r.natoms;
+    if ((r.flags & kAbortBits) || r.active != 7 || n <= 0 || requested == TNR_BRUTE_FORCE)
+        return false;
+    if (requested == TNR_AUTO && !(n * r.nimages > kAutoBrutePeriodic)) return false;
+    double cell[9];
+#pragma unroll
+    for (int e = 0; e < 9; ++e) cell[e] = (double)cells[e];
+    double maxp = 0;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) maxp = fmax(maxp, fabs(cell[c]) + fabs(cell[3 + c]) + fabs(cell[6 + c]));
+    const Margins m = plan_margins<T>(cell, r, maxp, 0u, cutoff);
+    if (!m.safe) return false;
+    return choose_grid<T>(r, nullptr, cutoff, m.pad, n, reach_target, gp);
 }
 
 // One workgroup per structure: combines the block partials of k_atoms (all
@@ -1032,6 +1102,7 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
     __shared__ StructRec s_rec;
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
     __shared__ long long s_bins, s_units;
+    __shared__ int s_fast;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
     // the record (16-byte words) and this thread's partials in one round trip
     constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(int4));
@@ -1081,11 +1152,23 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
             r.flags = flags;
             s_bins = 0;
             s_units = 0;
+            s_fast = 0;
             r.algo = ALGO_NONE;
         }
         if (!(flags & kAbortBits))
             plan_structure<T>(cells, 0, r, v, cutoff, requested, reach_target, &s_bins,
                               &s_units);
+        if (blockIdx.x == 0) {
+            // whether the next count of this shape may take the periodic fast
+            // prologue (the plan bit kPlanPeriodicGrid); lane 0's writes to the
+            // record above are visible to the wave
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            GridPlan gp;
+            const bool fast = r.algo == ALGO_CELL &&
+                              periodic_grid<T>(r, cells, cutoff, requested, reach_target, gp);
+            if (lane == 0) s_fast = fast ? 1 : 0;
+        }
     }
     __syncthreads();
     if (tid == 0) {
@@ -1110,7 +1193,7 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
             status[SS_TOTAL_UNITS] = (unsigned long long)s_units;
             status[SS_ANY_WRAP] = r.algo == ALGO_CELL && r.any_wrap ? 1ull : 0ull;
             status[SS_PLAN] = r.algo == ALGO_CELL
-                                  ? 2ull
+                                  ? (s_fast ? 2ull | kPlanPeriodicGrid : 2ull)
                                   : (r.algo == ALGO_BRUTE
                                          ? (molecule_path(r.active, r.natoms) ? 1ull | kPlanMolecules
                                                                               : 1ull)
@@ -1161,6 +1244,327 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
         binned_w[at] = atom_wrap[i];
         binned_p[at] = Vec4<T>{pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], q.w};
     }
+}
+
+// ------------------------------------------------ periodic fast prologue
+// A request of one fully periodic structure whose previous count of the same
+// shape planned it as a cell list (plan bit kPlanPeriodicGrid) bins its atoms
+// without waiting for their reductions: the bin grid of a fully periodic
+// structure depends on the cell, the cutoff and the margin pad only, so it is
+// chosen from a margin estimate before any atom is reduced (periodic_grid)
+// and every atom is binned in the first kernel.  The margins are finished
+// from the atom reductions beside the bin scan, where the stencil reach is
+// refitted to the true margin (periodic_finish).
+//   k_periodic_atoms     set-up and grid per block; per atom: wraps, wrapped
+//                        position, block reductions, bin;
+//   k_periodic_rank      one returning atomic per atom on its bin counter;
+//   k_periodic_bin_scan  the bin scan (look-back), and in one more workgroup
+//                        the finished plan and the status words;
+//   k_scatter            as for every cell-list request.
+// Four launches, as the general single-structure prologue (k_atoms,
+// k_single_bin, the bin scan, k_scatter), but the reductions and the
+// planning no longer sit between the atom pass and the atomics (every
+// k_single_bin block re-reduces all partials and plans before it bins).
+
+// First kernel of the periodic fast prologue (one thread per atom).  As
+// k_atoms<T, true> (every block derives the record in LDS, thread 0; per
+// atom the wraps, the wrapped position and the block reductions, written as
+// the block's partial with its atoms' error bits), and wave 0 of every block
+// chooses the grid (periodic_grid), so each atom's bin is known here.  Block
+// 0 stores the record and the status words: all zero but the bin total, or
+// ST_PLAN_HINT when the fast prologue does not apply (every later kernel then
+// skips its work and the caller counts again without the hint).  The grid
+// also zeroes the bin counters, the pair scan's tile states and the
+// per-source pair counts.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_periodic_atoms(
+    const T* pos, const int64_t* bp, const T* cells, const uint8_t* pbc, double cutoff,
+    int64_t n_atoms, int requested, int reach_target, StructRec* recs, BlockPartial* partials,
+    int* atom_struct, int4* atom_wrap, Vec4<T>* atom_q, int* atom_bin,
+    unsigned long long* status, int* bin_count, int64_t n_bin_count, unsigned long long* tiles,
+    int64_t n_tiles, long long* counts, long long* struct_bins, long long* bin_off,
+    long long* struct_units, long long* unit_off) {
+    __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
+    __shared__ unsigned long long s_atom_flags;
+    __shared__ int s_fast;
+    __shared__ StructRec s_rec;
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
+    {
+        const int64_t stride = (int64_t)gridDim.x * kBlock;
+        const int64_t k0 = (int64_t)blockIdx.x * kBlock + tid;
+        if (k0 < n_atoms) counts[k0] = 0;
+        for (int64_t k = k0; k < n_bin_count; k += stride) bin_count[k] = 0;
+        for (int64_t k = k0; k < n_tiles; k += stride) tiles[k] = 0;
+    }
+    const int64_t i = (int64_t)blockIdx.x * kBlock + tid;
+    const int64_t ic = i < n_atoms ? i : n_atoms - 1;
+    T p_pre[3];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) p_pre[c] = pos[3 * ic + c];
+    if (tid == 0) {
+        setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, 0, s_rec);
+        s_atom_flags = 0;
+    }
+    __syncthreads();
+    if (wv == 0) {
+        GridPlan gp;
+        const bool fast = periodic_grid<T>(s_rec, cells, cutoff, requested, reach_target, gp);
+        if (lane == 0) {
+            StructRec& r = s_rec;
+            r.bin0 = 0;
+            r.unit0 = 0;
+            r.algo = fast ? ALGO_CELL : ALGO_NONE;
+            r.nbins = fast ? gp.nbins : 0;
+            if (fast) {
+#pragma unroll
+                for (int a = 0; a < 3; ++a) {
+                    r.nb[a] = (int32_t)gp.nb[a];
+                    r.inv_w[a] = gp.inv_w[a];
+                    r.lo[a] = gp.lo[a];
+                    r.reach[a] = gp.reach[a];
+                }
+                r.zseg = gp.zs;
+            }
+            s_fast = fast ? 1 : 0;
+            if (blockIdx.x == 0) {
+                recs[0] = r;
+                const long long nbins = fast ? (long long)gp.nbins : 0;
+                struct_bins[0] = nbins;
+                bin_off[0] = 0;
+                bin_off[1] = nbins;
+                struct_units[0] = 0;
+                unit_off[0] = 0;
+                unit_off[1] = 0;
+                for (int k = 0; k < SS_SLOTS; ++k) status[k] = 0;
+                status[SS_TOTAL_BINS] = (unsigned long long)nbins;
+                status[SS_FLAGS] = fast ? 0ull : ST_PLAN_HINT;
+            }
+        }
+    }
+    __syncthreads();
+    const bool valid = i < n_atoms;
+    if (!s_fast) {
+        if (valid) atom_bin[i] = -1;
+        if (tid == 0) partials[blockIdx.x].flags = 0;
+        return;
+    }
+    const StructRec& r = s_rec;
+    bool good = false;
+    T q[3] = {T(0), T(0), T(0)};
+    int w[3] = {0, 0, 0};
+    double u[3] = {0, 0, 0};
+    double pmax = 0;
+    unsigned long long st = 0;
+    if (valid) {
+        atom_struct[i] = 0;
+        bool finite = true;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) finite = finite && isfinite((double)p_pre[c]);
+        if (!finite) {
+            st |= ST_POS_NONFINITE;
+        } else {
+            const double pd[3] = {(double)p_pre[0], (double)p_pre[1], (double)p_pre[2]};
+            bool ok = true;
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                const double dcol[3] = {(double)(T)r.dual[a], (double)(T)r.dual[3 + a],
+                                        (double)(T)r.dual[6 + a]};
+                w[a] = wrap_of(pd, dcol, &ok);
+            }
+            if (!ok) {
+                st |= ST_WRAP_RANGE;
+            } else {
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    T x = p_pre[c];
+#pragma unroll
+                    for (int a = 0; a < 3; ++a)
+                        x = Ops<T>::sub(x, Ops<T>::mul((T)w[a], cells[3 * a + c]));
+                    q[c] = x;
+                }
+                grid_coords(r, q, u);
+                pmax = fmax(fabs(pd[0]), fmax(fabs(pd[1]), fabs(pd[2])));
+                good = true;
+            }
+        }
+        atom_wrap[i] = make_int4(w[0], w[1], w[2], 0);
+        atom_q[i] = Vec4<T>{q[0], q[1], q[2], idx_as((int)i, T(0))};
+        atom_bin[i] = good ? (int)local_bin(r, q) : -1;
+    }
+    if (st) atomicOr(&s_atom_flags, st);
+    using K = RedKeys<T>;
+    unsigned long long v[kRedCount];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        v[kRedUlo + a] = good ? K::lower(u[a]) : 0ull;
+        v[kRedUhi + a] = good ? K::upper(u[a]) : 0ull;
+        v[kRedClo + a] = good ? K::lower_exact(q[a]) : 0ull;
+        v[kRedChi + a] = good ? K::upper_exact(q[a]) : 0ull;
+    }
+    v[kRedP] = good ? K::magnitude(pmax) : 0ull;
+    v[kRedW] = good ? (unsigned long long)max(max(abs(w[0]), abs(w[1])), abs(w[2])) : 0ull;
+#pragma unroll
+    for (int e = 0; e < kRedCount; ++e) v[e] = K::wave_max(v[e]);
+    if (lane == 0)
+#pragma unroll
+        for (int e = 0; e < kRedCount; ++e) s_red[wv][e] = v[e];
+    __syncthreads();
+    if (tid < kRedCount) {
+        const int e = tid;
+        unsigned long long x = s_red[0][e];
+#pragma unroll
+        for (int k = 1; k < kWavesPerBlock; ++k) x = s_red[k][e] > x ? s_red[k][e] : x;
+        partials[blockIdx.x].red[e] = x;
+    }
+    if (tid == kRedCount) partials[blockIdx.x].flags = s_atom_flags;
+}
+
+// Last workgroup of k_periodic_bin_scan: the reductions of every k_periodic_atoms
+// block, the margins (plan_margins), the reference's layout rule for an
+// explicit cell_list, and the stencil reach refitted to the true margin
+// (bins of the chosen grid, a padded cutoff of rc + 2 pad); a structure whose
+// refitted stencil no longer fits is planned as brute force (the same pair
+// set).  Then the record, the per-structure arrays and the status words.
+template <typename T>
+__device__ __forceinline__ void periodic_finish(const T* cells, int64_t n_atoms, double cutoff,
+                                                int requested, StructRec* recs,
+                                                const BlockPartial* partials, int64_t n_partials,
+                                                long long* struct_bins, long long* bin_off,
+                                                long long* struct_units, long long* unit_off,
+                                                int64_t cap_bins, unsigned long long* status) {
+    using K = RedKeys<T>;
+    __shared__ StructRec s_rec;
+    __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
+    const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
+    constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(int4));
+    if (tid < kRecWords)
+        reinterpret_cast<int4*>(&s_rec)[tid] = reinterpret_cast<const int4*>(recs)[tid];
+    const unsigned long long st0 = load_status(status + SS_FLAGS);
+    unsigned long long v[kRedCount + 1];
+#pragma unroll
+    for (int e = 0; e <= kRedCount; ++e) v[e] = 0;
+#pragma unroll 2
+    for (int64_t kb = tid; kb < n_partials; kb += kBlock) {
+        const ulonglong2* wp = reinterpret_cast<const ulonglong2*>(partials + kb);
+        ulonglong2 x[kRedCount / 2 + 1];
+#pragma unroll
+        for (int e = 0; e <= kRedCount / 2; ++e) x[e] = wp[e];
+#pragma unroll
+        for (int e = 0; e < kRedCount / 2; ++e) {
+            v[2 * e] = x[e].x > v[2 * e] ? x[e].x : v[2 * e];
+            v[2 * e + 1] = x[e].y > v[2 * e + 1] ? x[e].y : v[2 * e + 1];
+        }
+        v[kRedCount] |= x[kRedCount / 2].x;
+    }
+    if (st0 & kAbortBits) return;  // the hint did not hold (block-uniform)
+#pragma unroll
+    for (int e = 0; e < kRedCount; ++e) v[e] = K::wave_max(v[e]);
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) v[kRedCount] |= __shfl_xor(v[kRedCount], d);
+    if (lane == 0)
+#pragma unroll
+        for (int e = 0; e <= kRedCount; ++e) s_red[wv][e] = v[e];
+    __syncthreads();
+    if (wv != 0) return;
+#pragma unroll
+    for (int e = 0; e <= kRedCount; ++e) v[e] = s_red[0][e];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) {
+#pragma unroll
+        for (int e = 0; e < kRedCount; ++e) v[e] = s_red[w][e] > v[e] ? s_red[w][e] : v[e];
+        v[kRedCount] |= s_red[w][kRedCount];
+    }
+    StructRec& r = s_rec;
+    const int64_t n = r.natoms;
+    unsigned long long st = r.flags | v[kRedCount];
+    int algo = ALGO_CELL;
+    long long nbins = r.nbins, units = 0;
+    if (!(st & kAbortBits)) {
+        double cell[9];
+#pragma unroll
+        for (int e = 0; e < 9; ++e) cell[e] = (double)cells[e];
+        const double rc = cutoff;
+        const Margins m = plan_margins<T>(cell, r, K::magnitude_value(v[kRedP]), (unsigned)v[kRedW], rc);
+        if (requested == TNR_CELL_LIST && cell_unsafe<T>(v, rc, m, n, r.nimages))
+            st |= ST_CELL_UNSAFE;
+        // the reach that bins of the chosen grid need for the true margin
+        bool fits = m.safe;
+        int reach[3];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const double gn = sqrt(r.grid[3 * a] * r.grid[3 * a] + r.grid[3 * a + 1] * r.grid[3 * a + 1] +
+                                   r.grid[3 * a + 2] * r.grid[3 * a + 2]);
+            const double rcu = (rc + 2 * m.pad) * gn;
+            const double rd = floor(rcu * (double)r.nb[a] * (1.0 + 1e-12)) + 1.0;
+            fits = fits && rd < 256.0;
+            reach[a] = rd < 256.0 ? (int)rd : 1;
+        }
+        const int zs = stencil_zseg(true, reach[2], r.nb[2]);
+        const int rows = (2 * reach[0] + 1) * (2 * reach[1] + 1);
+        fits = fits && (long long)rows * zs <= kPieceCap &&
+               (double)n * (double)(rows * zs) < 2147483647.0;
+        if (lane == 0) {
+            write_margins<T>(r, m, cutoff);
+            if (fits) {
+#pragma unroll
+                for (int a = 0; a < 3; ++a) r.reach[a] = reach[a];
+                r.zseg = zs;
+            } else {
+                algo = ALGO_BRUTE;
+                nbins = 0;
+                r.nbins = 0;
+                units = plan_brute_units(r, n);
+            }
+        }
+    }
+    if (lane != 0) return;
+    r.algo = (st & kAbortBits) ? ALGO_NONE : algo;
+    r.flags = st;
+    recs[0] = r;
+    struct_bins[0] = nbins;
+    bin_off[1] = nbins;
+    struct_units[0] = units;
+    unit_off[1] = units;
+    const unsigned long long images = (unsigned long long)r.img_total;
+    if (nbins > cap_bins) st |= ST_CAPACITY;
+    if (images > (unsigned long long)kImageCap) st |= ST_BATCH_IMAGE_CAP;
+    // the bin total stays the grid's (the bin scan beside this workgroup
+    // reads it); a structure planned as brute force has no cell-list work
+    status[SS_TOTAL_UNITS] = (unsigned long long)units;
+    status[SS_ANY_WRAP] = algo == ALGO_CELL && r.any_wrap ? 1ull : 0ull;
+    status[SS_PLAN] = algo == ALGO_CELL ? 2ull | kPlanPeriodicGrid : 1ull;
+    status[SS_TOTAL_IMAGES] = images;
+    if (st) atomicOr(status + SS_FLAGS, st);
+}
+
+// Second kernel of the periodic fast prologue: one returning atomic per
+// binned atom on its bin's counter (the atom's rank in the bin).
+__global__ __launch_bounds__(kBlock) void k_periodic_rank(int64_t n_atoms, const int* atom_bin,
+                                                           int* atom_rank, int* bin_count) {
+    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (i >= n_atoms) return;
+    const int g = atom_bin[i];
+    if (g >= 0) atom_rank[i] = atomicAdd(bin_count + g, 1);
+}
+
+// Third kernel of the periodic fast prologue: the look-back scan of the bin
+// counts (bin starts), and in its last workgroup, which takes no scan tile,
+// the finished plan (periodic_finish), which leaves the bin total the scan
+// reads alone.  Per-block timestamps on C4: run beside the ranking atomics,
+// the finishing workgroup waited 7.8 us for its loads of the block partials.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_periodic_bin_scan(
+    const T* cells, int64_t n_atoms, double cutoff, int requested, StructRec* recs,
+    const BlockPartial* partials, int64_t n_partials, long long* struct_bins, long long* bin_off,
+    long long* struct_units, long long* unit_off, int64_t cap_bins, unsigned long long* status,
+    const int* bin_count, int* bin_start, unsigned long long* tiles) {
+    if (blockIdx.x + 1 == gridDim.x) {
+        periodic_finish<T>(cells, n_atoms, cutoff, requested, recs, partials, n_partials,
+                           struct_bins, bin_off, struct_units, unit_off, cap_bins, status);
+        return;
+    }
+    scan_lookback_block<int, int>(bin_count, cap_bins, status + SS_TOTAL_BINS, bin_start, tiles,
+                                  status + SS_TICKET_BINS, status, nullptr, nullptr);
 }
 
 }  // namespace tnr

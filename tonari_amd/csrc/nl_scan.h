@@ -91,7 +91,8 @@ __device__ __forceinline__ long long lookback_exclusive(unsigned long long* tile
 }
 
 // Exclusive scan of n (min(n, *n_dev) when n_dev is given) non-negative values of
-// `in` into out[0..n], out[n] = total, in one launch.  Blocks take tiles of
+// `in` (which holds at least one element) into out[0..n], out[n] = total, in
+// one launch.  Blocks take tiles of
 // kScanTile items in the order they start (an atomic ticket), so every
 // earlier tile belongs to a block that is already running; a block publishes
 // its tile aggregate, then its first wave looks back over the 64 preceding
@@ -105,13 +106,13 @@ __device__ __forceinline__ long long lookback_exclusive(unsigned long long* tile
 // pinned host buffer, which the caller reads after synchronising with the
 // stream.
 template <typename In, typename Out>
-__global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t n,
-                                                           const unsigned long long* n_dev,
-                                                           Out* out, unsigned long long* tiles,
-                                                           unsigned long long* ticket,
-                                                           unsigned long long* status,
-                                                           unsigned long long* total_slot,
-                                                           long long* host_out = nullptr) {
+__device__ __forceinline__ void scan_lookback_block(const In* in, int64_t n,
+                                                    const unsigned long long* n_dev, Out* out,
+                                                    unsigned long long* tiles,
+                                                    unsigned long long* ticket,
+                                                    unsigned long long* status,
+                                                    unsigned long long* total_slot,
+                                                    long long* host_out) {
     __shared__ long long s_tile, s_excl;
     if (n_dev) n = min(n, (int64_t)*n_dev);
     const int64_t ntiles = n > 0 ? (n + kScanTile - 1) / kScanTile : 1;
@@ -122,12 +123,16 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
     __syncthreads();
     const int64_t tile = s_tile;
     const int64_t base = tile * kScanTile + (int64_t)threadIdx.x * kTileItems;
+    // every load is issued before the first is used (slots past n re-read
+    // in[0], which every caller's input holds, and count as 0)
+    In raw[kTileItems];
+#pragma unroll
+    for (int k = 0; k < kTileItems; ++k) raw[k] = in[base + k < n ? base + k : 0];
     long long v[kTileItems];
     long long s = 0;
 #pragma unroll
     for (int k = 0; k < kTileItems; ++k) {
-        const int64_t i = base + k;
-        v[k] = i < n ? (long long)in[i] : 0;
+        v[k] = base + k < n ? (long long)raw[k] : 0;
         s += v[k];
     }
     long long total;
@@ -154,6 +159,17 @@ __global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t 
                                                            __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+}
+
+template <typename In, typename Out>
+__global__ __launch_bounds__(kBlock) void k_scan_lookback(const In* in, int64_t n,
+                                                           const unsigned long long* n_dev,
+                                                           Out* out, unsigned long long* tiles,
+                                                           unsigned long long* ticket,
+                                                           unsigned long long* status,
+                                                           unsigned long long* total_slot,
+                                                           long long* host_out = nullptr) {
+    scan_lookback_block<In, Out>(in, n, n_dev, out, tiles, ticket, status, total_slot, host_out);
 }
 
 // The summary of record r for the batch scan.

@@ -10,6 +10,11 @@
 //              position, block reductions; zeroes the bin counters and scan
 //              tiles) -> k_single_bin (plan: margins, algorithm, bin grid,
 //              status words; then binning);
+//   tnr_count, one fully periodic structure with the plan hint of an
+//              earlier count: k_periodic_atoms (grid from the cell and
+//              cutoff; per atom also its bin) -> k_periodic_rank (bin
+//              atomics) -> k_periodic_bin_scan (bin starts, and the plan
+//              finished from the atom reductions) -> k_scatter;
 //   tnr_count, a batch: k_setup (zeroes the status words; per structure:
 //              batch_ptr checks, active pseudo-inverse, image repeats, grid
 //              frame) -> k_atoms<T, false> -> k_plan (one workgroup per
@@ -260,13 +265,19 @@ static void dispatch_queries(const tnr_request* req, const Layout& L, const Quer
 //   HINT_MOLECULES  every structure a molecule: k_molecule_setup and
 //                   k_struct_scan are the whole prologue (ST_PLAN_HINT for
 //                   any other structure).
-enum CountHint : int { HINT_NONE = 0, HINT_BRUTE = 1, HINT_MOLECULES = 2 };
+//   HINT_PERIODIC   one fully periodic structure planned as a cell list
+//                   whose grid periodic_grid chooses: the periodic fast
+//                   prologue (k_periodic_atoms, k_periodic_rank,
+//                   k_periodic_scatter; ST_PLAN_HINT if it does not apply).
+enum CountHint : int { HINT_NONE = 0, HINT_BRUTE = 1, HINT_MOLECULES = 2, HINT_PERIODIC = 3 };
 
 template <typename T>
 static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                             hipStream_t stream, long long* host_out, int hint) {
     const bool brute_hint = hint == HINT_BRUTE;
-    const bool cell_kernels = req->algorithm != TNR_BRUTE_FORCE && hint == HINT_NONE;
+    const bool periodic = hint == HINT_PERIODIC;
+    const bool cell_kernels =
+        req->algorithm != TNR_BRUTE_FORCE && (hint == HINT_NONE || periodic);
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
     const int reach = req->stencil_reach;  // 0: chosen per structure
@@ -280,6 +291,21 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, v.struct_meta,
                                                 nb, n, v.struct_bin_off, v.struct_unit_off,
                                                 v.recs, v.status, L.cap_bins, 0);
+    } else if (periodic) {
+        // one fully periodic structure: set-up, grid, atoms and bins; ranks;
+        // the bin scan beside the finished plan (k_scatter follows below)
+        const unsigned nblk = blocks_for(n);
+        k_periodic_atoms<T><<<nblk, kBlock, 0, stream>>>(
+            (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc, req->cutoff,
+            n, req->algorithm, reach, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
+            (Vec4<T>*)v.atom_q, v.atom_bin, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins,
+            n_tiles, v.counts, v.struct_bins, v.struct_bin_off, v.struct_units,
+            v.struct_unit_off);
+        k_periodic_rank<<<nblk, kBlock, 0, stream>>>(n, v.atom_bin, v.atom_rank, v.bin_count);
+        k_periodic_bin_scan<T><<<(unsigned)(L.n_tiles_bins + 1), kBlock, 0, stream>>>(
+            (const T*)req->cell, n, req->cutoff, req->algorithm, v.recs, v.block_partials,
+            (int64_t)nblk, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
+            L.cap_bins, v.status, v.bin_count, v.bin_start, v.tiles_bins);
     } else if (nb == 1 && n > 0) {
         // one structure: set-up and atoms, then plan and binning, in two
         // launches; k_single_bin writes the status words
@@ -319,9 +345,10 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                                                            v.atom_rank, v.bin_count, v.status);
     }
     if (n > 0 && cell_kernels) {
-        k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
-            v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
-            v.status + SS_TICKET_BINS, v.status, nullptr);
+        if (!periodic)
+            k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
+                v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
+                v.status + SS_TICKET_BINS, v.status, nullptr);
         k_scatter<T><<<blocks_for(n), kBlock, 0, stream>>>(n, (const Vec4<T>*)v.atom_q,
                                                            v.atom_bin, v.atom_rank,
                                                            v.bin_start, (Vec4<T>*)v.binned,
@@ -760,6 +787,11 @@ int tnr_count_async_hinted(const tnr_request* req, void* workspace, size_t works
     // a hint of brute force only (plan bits 0-1 equal to 1) from an earlier
     // count; with bit 2 every structure was a molecule
     int hint = tnr::HINT_NONE;
+    // a hint of one fully periodic cell-list structure (plan bit 3)
+    if (plan_hint >= 0 && (plan_hint & (int64_t)tnr::kPlanPeriodicGrid) &&
+        (plan_hint & (int64_t)tnr::kPlanFamilies) == 2 && req->n_structures == 1 &&
+        req->n_atoms > 0 && req->algorithm != TNR_BRUTE_FORCE)
+        hint = tnr::HINT_PERIODIC;
     if (plan_hint >= 0 && (plan_hint & (int64_t)tnr::kPlanFamilies) == 1 && req->n_structures > 0 &&
         (req->algorithm == TNR_AUTO || req->algorithm == TNR_BRUTE_FORCE)) {
         if (plan_hint & (int64_t)tnr::kPlanMolecules)
