@@ -114,8 +114,11 @@ __device__ inline void normalize3(double v[3]) {
 // (geometry.cpp:123-219) and the grid frame used for binning, into r.  Grid rows:
 // dual columns on periodic axes (the grid coordinate is the fractional
 // coordinate) and orthonormal complements of the periodic rows elsewhere.
-// Per-structure errors go to the record's flags.
-template <typename T>
+// Per-structure errors go to the record's flags.  OPEN (the molecule plan of
+// a plan hint): only structures without periodic axes are set up; any other
+// raises ST_PLAN_HINT and gets no geometry, and the pseudo-inverse is not
+// compiled in.
+template <typename T, bool OPEN = false>
 __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cells,
                                                 const uint8_t* pbc, int64_t nb, int64_t n_atoms,
                                                 double cutoff, int64_t b, StructRec& r) {
@@ -177,7 +180,8 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     }
     r.nimages = 1;
     double dual_slot[3][3] = {{0, 0, 0}, {0, 0, 0}, {0, 0, 0}};
-    if (finite && natoms > 0) {
+    if (OPEN && k > 0) st |= ST_PLAN_HINT;
+    if (finite && natoms > 0 && !(OPEN && k > 0)) {
         double w[3][3];
 #pragma unroll
         for (int j = 0; j < 3; ++j)
@@ -186,7 +190,9 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
                 w[c][j] = j >= k ? 0.0
                                  : (slot_axis[j] == 0 ? cell[0][c]
                                                       : (slot_axis[j] == 1 ? cell[1][c] : cell[2][c]));
-        if (k > 0 && !active_pinv(w, k, dual_slot)) st |= ST_CELL_RANK;
+        if constexpr (!OPEN) {
+            if (k > 0 && !active_pinv(w, k, dual_slot)) st |= ST_CELL_RANK;
+        }
         int64_t reps[3] = {0, 0, 0};
         if (!(st & ST_CELL_RANK)) {
 #pragma unroll
@@ -251,7 +257,9 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
             if (r.active >> a & 1)
 #pragma unroll
                 for (int c = 0; c < 3; ++c) g[a][c] = dual_axis[c][a];
-        if (k == 2) {
+        if (OPEN) {
+            // no periodic axis: the grid frame is the identity
+        } else if (k == 2) {
             const int i0 = slot_axis[0], i1 = slot_axis[1], ic = slot_axis[2];
             double r0[3], r1[3], nrm[3];
 #pragma unroll
@@ -307,15 +315,36 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     r.flags = st;
 }
 
-// One thread per structure (setup_structure).  Block 0 first zeroes the
-// status block of the request (every later kernel reads it).  Per-structure
-// errors go to the record (k_plan folds them into the status words), so no
-// thread races the zeroing.
+// Structures per workgroup of the per-structure set-up kernels.
+constexpr int kSetupBlock = 64;
+
+// Copies the records of structures [b0, b0 + count) from the workgroup's
+// LDS copies to recs (16-byte words, consecutive threads on consecutive
+// words); every thread calls it.
+__device__ __forceinline__ void store_records(const StructRec* s_recs, StructRec* recs,
+                                              int64_t b0, int64_t count) {
+    static_assert(sizeof(StructRec) % sizeof(int4) == 0, "records copy as 16-byte words");
+    __syncthreads();
+    const int64_t words = count * (int64_t)(sizeof(StructRec) / sizeof(int4));
+    const int4* src = reinterpret_cast<const int4*>(s_recs);
+    int4* dst = reinterpret_cast<int4*>(recs + b0);
+    for (int64_t k = threadIdx.x; k < words; k += blockDim.x) dst[k] = src[k];
+}
+
+// One thread per structure (setup_structure), kSetupBlock per workgroup,
+// each record built in LDS and stored with the workgroup's others
+// (store_records).  Block 0 first zeroes the status block of the request
+// (every later kernel reads it).  Per-structure errors go to the record
+// (k_plan folds them into the status words), so no thread races the zeroing.
 template <typename T>
-__global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb,
-                        int64_t n_atoms, double cutoff, StructRec* recs,
-                        unsigned long long* status) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(kSetupBlock) void k_setup(const int64_t* bp, const T* cells,
+                                                       const uint8_t* pbc, int64_t nb,
+                                                       int64_t n_atoms, double cutoff,
+                                                       StructRec* recs,
+                                                       unsigned long long* status) {
+    __shared__ StructRec s_recs[kSetupBlock];
+    const int64_t b0 = (int64_t)blockIdx.x * kSetupBlock;
+    const int64_t b = b0 + threadIdx.x;
     if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
         __syncthreads();
@@ -326,8 +355,8 @@ __global__ void k_setup(const int64_t* bp, const T* cells, const uint8_t* pbc, i
             status[SS_FLAGS] = st;
         }
     }
-    if (b >= nb) return;
-    setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, recs[b]);
+    if (b < nb) setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, s_recs[threadIdx.x]);
+    if (b0 < nb) store_records(s_recs, recs, b0, min((int64_t)kSetupBlock, nb - b0));
 }
 
 // Structure of atom i: the b in [lo, hi) with bp[b] <= i < bp[b + 1]
@@ -992,29 +1021,21 @@ __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_
                       status, cap_bins, brute_hint);
 }
 
-// The set-up and plan of a request whose structures are all molecules (a
-// plan hint from an earlier count of the same shape), one thread per
-// structure: the set-up of k_setup (block 0 zeroes the status words and the
-// pair scan's tile states), then the molecule plan (brute force with hit
-// masks needs no wraps, no bounds and no bin grid, so k_atoms, k_plan and
-// the cell-list kernels have nothing to do).  k_struct_scan follows.  A
-// structure that is not a molecule under the request's algorithm raises
-// ST_PLAN_HINT in its record, which the scan folds into the status words.
+// The set-up and plan of structure b of a request whose structures are all
+// molecules (a plan hint from an earlier count of the same shape): the
+// set-up of k_setup, then the molecule plan (brute force with hit masks
+// needs no wraps, no bounds and no bin grid, so k_atoms, k_plan and the
+// cell-list kernels have nothing to do).  A structure that is not a molecule
+// under the request's algorithm raises ST_PLAN_HINT in its record, which the
+// batch scan folds into the status words.
 template <typename T>
-__global__ void k_molecule_setup(const int64_t* bp, const T* cells, const uint8_t* pbc,
-                                 int64_t nb, int64_t n_atoms, double cutoff, int requested,
-                                 StructRec* recs, long long* struct_bins,
-                                 long long* struct_units, PlanSummary* meta,
-                                 unsigned long long* status, unsigned long long* tiles,
-                                 int64_t n_tiles) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (blockIdx.x == 0) {
-        for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
-        for (int64_t k = threadIdx.x; k < n_tiles; k += blockDim.x) tiles[k] = 0;
-    }
-    if (b >= nb) return;
-    StructRec& r = recs[b];
-    setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, r);
+__device__ __forceinline__ void molecule_setup_one(const int64_t* bp, const T* cells,
+                                                   const uint8_t* pbc, int64_t nb,
+                                                   int64_t n_atoms, double cutoff, int requested,
+                                                   StructRec& r, long long* struct_bins,
+                                                   long long* struct_units, PlanSummary* meta,
+                                                   int64_t b) {
+    setup_structure<T, true>(bp, cells, pbc, nb, n_atoms, cutoff, b, r);
     const int64_t n = r.natoms;
     long long units = 0;
     if (!(r.flags & kAbortBits) && n > 0) {
@@ -1042,6 +1063,29 @@ __global__ void k_molecule_setup(const int64_t* bp, const T* cells, const uint8_
     struct_bins[b] = 0;
     struct_units[b] = units;
     write_summary(meta + b, r);
+}
+
+// Molecule plan, one thread per structure (molecule_setup_one), kSetupBlock
+// per workgroup with the records built in LDS (store_records); block 0
+// first zeroes the status words and the pair scan's tile states.
+// k_struct_scan follows.
+template <typename T>
+__global__ __launch_bounds__(kSetupBlock) void k_molecule_setup(
+    const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb, int64_t n_atoms,
+    double cutoff, int requested, StructRec* recs, long long* struct_bins,
+    long long* struct_units, PlanSummary* meta, unsigned long long* status,
+    unsigned long long* tiles, int64_t n_tiles) {
+    __shared__ StructRec s_recs[kSetupBlock];
+    const int64_t b0 = (int64_t)blockIdx.x * kSetupBlock;
+    const int64_t b = b0 + threadIdx.x;
+    if (blockIdx.x == 0) {
+        for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
+        for (int64_t k = threadIdx.x; k < n_tiles; k += blockDim.x) tiles[k] = 0;
+    }
+    if (b < nb)
+        molecule_setup_one<T>(bp, cells, pbc, nb, n_atoms, cutoff, requested,
+                              s_recs[threadIdx.x], struct_bins, struct_units, meta, b);
+    if (b0 < nb) store_records(s_recs, recs, b0, min((int64_t)kSetupBlock, nb - b0));
 }
 
 template <typename T>

@@ -780,4 +780,30 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
     }
 }
 
+// Counting or emitting pass of a request whose brute-force structures are
+// all molecules (plan bit kPlanMolecules, or a molecule plan hint): the
+// molecule passes alone, without the registers of the periodic image walk
+// that k_brute also holds, so every unit of a large batch is resident at
+// once.  Exits at once when the request has no brute-force structure.
+template <typename T, int MODE, bool EMIT>
+__global__ __launch_bounds__(kBlock) void k_molecules(QueryArgs<T> a) {
+    if ((load_status(a.status + SS_FLAGS) & kAbortBits) ||
+        !(load_status(a.status + SS_PLAN) & 1))
+        return;
+    if constexpr (EMIT) place_edge_index(a);
+    __shared__ int s_list[kWavesPerBlock][EMIT ? kMolList : 1];
+    const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
+    const int wv = uniform(threadIdx.x / kWave);
+    const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
+    const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    for (int64_t u = wave0; u < units; u += nwaves) {
+        const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+        const StructRec& r = a.recs[b];
+        if constexpr (EMIT)
+            molecule_emit<T, MODE>(a, r, b, u, s_list[wv]);
+        else
+            molecule_count<T, MODE>(a, r, u);
+    }
+}
+
 }  // namespace tnr

@@ -194,12 +194,13 @@ __device__ __forceinline__ void write_summary(PlanSummary* s, const StructRec& r
 // is issued at once (indices clamped to the last structure, values masked),
 // and the batch reductions go through wave reductions and one LDS slot per
 // wave, without atomics.
-__device__ void struct_scan_block(const long long* struct_bins, const long long* struct_units,
-                                  const PlanSummary* meta,
-                                  int64_t nb, int64_t n_atoms, long long* bin_off,
-                                  long long* unit_off, StructRec* recs,
-                                  unsigned long long* status, int64_t cap_bins,
-                                  int brute_hint) {
+__device__ __forceinline__ void struct_scan_block(const long long* struct_bins,
+                                                  const long long* struct_units,
+                                                  const PlanSummary* meta, int64_t nb,
+                                                  int64_t n_atoms, long long* bin_off,
+                                                  long long* unit_off, StructRec* recs,
+                                                  unsigned long long* status, int64_t cap_bins,
+                                                  int brute_hint) {
     __shared__ long long s_carry, s_ucarry, s_mcarry;
     __shared__ unsigned long long s_red[4][kWavesPerBlock];
     if (threadIdx.x == 0) {
@@ -211,32 +212,37 @@ __device__ void struct_scan_block(const long long* struct_bins, const long long*
     unsigned long long flags = 0, plan = 0, images = 0, wrap = 0, nonmol = 0;
     for (int64_t base = 0; base < nb; base += kScanChunk) {
         const int64_t i0 = base + (int64_t)threadIdx.x * kScanItems;
+        // every load of the chunk is issued before the first is used
+        // (indices clamped to the last structure, values masked below)
+        PlanSummary sm[kScanItems];
+        long long bv[kScanItems], uv[kScanItems];
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            const int64_t ic = i0 + k < nb ? i0 + k : nb - 1;
+            sm[k] = meta[ic];
+            bv[k] = struct_bins[ic];
+            uv[k] = struct_units[ic];
+        }
         long long v[kScanItems], u[kScanItems], m[kScanItems];
         long long sum = 0, usum = 0, msum = 0;
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
-            const int64_t i = i0 + k;
-            const bool in = i < nb;
-            const int64_t ic = in ? i : nb - 1;
-            const PlanSummary sm = meta[ic];
-            const long long bv = struct_bins[ic], uv = struct_units[ic];
-            const unsigned long long fl = sm.flags;
-            const int algo = (int)(sm.kind & 0xff);
-            const bool aw = (sm.kind >> 8) & 1, mol = (sm.kind >> 9) & 1;
-            const long long img = sm.img_total, na = sm.natoms;
-            v[k] = in ? bv : 0;
-            u[k] = in ? uv : 0;
+            const bool in = i0 + k < nb;
+            const unsigned long long fl = sm[k].flags;
+            const int algo = (int)(sm[k].kind & 0xff);
+            const bool aw = (sm[k].kind >> 8) & 1, mol = (sm[k].kind >> 9) & 1;
+            const long long img = sm[k].img_total, na = sm[k].natoms;
+            v[k] = in ? bv[k] : 0;
+            u[k] = in ? uv[k] : 0;
             m[k] = in && algo == ALGO_BRUTE ? na : 0;
             sum += v[k];
             usum += u[k];
             msum += m[k];
-            if (in) {
-                flags |= fl;
-                plan |= algo == ALGO_CELL ? 2ull : (algo == ALGO_BRUTE ? 1ull : 0ull);
-                if (algo == ALGO_CELL && aw) wrap = 1;
-                if (algo == ALGO_BRUTE && !mol) nonmol = 1;
-                images += (unsigned long long)img;
-            }
+            flags |= in ? fl : 0ull;
+            plan |= !in ? 0ull : (algo == ALGO_CELL ? 2ull : (algo == ALGO_BRUTE ? 1ull : 0ull));
+            wrap |= in && algo == ALGO_CELL && aw ? 1ull : 0ull;
+            nonmol |= in && algo == ALGO_BRUTE && !mol ? 1ull : 0ull;
+            images += in ? (unsigned long long)img : 0ull;
         }
         long long tot, utot, mtot;
         long long run = block_exclusive_scan(sum, &tot) + s_carry;

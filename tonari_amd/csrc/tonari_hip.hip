@@ -169,15 +169,31 @@ static unsigned emit_blocks(int64_t bins) {
     return (unsigned)(b > 0 ? b : 8);
 }
 
-// Workgroups of the brute-force kernels: one wave per work unit (a batch has
-// at most one unit per atom), no more than the device holds at once (the
-// waves stride over the units; surplus workgroups would only cost dispatch).
-template <typename T, int MODE, bool EMIT>
-static unsigned brute_blocks(int64_t n) {
+// Workgroups of the brute-force kernels (K: k_brute or k_molecules): one
+// wave per work unit (a batch has at most one unit per atom), no more than
+// the device holds at once (the waves stride over the units; surplus
+// workgroups would only cost dispatch).
+template <auto K>
+static unsigned unit_blocks(int64_t n) {
     const int64_t want = (n + kWavesPerBlock - 1) / kWavesPerBlock;
-    const int64_t cap = resident_blocks<k_brute<T, MODE, EMIT>>();
+    const int64_t cap = resident_blocks<K>();
     const int64_t b = want < cap ? want : cap;
     return (unsigned)(b > 0 ? b : 1);
+}
+template <typename T, int MODE, bool EMIT>
+static unsigned brute_blocks(int64_t n) {
+    return unit_blocks<k_brute<T, MODE, EMIT>>(n);
+}
+
+// The brute-force pass of a request: k_molecules when every brute-force
+// structure is known to be a molecule, else k_brute.
+template <typename T, int MODE, bool EMIT>
+static void launch_brute(const QueryArgs<T>& q, int64_t n, bool molecules, hipStream_t stream) {
+    if (molecules)
+        k_molecules<T, MODE, EMIT><<<unit_blocks<k_molecules<T, MODE, EMIT>>(n), kBlock, 0,
+                                     stream>>>(q);
+    else
+        k_brute<T, MODE, EMIT><<<brute_blocks<T, MODE, EMIT>(n), kBlock, 0, stream>>>(q);
 }
 
 template <typename T>
@@ -209,7 +225,8 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
 // Counting: the plan is only known on the device, so with auto both
 // families are launched and each exits at once when the plan has none of
 // its structures, unless plan is 1 (a hint that there is no cell-list
-// structure, checked by the planner).  An explicit brute_force request launches the brute-force
+// structure, checked by the planner) or 5 (every structure a molecule:
+// k_molecules counts).  An explicit brute_force request launches the brute-force
 // kernel only, an explicit cell_list request the cell-list kernel only,
 // which also counts the structures that no bin grid fits (brute force,
 // QueryArgs::brute_in_cell).  Emitting: plan bit 0 launches the
@@ -220,14 +237,16 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
                            int64_t plan, int64_t n_tasks, hipStream_t stream) {
     const int64_t n = req->n_atoms;
     if (n == 0) return;
+    // every brute-force structure a molecule (plan bit 2 with brute force only)
+    const bool molecules = plan >= 0 && (plan & (int64_t)kPlanMolecules) != 0;
     if constexpr (!EMIT) {
-        // plan 1: brute force only (an explicit request or a plan hint)
+        // plan 1: brute force only (an explicit request or a plan hint);
+        // plan 5: molecules only (the molecule plan hint)
         (void)n_tasks;
-        if (req->algorithm != TNR_BRUTE_FORCE && plan != 1)
+        if (req->algorithm != TNR_BRUTE_FORCE && (plan & (int64_t)kPlanFamilies) != 1)
             k_cell_count<T, MODE><<<count_blocks<T, MODE>(2 * (L.cap_bins > n ? L.cap_bins : n)),
                                     kBlock, 0, stream>>>(q);
-        if (req->algorithm != TNR_CELL_LIST)
-            k_brute<T, MODE, false><<<brute_blocks<T, MODE, false>(n), kBlock, 0, stream>>>(q);
+        if (req->algorithm != TNR_CELL_LIST) launch_brute<T, MODE, false>(q, n, molecules, stream);
     } else if (plan < 0) {
         // plan and bins unknown on the host: both families, grids the device
         // holds at once, the kernels reading plan and bins from the status
@@ -239,7 +258,7 @@ static void launch_queries(const tnr_request* req, const Layout& L, const QueryA
     } else {
         if ((plan & 2) && n_tasks > 0)
             k_cell_emit<T, MODE><<<emit_blocks(n_tasks), kBlock, 0, stream>>>(q);
-        if (plan & 1) k_brute<T, MODE, true><<<brute_blocks<T, MODE, true>(n), kBlock, 0, stream>>>(q);
+        if (plan & 1) launch_brute<T, MODE, true>(q, n, molecules, stream);
     }
 }
 
@@ -284,7 +303,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     const int64_t n_tiles =
         (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) + L.n_tiles_pairs;
     if (hint == HINT_MOLECULES) {
-        k_molecule_setup<T><<<blocks_for(nb, 64), 64, 0, stream>>>(
+        k_molecule_setup<T><<<blocks_for(nb, kSetupBlock), kSetupBlock, 0, stream>>>(
             req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, req->algorithm,
             v.recs, v.struct_bins, v.struct_units, v.struct_meta, v.status, v.tiles_pairs,
             L.n_tiles_pairs);
@@ -321,7 +340,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     } else {
         // k_setup zeroes the status words; k_atoms zeroes the bin counters and
         // the tile states of both single-pass scans.
-        k_setup<T><<<blocks_for(nb > 0 ? nb : 1, 64), 64, 0, stream>>>(
+        k_setup<T><<<blocks_for(nb > 0 ? nb : 1, kSetupBlock), kSetupBlock, 0, stream>>>(
             req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, v.recs, v.status);
         if (n > 0)
             k_atoms<T, false><<<blocks_for(n), kBlock, 0, stream>>>(
@@ -357,7 +376,9 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                                                            v.status);
     }
     const QueryArgs<T> q = query_args<T>(req, v);
-    dispatch_queries<T, false>(req, L, q, cell_kernels ? 0 : 1, 0, stream);
+    dispatch_queries<T, false>(
+        req, L, q, cell_kernels ? 0 : (hint == HINT_MOLECULES ? 1 | (int64_t)kPlanMolecules : 1), 0,
+        stream);
     // pairs per source -> offsets; the total (E) goes to the status words
     k_scan_lookback<long long, long long>
         <<<(unsigned)((n + kScanTile - 1) / kScanTile > 0 ? (n + kScanTile - 1) / kScanTile : 1),
