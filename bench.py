@@ -493,25 +493,37 @@ def sweep_cases():
     """Batches of equal structures for the brute-force / cell-list crossover.
 
     Periodic cubic cells at density 0.1 /A^3 (rc 6 A) and 0.05 /A^3 (rc 8 A,
-    more images per structure), and non-periodic Gaussian clusters (rc 5 A),
-    from 4 to 2,048 atoms per structure; about 16,384 atoms per batch.
+    more images per structure), skewed triclinic cells (angles 75, 105, 65
+    degrees, C2's kind of crystal) at density 0.1 /A^3 and rc 6 A, and
+    non-periodic Gaussian clusters (rc 5 A), from 4 to 2,048 atoms per
+    structure, denser around the crossovers; about 16,384 atoms per batch.
     """
     import numpy as np
 
     from tonari_amd import workloads as W
 
     rng = np.random.Generator(np.random.PCG64(2027))
-    for rc, rho in ((6.0, 0.1), (8.0, 0.05)):
-        for n in (4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048):
+    sizes = (4, 8, 16, 32, 48, 64, 80, 96, 112, 128, 160, 192, 256, 512, 1024, 2048)
+    for rc, rho, angles in ((6.0, 0.1, None), (8.0, 0.05, None), (6.0, 0.1, (75.0, 105.0, 65.0))):
+        for n in sizes:
             B = max(1, 16384 // n)
-            edge = (n / rho) ** (1.0 / 3.0)
-            pos = [rng.uniform(0.0, edge, size=(n, 3)) for _ in range(B)]
-            cfg = W._pack(pos, [edge * np.eye(3)] * B, [np.ones(3, bool)] * B, [n] * B,
+            if angles is None:
+                edge = (n / rho) ** (1.0 / 3.0)
+                cell = edge * np.eye(3)
+            else:
+                unit = W.triclinic_cell((1.0, 1.0, 1.0), angles)
+                cell = unit * (n / rho / abs(np.linalg.det(unit))) ** (1.0 / 3.0)
+            frac = [rng.uniform(0.0, 1.0, size=(n, 3)) for _ in range(B)]
+            pos = [f @ cell for f in frac]
+            cfg = W._pack(pos, [cell] * B, [np.ones(3, bool)] * B, [n] * B,
                           np.float32, rc, quantities="PS", algorithm="auto", half_list=False,
                           include_self=False, sorted=False)
-            images = (2 * int(np.ceil(rc / edge)) + 1) ** 3
-            yield f"periodic rho {rho} rc {rc}", n, B, images, cfg
-    for n in (16, 32, 64, 128, 256, 512, 1024, 2048):
+            dual = np.linalg.inv(cell)
+            reps = [int(np.ceil(rc * np.linalg.norm(dual[:, a]))) for a in range(3)]
+            images = int(np.prod([2 * r + 1 for r in reps]))
+            kind = "cubic" if angles is None else "triclinic"
+            yield f"periodic {kind} rho {rho} rc {rc}", n, B, images, cfg
+    for n in (16, 32, 64, 128, 192, 256, 320, 384, 448, 512, 1024, 2048):
         B = max(1, 16384 // n)
         pos = [W._gaussian_molecule(rng, n, sigma=0.5 * n ** (1.0 / 3.0) + 1.0, dmin=0.9)
                for _ in range(B)]
@@ -532,6 +544,8 @@ def auto_sweep(dev, steps: int, warmup: int) -> None:
             res[f"ms_{algorithm}"] = round(ms * 1e3, 4)
             res["pairs"] = pairs
         res["faster"] = min(("brute_force", "cell_list"), key=lambda a: res[f"ms_{a}"])
+        ms_auto, _ = time_public(dict(cfg, algorithm="auto"), t, steps, warmup)
+        res["ms_auto"] = round(ms_auto * 1e3, 4)
         print(json.dumps(res), flush=True)
         del t
 

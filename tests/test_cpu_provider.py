@@ -217,3 +217,71 @@ def test_torch_cpu_finite_difference_gradient():
         return (d ** 2 * torch.exp(-d)).sum()
 
     assert torch.autograd.gradcheck(energy, (pos,), eps=1e-6, atol=1e-6)
+
+
+LAYOUT = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "layout_limit.json")))
+
+
+@pytest.mark.parametrize("case", LAYOUT, ids=lambda c: f"{c['kind']}-{c['dtype']}-{c['L']}")
+def test_cell_list_refusal_matches_the_reference_to_the_ulp(case):
+    # the reference core's outcome for an explicit cell_list at its bin
+    # layout limit (tests/golden/make_layout_golden.py): the last accepted
+    # length and three ulps either side
+    from tests.golden.make_layout_golden import shape
+
+    cfg = shape(case["kind"], float.fromhex(case["L"]), np.dtype(case["dtype"]))
+    args = ("PS", cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"])
+    if case["pairs"] is None:
+        with pytest.raises(RuntimeError, match="cell_list cannot safely process this structure"):
+            neighbor_list(*args, algorithm="cell_list", cpu_threads=2)
+    else:
+        P, _ = neighbor_list(*args, algorithm="cell_list", cpu_threads=2)
+        assert len(P) == case["pairs"]
+
+
+def test_shift_range_message_is_the_cpu_paths():
+    # neighbors_cpu.cpp:266 words it for the cutoff pairs
+    with pytest.raises(RuntimeError, match="^a cell shift required by the cutoff pairs exceeds "
+                                           "the int32 output range$"):
+        neighbor_list("PS", *_single([[-(2**31) + 0.1, 0, 0], [2**31 - 0.8, 0, 0]], np.eye(3),
+                                     [1, 0, 0], 0.5))
+
+
+def test_worker_pool_survives_thread_start_failure():
+    # In a child process whose address space leaves room for only a few
+    # thread stacks, a search asking for 64 threads runs on the workers it
+    # could start (or reports a clean error), never aborting the process;
+    # the same process then searches again.
+    import subprocess
+    import sys
+    import textwrap
+
+    code = textwrap.dedent("""
+        import resource, sys
+        import numpy as np
+        sys.path.insert(0, %r)
+        from tonari_amd import neighbor_list
+        from tonari_amd import workloads as W
+        cfg = W.c4(seed=71, n_atoms=3000)
+        args = ("PS", cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"])
+        P1, S1 = neighbor_list(*args, cpu_threads=1)
+        with open("/proc/self/statm") as fh:
+            vm = int(fh.read().split()[0]) * resource.getpagesize()
+        resource.setrlimit(resource.RLIMIT_AS, (vm + (40 << 20), resource.RLIM_INFINITY))
+        for attempt in range(2):
+            try:
+                P, S = neighbor_list(*args, cpu_threads=64)
+            except RuntimeError as error:
+                print("error:", error)
+                continue
+            assert np.array_equal(P, P1) and np.array_equal(S, S1)
+            print("equal")
+    """) % os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    # one malloc arena: a thread that cannot have its own fails to start
+    # instead of aborting in the C library
+    env = dict(os.environ, MALLOC_ARENA_MAX="1")
+    run = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300,
+                         env=env)
+    assert run.returncode == 0, run.stderr[-2000:]
+    lines = run.stdout.split()
+    assert "equal" in lines or "error:" in lines, run.stdout

@@ -152,10 +152,10 @@ def test_molecule_repeated_calls_with_smaller_batch():
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 def test_molecules_beside_cell_list_structures(dtype):
-    # with algorithm 'auto', small molecules take the molecule form and large
-    # ones, and the periodic box, a cell list: both store hit masks in one
-    # buffer, the molecules in slots counted down from the top
-    sizes = [90, 1500, 40, 700, 2500, 120]
+    # with algorithm 'auto', molecules of up to 2,048 atoms take the molecule
+    # form and larger ones, and the periodic boxes, a cell list: both store
+    # hit masks in one buffer, the molecules in slots counted down from the top
+    sizes = [90, 2600, 40, 700, 2500, 120]
     pbcs = [[0, 0, 0], [0, 0, 0], [0, 0, 0], [1, 1, 1], [1, 1, 1], [0, 0, 0]]
     for mode, (half_list, include_self) in enumerate(
             [(False, False), (False, True), (True, False), (True, True)]):

@@ -70,7 +70,7 @@ def test_more_bins_than_launch_covered():
 
 def test_plan_switch():
     # the same atom count searched by brute force (an open cluster of at
-    # most 384 atoms under auto) and then by a cell list (a periodic box of
+    # most 2,048 atoms under auto) and then by a cell list (a periodic box of
     # 300 x 27 atom images)
     rng = np.random.default_rng(16)
     n = 300
@@ -100,15 +100,15 @@ def _molecules(sizes, seed):
 
 def test_plan_hint_miss_in_a_batch():
     # batches of one shape: molecules that auto searches by brute force
-    # (each at most 384 atoms), then the same atom count with one molecule of
-    # 500 atoms (a cell list), and with a periodic structure (brute force,
-    # not a molecule).  A repeat after a molecules-only plan runs the
+    # (each at most 2,048 atoms), then the same atom count with one molecule
+    # of 2,500 atoms (a cell list), and with a periodic structure (brute
+    # force, not a molecule).  A repeat after a molecules-only plan runs the
     # molecule prologue; the device finds the other structure and the count
     # runs again in full.
-    brute = _molecules([200, 300, 90, 260], 18)
-    mixed = _molecules([500, 150, 100, 100], 19)
-    periodic = _molecules([200, 300, 90, 260], 20)
-    periodic["pbc"][2] = True  # 90 atoms x 27 images: brute force under auto
+    brute = _molecules([1200, 1500, 50, 2000], 18)
+    mixed = _molecules([2500, 1000, 850, 400], 19)
+    periodic = _molecules([1200, 1500, 50, 2000], 20)
+    periodic["pbc"][2] = True  # 50 atoms x 27 images: brute force under auto
     periodic["cell"][2] = np.eye(3, dtype=np.float32) * 25.0
     for cfg in (brute, brute, mixed, brute, mixed, mixed, brute, periodic, periodic, brute):
         check(cfg)
@@ -149,9 +149,9 @@ def test_plan_hint_through_the_abi():
         code = lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err))
         return code, int(n.value), int(host[3]), err.value.decode()
 
-    brute = _molecules([200, 300, 90, 260], 18)
-    mixed = _molecules([500, 150, 100, 100], 19)
-    periodic = _molecules([200, 300, 90, 260], 20)
+    brute = _molecules([1200, 1500, 50, 2000], 18)
+    mixed = _molecules([2500, 1000, 850, 400], 19)
+    periodic = _molecules([1200, 1500, 50, 2000], 20)
     periodic["pbc"][2] = True
     periodic["cell"][2] = np.eye(3, dtype=np.float32) * 25.0
     # hint 1: brute force only; hint 5: every structure a molecule
@@ -168,8 +168,8 @@ def test_plan_hint_through_the_abi():
                 assert code == TNR_RETRY and "plan hint" in msg, (plan, hint)
     # the molecule prologue skips the atom pass: the molecule count checks
     # the positions
-    bad = _molecules([200, 300, 90, 260], 21)
-    bad["positions"][350, 1] = np.nan
+    bad = _molecules([1200, 1500, 50, 2000], 21)
+    bad["positions"][1350, 1] = np.nan
     code, _, _, msg = count(bad, 5)
     assert code != TNR_OK and "finite" in msg
 

@@ -27,14 +27,20 @@
 
 #include "../../../include/tonari_cpu.h"
 
+#include <pthread.h>
+
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <condition_variable>
 #include <cstdint>
 #include <cstring>
+#include <deque>
+#include <exception>
+#include <functional>
 #include <limits>
+#include <mutex>
 #include <new>
-#include <system_error>
 #include <thread>
 #include <vector>
 
@@ -44,7 +50,6 @@ constexpr int kOk = 0, kInputError = 1, kSearchError = 2;
 constexpr int kFloat32 = 0, kFloat64 = 1;
 constexpr int kAuto = 0, kBruteForce = 1, kCellList = 2;
 constexpr int64_t kImageCap = int64_t{1} << 24;        // geometry.cpp:12
-constexpr double kLayoutCap = 67108864.0;              // neighbors_cpu.cpp:379-430
 constexpr int64_t kAutoCandidates = 4096;              // this provider's brute/cell crossover
 constexpr int64_t kSourcesPerTask = 256;  // at most; fewer when that leaves threads idle
 
@@ -90,7 +95,7 @@ const Message kMessages[] = {
     {E_CELL_UNSAFE, kSearchError,
      "cell_list cannot safely process this structure; use algorithm='auto' or 'brute_force'"},
     {E_SHIFT_RANGE, kSearchError,
-     "a cell shift required by the neighbor list exceeds the int32 output range"},
+     "a cell shift required by the cutoff pairs exceeds the int32 output range"},
 };
 
 int put_error(char* err, size_t len, int code, const char* msg) {
@@ -344,26 +349,162 @@ int wrap_of(const double x[3], const double y[3], bool* ok) {
 }
 
 // ------------------------------------------------------------- threads
+//
+// One worker pool per process, as the reference's CPU provider keeps
+// (thread_pool.cpp:22-191): workers are started on demand, kept, and reused
+// by every later call, so a small search with several threads does not pay
+// for starting them.  A job hands out tickets, one per helper it asks for;
+// a worker that takes a ticket runs the job's items with the caller until
+// none are left.  Tickets still queued when the caller has run out of items
+// are withdrawn, so a job never waits for workers busy with another one.
+// A worker that cannot be started leaves the pool smaller (the job runs on
+// fewer threads); an exception thrown by an item stops the job's other
+// items and is rethrown to the caller.  After fork() the child starts a new
+// pool (its parent's workers do not exist in it).
 
-// Runs f(i) for i in [0, n) on `threads` threads (the calling one included),
-// items taken in order from a shared counter.
+class WorkerPool {
+  public:
+    static WorkerPool& instance();
+
+    // f(i) for i in [0, n) on the calling thread and up to `helpers` workers.
+    void run(int64_t n, int64_t helpers, const std::function<void(int64_t)>& f);
+
+  private:
+    struct Job {
+        const std::function<void(int64_t)>* f;
+        int64_t n;
+        std::atomic<int64_t> next{0};
+        std::atomic<bool> stop{false};
+        std::exception_ptr error;  // the first item's exception (under mu_)
+        int running = 0;           // workers inside this job (under mu_)
+        std::condition_variable idle;
+    };
+
+    void grow(int64_t workers);
+    void work(Job& job);
+    void loop();
+
+    std::mutex mu_;
+    std::condition_variable wake_;
+    std::deque<Job*> tickets_;
+    int64_t workers_ = 0;
+};
+
+namespace {
+std::mutex g_pool_mu;
+WorkerPool* g_pool = nullptr;
+bool g_atfork = false;
+
+void pool_prepare() { g_pool_mu.lock(); }
+void pool_parent() { g_pool_mu.unlock(); }
+void pool_child() {
+    // the parent's workers do not exist here: the old pool is left as it is
+    // (its state may be mid-update) and a new one is made on demand
+    g_pool = nullptr;
+    g_pool_mu.unlock();
+}
+
+// Workers at most: a few per hardware thread.
+int64_t worker_cap() {
+    const int64_t hw = (int64_t)std::thread::hardware_concurrency();
+    return std::max<int64_t>(1, std::min<int64_t>(4 * std::max<int64_t>(hw, 1), 1024));
+}
+}  // namespace
+
+WorkerPool& WorkerPool::instance() {
+    std::lock_guard<std::mutex> guard(g_pool_mu);
+    if (!g_atfork) g_atfork = pthread_atfork(pool_prepare, pool_parent, pool_child) == 0;
+    // held until the process ends: workers wait on it until then
+    if (!g_pool) g_pool = new WorkerPool();
+    return *g_pool;
+}
+
+// Workers run with 1 MiB stacks (the search keeps its data on the heap),
+// detached: the pool outlives them.
+void WorkerPool::grow(int64_t workers) {
+    std::lock_guard<std::mutex> guard(mu_);
+    if (workers_ >= workers) return;
+    pthread_attr_t attr;
+    if (pthread_attr_init(&attr) != 0) return;
+    pthread_attr_setstacksize(&attr, size_t{1} << 20);
+    pthread_attr_setdetachstate(&attr, PTHREAD_CREATE_DETACHED);
+    while (workers_ < workers) {
+        pthread_t id;
+        auto entry = [](void* self) -> void* {
+            static_cast<WorkerPool*>(self)->loop();
+            return nullptr;
+        };
+        // a worker that cannot start leaves the pool smaller
+        if (pthread_create(&id, &attr, entry, this) != 0) break;
+        ++workers_;
+    }
+    pthread_attr_destroy(&attr);
+}
+
+void WorkerPool::work(Job& job) {
+    while (!job.stop.load(std::memory_order_relaxed)) {
+        const int64_t i = job.next.fetch_add(1, std::memory_order_relaxed);
+        if (i >= job.n) break;
+        try {
+            (*job.f)(i);
+        } catch (...) {
+            std::lock_guard<std::mutex> guard(mu_);
+            if (!job.error) job.error = std::current_exception();
+            job.stop.store(true, std::memory_order_relaxed);
+        }
+    }
+}
+
+void WorkerPool::loop() {
+    for (;;) {
+        Job* job;
+        {
+            std::unique_lock<std::mutex> lock(mu_);
+            wake_.wait(lock, [this] { return !tickets_.empty(); });
+            job = tickets_.front();
+            tickets_.pop_front();
+            ++job->running;
+        }
+        work(*job);
+        std::lock_guard<std::mutex> guard(mu_);
+        if (--job->running == 0) job->idle.notify_all();
+    }
+}
+
+void WorkerPool::run(int64_t n, int64_t helpers, const std::function<void(int64_t)>& f) {
+    Job job;
+    job.f = &f;
+    job.n = n;
+    grow(helpers);
+    {
+        std::lock_guard<std::mutex> guard(mu_);
+        helpers = std::min(helpers, workers_);
+        for (int64_t k = 0; k < helpers; ++k) tickets_.push_back(&job);
+    }
+    if (helpers == 1)
+        wake_.notify_one();
+    else if (helpers > 1)
+        wake_.notify_all();
+    work(job);
+    std::unique_lock<std::mutex> lock(mu_);
+    tickets_.erase(std::remove(tickets_.begin(), tickets_.end(), &job), tickets_.end());
+    job.idle.wait(lock, [&job] { return job.running == 0; });
+    if (job.error) std::rethrow_exception(job.error);
+}
+
+// Runs f(i) for i in [0, n) on `threads` threads (the calling one included,
+// the others from the process's worker pool), items taken in order from a
+// shared counter.
 template <typename F>
 void parallel_for(int64_t n, int64_t threads, F f) {
     if (n <= 0) return;
-    const int64_t nt = std::max<int64_t>(1, std::min<int64_t>(threads, n));
+    const int64_t nt = std::max<int64_t>(1, std::min({threads, n, worker_cap() + 1}));
     if (nt == 1) {
         for (int64_t i = 0; i < n; ++i) f(i);
         return;
     }
-    std::atomic<int64_t> next{0};
-    auto work = [&]() {
-        for (int64_t i = next.fetch_add(1); i < n; i = next.fetch_add(1)) f(i);
-    };
-    std::vector<std::thread> pool;
-    pool.reserve((size_t)(nt - 1));
-    for (int64_t t = 1; t < nt; ++t) pool.emplace_back(work);
-    work();
-    for (auto& th : pool) th.join();
+    const std::function<void(int64_t)> fn = [&f](int64_t i) { f(i); };
+    WorkerPool::instance().run(n, nt - 1, fn);
 }
 
 // ------------------------------------------------------------- search
@@ -504,6 +645,64 @@ void search_sources(const Structure& r, const T* pos, const T* cell, const Atoms
     }
 }
 
+// Whether the reference's CPU path refuses an explicit cell_list for
+// structure r ("cell_list cannot safely process this structure"), evaluated
+// as it does: the operation scale and padding in long double from the
+// largest |position| per component and the largest |wrap| and |image shift|
+// per axis (neighbors_cpu.cpp:157-218), the search cutoff rounded to T and
+// moved up one ulp, then the dense bin layout over the wrapped positions in
+// T arithmetic, with its caps on bins and bins per atom image
+// (neighbors_cpu.cpp:380-430).
+template <typename T>
+bool reference_refuses_cell_list(const Structure& r, const T* pos, const double cell[3][3],
+                                 const Atoms<T>& at, T cutoff) {
+    constexpr int64_t kDenseBins = int64_t{1} << 26;
+    constexpr int64_t kBinsPerImage = 64;
+    const int64_t a0 = r.atom0, n = r.n;
+    long double maxp[3] = {0.0L, 0.0L, 0.0L};
+    int64_t maxw[3] = {0, 0, 0};
+    T lo[3], hi[3];
+    for (int c = 0; c < 3; ++c) {
+        lo[c] = std::numeric_limits<T>::infinity();
+        hi[c] = -std::numeric_limits<T>::infinity();
+    }
+    for (int64_t i = a0; i < a0 + n; ++i)
+        for (int c = 0; c < 3; ++c) {
+            const T q = at.q[3 * i + c];
+            if (!std::isfinite(q)) return true;
+            maxp[c] = std::max(maxp[c], std::fabs((long double)pos[3 * i + c]));
+            maxw[c] = std::max<int64_t>(maxw[c], std::llabs((long long)at.w[3 * i + c]));
+            lo[c] = std::min(lo[c], q);
+            hi[c] = std::max(hi[c], q);
+        }
+    long double scale = 0.0L;
+    for (int c = 0; c < 3; ++c) {
+        long double comp = 2 * maxp[c];
+        for (int a = 0; a < 3; ++a)
+            comp += (long double)((int64_t)r.reps[a] + 2 * maxw[a]) *
+                    std::fabs((long double)(T)cell[a][c]);
+        scale = std::max(scale, comp);
+    }
+    const long double padded =
+        (long double)cutoff + 64 * (long double)std::numeric_limits<T>::epsilon() * scale;
+    if (!std::isfinite(padded) || padded > 2 * (long double)cutoff ||
+        padded > (long double)std::numeric_limits<T>::max())
+        return true;
+    const T size = std::nextafter((T)padded, std::numeric_limits<T>::infinity());
+    if (!std::isfinite(size) || size == T(0)) return true;
+    int64_t count = 1;
+    for (int c = 0; c < 3; ++c) {
+        const T span = hi[c] - lo[c] + 2 * size;
+        const T dim = span / size;
+        if (!std::isfinite(dim) || dim > (T)kDenseBins) return true;
+        const int64_t d = std::max<int64_t>(1, (int64_t)std::ceil(dim));
+        if (count > kDenseBins / d) return true;
+        count *= d;
+    }
+    if (n > std::numeric_limits<int64_t>::max() / r.nimages) return true;
+    return !(count <= kDenseBins && (count + kBinsPerImage - 1) / kBinsPerImage <= n * r.nimages);
+}
+
 // Plans structure r from its atoms: the broad-phase margin pad = 64 eps_T
 // max(scale, rc) with the operation scale of neighbors_cpu.cpp:156-219
 // (2 max|p| + sum_a (R_a + 2 max|w|) |cell_ac|, maximised over c), the
@@ -539,19 +738,8 @@ void plan_structure(Structure& r, const T* pos, const double cell[3][3], const A
     }
     const double pad = 64.0 * Limits<T>::eps * std::fmax(scale, rc);
     const bool safe = std::isfinite(rc + pad) && rc + pad <= 2 * rc && rc + pad <= Limits<T>::max;
-    if (algorithm == kCellList) {
-        const double size = rc + pad;
-        double count = 1;
-        bool ok = safe;
-        for (int c = 0; c < 3; ++c) {
-            const double span = qhi[c] - qlo[c] + 2 * size;
-            const double dim = span / size;
-            if (!std::isfinite(dim) || dim > kLayoutCap) ok = false;
-            count *= std::fmax(1.0, std::ceil(dim));
-        }
-        if (!ok || count > kLayoutCap || std::ceil(count / 64.0) > (double)n * (double)r.nimages)
-            r.flags |= E_CELL_UNSAFE;
-    }
+    if (algorithm == kCellList && reference_refuses_cell_list<T>(r, pos, cell, at, (T)cutoff))
+        r.flags |= E_CELL_UNSAFE;
     const bool large = (double)n * (double)r.nimages > (double)kAutoCandidates;
     bool want_cell = algorithm == kCellList || (algorithm == kAuto && large);
     if (!safe) want_cell = false;
@@ -839,8 +1027,8 @@ int tnr_cpu_search(int32_t dtype, const void* positions, int64_t n_atoms,
                                   include_self != 0, algorithm, threads, res, err, err_len);
     } catch (const std::bad_alloc&) {
         rc = put_error(err, err_len, kSearchError, "out of host memory");
-    } catch (const std::system_error&) {
-        rc = put_error(err, err_len, kSearchError, "could not start a search thread");
+    } catch (...) {
+        rc = put_error(err, err_len, kSearchError, "the host search failed");
     }
     if (rc != kOk) {
         delete res;
@@ -857,14 +1045,20 @@ void tnr_cpu_copy(const tnr_cpu_result* result, int64_t* pairs, int32_t* shifts,
     const auto& parts = result->parts;
     std::vector<int64_t> off(parts.size() + 1, 0);
     for (size_t k = 0; k < parts.size(); ++k) off[k + 1] = off[k] + (int64_t)(parts[k].idx.size() / 2);
-    tnr_cpu::parallel_for((int64_t)parts.size(), threads < 1 ? 1 : threads, [&](int64_t k) {
+    auto copy = [&](int64_t k) {
         const auto& part = parts[(size_t)k];
         if (part.idx.empty()) return;
         if (pairs)
             std::memcpy(pairs + 2 * off[(size_t)k], part.idx.data(), part.idx.size() * sizeof(int64_t));
         if (shifts)
             std::memcpy(shifts + 3 * off[(size_t)k], part.sh.data(), part.sh.size() * sizeof(int32_t));
-    });
+    };
+    try {
+        tnr_cpu::parallel_for((int64_t)parts.size(), threads < 1 ? 1 : threads, copy);
+    } catch (...) {
+        // the pool could not be reached (out of memory): copy on this thread
+        for (int64_t k = 0; k < (int64_t)parts.size(); ++k) copy(k);
+    }
 }
 
 void tnr_cpu_free(tnr_cpu_result* result) { delete result; }

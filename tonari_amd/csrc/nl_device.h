@@ -25,10 +25,11 @@ constexpr int64_t kImageCap = int64_t{1} << 24;   // geometry.cpp:12
 // algorithm='auto', per structure: brute force at or below these sizes, the
 // crossovers measured on gfx950 (bench.py --auto-sweep, batches of ~16k atoms
 // of equal structures): periodic structures by atoms x images (brute force
-// faster at 1,728, the cell list at 3,456), non-periodic ones by atoms
-// (brute force faster at 256, the cell list at 512).
-constexpr int64_t kAutoBrutePeriodic = 2500;
-constexpr int64_t kAutoBruteIsolated = 384;
+// faster up to 1,296, the cell list from 1,728, in cubic and skewed cells
+// alike), non-periodic ones by atoms (the molecule form of brute force is
+// faster at every size it takes, up to kMoleculeCap = 2,048 atoms).
+constexpr int64_t kAutoBrutePeriodic = 1500;
+constexpr int64_t kAutoBruteIsolated = 2048;
 // Brute force: a work unit takes about this many rounds of one image walk
 // per lane, a round (64 (source, k0, target) triples) costing 1 + (images
 // of one k0 plane) / 4 (most images fall outside the cutoff sphere and are
