@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TNR_ABI_VERSION 5
+#define TNR_ABI_VERSION 6
 
 #define TNR_OK 0
 #define TNR_INPUT_ERROR 1
@@ -207,7 +207,7 @@ typedef struct tnr_skin_list {
     int64_t n_atoms;      /* N of the stored list's request */
     int64_t n_structures; /* B */
     int32_t dtype;
-    int32_t reserved;
+    int32_t pair_mode;    /* the stored list's half_list << 1 | include_self */
     double build_cutoff;  /* cutoff the stored list was searched with */
 } tnr_skin_list;
 
@@ -225,8 +225,9 @@ int tnr_skin_store(const tnr_request* req, double build_cutoff, const int64_t* p
                    size_t workspace_bytes, tnr_skin_list* list, void* stream, char* err,
                    size_t err_len);
 
-/* Filters the stored list at req's positions, cell and cutoff (dtype, N and
- * B as stored) into `out` (P, S, d, D, i, j; no edge_index), rows at and
+/* Filters the stored list at req's positions, cell and cutoff (dtype, N, B,
+ * half_list and include_self as stored; any other request is refused with
+ * TNR_INPUT_ERROR) into `out` (P, S, d, D, i, j; no edge_index), rows at and
  * beyond out->n_pairs being dropped: out->n_pairs = list->n_pairs always
  * suffices.  The status words reach `host_result` (pinned,
  * TNR_HOST_RESULT_SLOTS int64) when the stream has reached this point. */

@@ -292,3 +292,54 @@ def test_sources_recovered_across_tiles_and_empty_structures():
             assert P.shape[0] > 2 * 2048
             t = _walk(t, rng, 0.1)
         assert vl.builds == 1
+
+
+def test_filter_in_another_pair_mode_is_refused():
+    # a list stored in one pair mode holds other pairs than another mode's:
+    # the C ABI records the mode with the list and refuses a filter request
+    # whose half_list or include_self differ (the same mode is accepted)
+    import ctypes
+
+    from tonari_amd._extensions import (
+        ALGORITHMS, TNR_INPUT_ERROR, TNR_OK, Outputs, Request, SkinList, load_torch_hip,
+    )
+
+    lib = load_torch_hip()
+    cfg = W.c4(seed=91, n_atoms=3000)
+    t = _t(cfg)
+    P, S = neighbor_list("PS", t["positions"], t["cell"], t["pbc"], cfg["cutoff"] + 0.5,
+                         t["batch_ptr"])
+    n = P.shape[0]
+
+    def request(half_list, include_self):
+        return Request(
+            dtype=0, algorithm=ALGORITHMS["auto"], n_atoms=t["positions"].shape[0],
+            n_structures=1, positions=t["positions"].data_ptr(),
+            batch_ptr=t["batch_ptr"].data_ptr(), cell=t["cell"].data_ptr(),
+            pbc=t["pbc"].data_ptr(), cutoff=cfg["cutoff"], half_list=int(half_list),
+            include_self=int(include_self), sorted=0, stencil_reach=0,
+        )
+
+    req = request(False, False)
+    ws_bytes = int(lib.tnr_skin_workspace_size(ctypes.byref(req), n))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    lst = SkinList()
+    err = ctypes.create_string_buffer(256)
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.tnr_skin_store(ctypes.byref(req), cfg["cutoff"] + 0.5, P.data_ptr(), S.data_ptr(),
+                              n, ws.data_ptr(), ws_bytes, ctypes.byref(lst), stream, err,
+                              len(err)) == TNR_OK
+    assert lst.pair_mode == 0
+    Pout = torch.empty((n, 2), dtype=torch.int64, device=DEV)
+    out = Outputs(n_pairs=n, plan=0, n_tasks=0, pairs=Pout.data_ptr())
+    host = torch.zeros(8, dtype=torch.int64, pin_memory=True)
+    for half_list, include_self in ((True, False), (False, True), (True, True)):
+        code = lib.tnr_skin_filter_async(ctypes.byref(request(half_list, include_self)),
+                                         ctypes.byref(lst), ws.data_ptr(), ws_bytes,
+                                         ctypes.byref(out), host.data_ptr(), stream, err,
+                                         len(err))
+        assert code == TNR_INPUT_ERROR and b"half_list or include_self" in err.value
+    assert lib.tnr_skin_filter_async(ctypes.byref(req), ctypes.byref(lst), ws.data_ptr(),
+                                     ws_bytes, ctypes.byref(out), host.data_ptr(), stream, err,
+                                     len(err)) == TNR_OK
+    torch.cuda.synchronize()

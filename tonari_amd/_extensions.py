@@ -14,7 +14,7 @@ from functools import lru_cache
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 HOST_RESULT_SLOTS = 8
 
 TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR, TNR_RETRY = 0, 1, 2, 3, 4
@@ -83,7 +83,7 @@ class SkinList(ctypes.Structure):
         ("n_atoms", ctypes.c_int64),
         ("n_structures", ctypes.c_int64),
         ("dtype", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("pair_mode", ctypes.c_int32),
         ("build_cutoff", ctypes.c_double),
     ]
 

@@ -591,6 +591,11 @@ static int check_skin_request(const tnr_request* req, int64_t n_pairs, size_t ws
     return TNR_OK;
 }
 
+// The pair mode of a request as tnr_skin_list::pair_mode records it.
+static int32_t pair_mode(const tnr_request* req) {
+    return (req->half_list ? 2 : 0) | (req->include_self ? 1 : 0);
+}
+
 static int check_skin_list(const tnr_request* req, const tnr_skin_list* list, char* err,
                            size_t err_len) {
     if (!list) return put_error(err, err_len, TNR_INPUT_ERROR, "list is null");
@@ -598,6 +603,10 @@ static int check_skin_list(const tnr_request* req, const tnr_skin_list* list, ch
         list->n_structures != req->n_structures)
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "the request's dtype, N or B differ from the stored list's");
+    // a list stored in one pair mode holds other pairs than another mode's
+    if (list->pair_mode != pair_mode(req))
+        return put_error(err, err_len, TNR_INPUT_ERROR,
+                         "the request's half_list or include_self differ from the stored list's");
     if (!(std::isfinite(list->build_cutoff) && list->build_cutoff >= req->cutoff))
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "the list's build cutoff must be finite and at least the cutoff");
@@ -927,7 +936,7 @@ int tnr_skin_store(const tnr_request* req, double build_cutoff, const int64_t* p
     list->n_atoms = req->n_atoms;
     list->n_structures = req->n_structures;
     list->dtype = req->dtype;
-    list->reserved = 0;
+    list->pair_mode = tnr::pair_mode(req);
     list->build_cutoff = build_cutoff;
     return TNR_OK;
 }
