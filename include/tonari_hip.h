@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TNR_ABI_VERSION 6
+#define TNR_ABI_VERSION 7
 
 #define TNR_OK 0
 #define TNR_INPUT_ERROR 1
@@ -49,7 +49,9 @@ extern "C" {
 #define TNR_RETRY 4 /* tnr_count_finish: a plan hint did not hold; count again without it */
 
 /* Slots of host_result: status flags, E, total periodic images, plan mask,
- * total cell-list bins, two internal tickets, one unused slot. */
+ * total cell-list bins, hit-mask words per atom the count wanted (the
+ * longest row any source or brute-force structure would store; 0 when none
+ * stores masks), one internal ticket, brute-force work units. */
 #define TNR_HOST_RESULT_SLOTS 8
 
 #define TNR_FLOAT32 0
@@ -75,6 +77,13 @@ typedef struct tnr_request {
     int32_t include_self;     /* 0 / 1 */
     int32_t sorted;           /* 0 / 1: sources in index order (see tnr_emit) */
     int32_t stencil_reach;    /* cell-list bins per cutoff along each axis, 1-4; 0 = chosen per structure */
+    int32_t mask_words;       /* 64-bit hit-mask words of workspace per atom, 0-64; 0 = 32.  A
+                                 cell-list bin whose stencil has more chunks of 64 candidates,
+                                 a molecule of more than 64 x mask_words atoms, and k0 slices
+                                 beyond mask_words take paths that store no masks: the results
+                                 are the same, only slower.  host_result[5] of a count gives the
+                                 value that avoids them for the same inputs.  Count and emit
+                                 of one workspace must use the same value. */
 } tnr_request;
 
 /* Output buffers for tnr_emit; any pointer may be NULL (not requested). */
@@ -112,7 +121,8 @@ const char* tnr_device_arch(void);
  * check of src/tonari/_extensions.py:42-48). */
 int tnr_hip_version(void);
 
-/* Device scratch bytes for `req`; depends only on dtype, N and B. */
+/* Device scratch bytes for `req`; depends only on dtype, N, B and mask_words
+ * (0 when mask_words is out of range). */
 size_t tnr_workspace_size(const tnr_request* req);
 
 /*
@@ -137,7 +147,8 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
  * the plan back, bindings_cuda.cpp:96-98,161-185).  tnr_count_async with a
  * plan hint: host_result[3] (the plan mask: bit 0 brute-force structures,
  * bit 1 cell-list structures, bit 2 every brute-force structure a
- * molecule, i.e. without periodic axes and of at most 2,048 atoms, bit 3
+ * molecule, i.e. without periodic axes and of at most 2,048 atoms and
+ * 64 x mask_words atoms, bit 3
  * one fully periodic structure whose bin grid follows from its cell and
  * cutoff) of an earlier count of a request of the same shape, or -1 for
  * none.  Hint 1 (brute force only) with algorithm TNR_AUTO: the cell-list

@@ -59,8 +59,9 @@ def test_version_and_target(lib):
 
 def test_struct_layouts_match_header():
     # offsets of tnr_request / tnr_outputs as laid out by the C compiler
-    assert ctypes.sizeof(ext.Request) == 80
+    assert ctypes.sizeof(ext.Request) == 88
     assert ext.Request.cutoff.offset == 56 and ext.Request.stencil_reach.offset == 76
+    assert ext.Request.mask_words.offset == 80
     assert ctypes.sizeof(ext.Outputs) == 80 and ext.Outputs.targets.offset == 64
     assert ext.Outputs.edge_index.offset == 72
     assert ext.Outputs.n_tasks.offset == 16
@@ -89,6 +90,22 @@ def test_workspace_size(lib):
     assert lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=-1))) == 0
 
 
+def test_workspace_size_follows_mask_words(lib):
+    # the hit-mask area is mask_words 8-byte words per atom (plus one row),
+    # 32 by default; every other sub-buffer is independent of it
+    n = 100_000
+
+    def size(mw):
+        return lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=n, mask_words=mw)))
+
+    assert size(0) == size(32)
+    for mw in (1, 11, 32, 63):
+        grown = size(64) - size(mw)
+        exact = 8 * (n + 1) * (64 - mw)
+        assert abs(grown - exact) < 256, (mw, grown, exact)
+    assert size(-1) == 0 and size(65) == 0
+
+
 def _count_async(lib, req, ws=1 << 24, ws_bytes=None, host=1 << 25):
     err = ctypes.create_string_buffer(256)
     if ws_bytes is None:
@@ -106,6 +123,8 @@ def _count_async(lib, req, ws=1 << 24, ws_bytes=None, host=1 << 25):
         ({"cutoff": 0.0}, "cutoff must be finite and positive"),
         ({"cutoff": float("inf")}, "cutoff must be finite and positive"),
         ({"stencil_reach": 9}, "stencil_reach"),
+        ({"mask_words": 65}, "mask_words must be in \\[0, 64\\]"),
+        ({"mask_words": -2}, "mask_words must be in \\[0, 64\\]"),
         ({"n_atoms": 2**31}, "fewer than 2\\^31 atoms"),
         ({"n_structures": -1}, "invalid sizes"),
     ],

@@ -16,6 +16,7 @@ import torch
 from tests._util import assert_geometry_close, assert_same_keys, keys_of, oracle_call
 from tonari_amd import neighbor_list
 from tonari_amd import workloads as W
+from tonari_amd._torch_frontend import _speculation
 
 pytestmark = pytest.mark.gpu
 
@@ -117,6 +118,22 @@ def test_plan_hint_miss_in_a_batch():
             cfg = dict(brute, half_list=half_list, include_self=include_self)
             for _ in range(2):
                 check(cfg, half_list=half_list, include_self=include_self)
+
+
+def test_molecule_plan_guess_with_a_periodic_structure():
+    # one shape (4,750 atoms in 4 structures): a cell list and molecules
+    # (plan 7), then a cell list, molecules and a small periodic structure
+    # searched by brute force (plan 3, not every brute-force structure a
+    # molecule).  The repeat's speculative emit, launched with plan 7, takes
+    # the molecule kernel, which must write nothing for such a count; the
+    # frontend then emits again with the count's plan.
+    mixed = _molecules([2500, 1000, 850, 400], 22)
+    periodic = _molecules([2500, 1000, 1200, 50], 23)
+    periodic["pbc"][3] = True
+    periodic["cell"][3] = np.eye(3, dtype=np.float32) * 25.0
+    _speculation().clear()
+    for cfg in (mixed, periodic, mixed, mixed, periodic, periodic):
+        check(cfg)
 
 
 def test_plan_hint_through_the_abi():

@@ -14,7 +14,7 @@ from functools import lru_cache
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(HERE, "_lib", "libtonari_hip.so")
-ABI_VERSION = 6
+ABI_VERSION = 7
 HOST_RESULT_SLOTS = 8
 
 TNR_OK, TNR_INPUT_ERROR, TNR_SEARCH_ERROR, TNR_DEVICE_ERROR, TNR_RETRY = 0, 1, 2, 3, 4
@@ -55,6 +55,7 @@ class Request(ctypes.Structure):
         ("include_self", ctypes.c_int32),
         ("sorted", ctypes.c_int32),
         ("stencil_reach", ctypes.c_int32),
+        ("mask_words", ctypes.c_int32),
     ]
 
 

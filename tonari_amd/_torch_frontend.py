@@ -184,7 +184,7 @@ def _host_result(device: torch.device):
 
 
 def _speculation() -> dict:
-    """This thread's last (output capacity, plan, bins) per request shape."""
+    """This thread's last (output capacity, plan, bins, hit-mask words) per request shape."""
     table = getattr(_HOST, "speculation", None)
     if table is None:
         table = _HOST.speculation = {}
@@ -195,6 +195,13 @@ def _speculation() -> dict:
 # 1/32 and a constant, which covers the drift of a molecular-dynamics step.
 def _capacity(n_pairs: int) -> int:
     return n_pairs + (n_pairs >> 5) + 4096
+
+
+# Hit-mask words per atom of the next call's workspace: the longest row the
+# last count wanted (host_result[5]) plus one for the drift of the densest
+# bin; a bin that outgrows it takes the slow path, with the same results.
+def _mask_words(need: int) -> int:
+    return min(need + 1, 64) if need > 0 else 1
 
 
 _ROWS = {
@@ -328,9 +335,6 @@ def neighbor_list_hip(
     with torch.cuda.device(device) if switch else contextlib.nullcontext():
         torch_stream = torch.cuda.current_stream(device)
         stream = torch_stream.cuda_stream
-        ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-        host, host_view, arrived = _host_result(device)
         # the cutoff is part of the shape: a call at another cutoff takes the
         # plain count -> emit path instead of a speculative emit sized for the
         # old one (the cell is not: it drifts a little on every step of NPT
@@ -339,6 +343,12 @@ def neighbor_list_hip(
                req.include_self, req.algorithm, float(req.cutoff), frozenset(want))
         table = _speculation()
         guess = table.get(key)
+        # hit-mask rows sized by the previous call of the shape (first call:
+        # the library's default)
+        req.mask_words = guess[3] if guess is not None else 0
+        ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        host, host_view, arrived = _host_result(device)
         # the previous call of this shape planned brute force only: count
         # without the cell-list kernels (the device checks the hint)
         hint = guess[1] if guess is not None else -1
@@ -351,7 +361,7 @@ def neighbor_list_hip(
         arrived.record(torch_stream)
         out: dict[str, Tensor] = {}
         if guess is not None and want:
-            capacity, plan_guess, bins_guess = guess
+            capacity, plan_guess, bins_guess, _ = guess
             out = _allocate(want, capacity, dtype, device)
             _emit(lib, req, workspace, ws_bytes, out, capacity, plan_guess, bins_guess, stream, err)
         arrived.synchronize()
@@ -373,13 +383,18 @@ def neighbor_list_hip(
         if code != TNR_OK:
             _raise(code, err.value.decode())
         count = int(n_pairs.value)
-        plan, bins = int(host_view[3]), int(host_view[4])
+        plan, bins, mask_need = int(host_view[3]), int(host_view[4]), int(host_view[5])
         if guess is not None and want:
             # after a retried count the speculative emit wrote nothing
+            # the speculative emit covered the count's kernel families (bits
+            # 0-1), took the molecule kernel (bit 2) only if every
+            # brute-force structure is still a molecule, and launched enough
+            # cell-list workgroups
             fits = (
                 not retried
                 and count <= capacity
-                and (plan & ~plan_guess) == 0
+                and (plan & ~plan_guess & 3) == 0
+                and (not plan & 1 or not plan_guess & 4 or plan & 4)
                 and (not plan & 2 or bins <= bins_guess)
             )
             if count > capacity:
@@ -391,7 +406,7 @@ def neighbor_list_hip(
             if count > 0 and out:
                 _emit(lib, req, workspace, ws_bytes, out, count, plan, bins, stream, err)
         out = _rows(out, count)
-        table[key] = (_capacity(count), plan, bins)
+        table[key] = (_capacity(count), plan, bins, _mask_words(mask_need))
         if need_grad:
             out["D"], out["d"] = _FusedGeometry.apply(
                 grad_positions, grad_cell, out["P"], out["S"], batch_ptr, out["D"], out["d"]

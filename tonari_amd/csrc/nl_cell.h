@@ -12,8 +12,9 @@
 // candidate) entries that are written 64 pairs per round, every lane busy
 // and consecutive lanes writing consecutive pairs.
 //
-// Stencils with more than kMapCap candidates take a slow path that decides
-// every candidate in both passes.
+// Stencils with more chunks of 64 candidates than an atom's hit-mask row
+// holds (so always those of more than kMapCap candidates) take a slow path
+// that decides every candidate in both passes.
 //
 // Reference: the cell-list query of csrc/torch/neighbors_cell_cuda.cu:294-442
 // (one warp per source walking linked lists) and csrc/core/neighbors_cpu.cpp:
@@ -649,7 +650,7 @@ __device__ __forceinline__ void emit_bin(const QueryArgs<T>& a, const StencilLds
         const long long cur = lane < ns ? a.offsets[cb.by_bin ? sg + lane : sidx] : 0;
         auto mask_of = [&](int s0_) -> unsigned long long {
             const int gi_ = s0_ + sl;
-            return sl < S && gi_ < ns ? a.masks[(int64_t)(sg + gi_) * kMaskWords + j] : 0ull;
+            return sl < S && gi_ < ns ? a.masks[(int64_t)(sg + gi_) * a.mask_words + j] : 0ull;
         };
         unsigned long long m_next = mask_of(0);
         for (int s0 = 0; s0 < ns; s0 += S) {
@@ -826,7 +827,7 @@ __device__ __forceinline__ void emit_fast(const QueryArgs<T>& a, const StencilLd
             unsigned long long m =
                 it == 0 ? m_pre0
                         : it == 1 ? m_pre1
-                                  : (sl < ns ? a.masks[(int64_t)(sg + sl) * kMaskWords + j] : 0ull);
+                                  : (sl < ns ? a.masks[(int64_t)(sg + sl) * a.mask_words + j] : 0ull);
             int c = __popcll(m);
             int incl = wave_inclusive_scan_i32(c);
             // output range check of each source of the group (lane sl * nch)
@@ -1088,9 +1089,9 @@ __device__ __forceinline__ void emit_staged(const QueryArgs<T>& a, StencilLds& s
         const int j = lane - sl * cb.nch;
         const int s0 = wv * S + sl, s1 = (wv + kWavesPerBlock) * S + sl;
         if (sl < S && s0 < min(nsrc, wv * S + S))
-            m0 = a.masks[(int64_t)(cb.sb + s0) * kMaskWords + j];
+            m0 = a.masks[(int64_t)(cb.sb + s0) * a.mask_words + j];
         if (sl < S && s1 < min(nsrc, (wv + kWavesPerBlock) * S + S))
-            m1 = a.masks[(int64_t)(cb.sb + s1) * kMaskWords + j];
+            m1 = a.masks[(int64_t)(cb.sb + s1) * a.mask_words + j];
     }
     if (WRAPPED)
         stage_wrapped<T>(a, s_st, cb.C, s_cand);
@@ -1112,25 +1113,26 @@ __device__ __forceinline__ void emit_staged(const QueryArgs<T>& a, StencilLds& s
 
 // Emitting pass for one bin whose stencil block_bin has built: staged
 // candidates (emit_staged), the decode path with candidates loaded from
-// global memory (emit_bin) or, beyond the piece map, the slow path.
+// global memory (emit_bin) or, beyond the hit-mask row, the slow path.
 template <typename T, int MODE>
 __device__ __forceinline__ void emit_one_bin(const QueryArgs<T>& a, StencilLds& s_st,
                                              Vec4<T>* s_cand, unsigned short* list,
                                              CellBin<T>& cb, const Vec4<T>& src_all, int wv,
                                              int lane) {
-    if (!cb.wrapped && cb.C <= EmitStageCap<T>::value) {
+    // the count stored hit masks for this bin when its row held them
+    if (cb.nch > a.mask_words) {
+        wave_sources(cb);
+        cell_slow<T, MODE, true>(a, s_st, cb);
+    } else if (!cb.wrapped && cb.C <= EmitStageCap<T>::value) {
         emit_staged<T, false>(a, s_st, s_cand, list, cb, src_all, wv, lane);
     } else if (cb.kwpack && cb.C <= WrapStageCap<T>::value) {
         emit_staged<T, true>(a, s_st, s_cand, list, cb, src_all, wv, lane);
-    } else if (cb.C <= kMapCap) {
+    } else {
         wave_sources(cb);
         if (cb.wrapped)
             emit_bin<T, false, true>(a, s_st, s_cand, cb, list);
         else
             emit_bin<T, false, false>(a, s_st, s_cand, cb, list);
-    } else {
-        wave_sources(cb);
-        cell_slow<T, MODE, true>(a, s_st, cb);
     }
 }
 

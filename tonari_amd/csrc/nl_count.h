@@ -290,7 +290,7 @@ __device__ __forceinline__ void count_pass(const QueryArgs<T>& a, const WaveSten
                 if (lane == sj) mv &= ~(1ull << (sp >> 16));
             }
         }
-        if (lane < NC) a.masks[(int64_t)(sg + gi) * kMaskWords + c0 + lane] = mv;
+        if (lane < NC) a.masks[(int64_t)(sg + gi) * a.mask_words + c0 + lane] = mv;
         acc += lane == gi ? cnt : 0;
     }
     if (bandsrc) {
@@ -310,7 +310,7 @@ __device__ __forceinline__ void count_pass(const QueryArgs<T>& a, const WaveSten
             for (unsigned b = (unsigned)__builtin_amdgcn_readlane(bandv, gi); b != 0u; b &= b - 1u) {
                 const int j = __builtin_ctz(b);
                 kept += band_fixup<T, MODE>(a, st, cb, c0, j, sx, sy, sz, si, sj, sl,
-                                            a.masks + (int64_t)(sg + gi) * kMaskWords + c0 + j);
+                                            a.masks + (int64_t)(sg + gi) * a.mask_words + c0 + j);
             }
             acc += lane == gi ? kept : 0;
         }
@@ -322,7 +322,7 @@ __device__ __forceinline__ void count_pass(const QueryArgs<T>& a, const WaveSten
         for (int gi = 0; gi < ns; ++gi) {
             const int si = as_idx(read_lane(own.w, gi));
             for (int j = 0; j < NC; ++j) {
-                const unsigned long long m = a.masks[(int64_t)(sg + gi) * kMaskWords + c0 + j];
+                const unsigned long long m = a.masks[(int64_t)(sg + gi) * a.mask_words + c0 + j];
                 if ((m >> lane) & 1ull) {
                     const int v = (int)__umul24((unsigned)lane, (unsigned)cb.nch) + c0 + j;
                     const int p = stencil_piece(st, v, cb.npieces);
@@ -387,6 +387,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
     if (load_status(a.status + SS_FLAGS) & kAbortBits) return;
     const unsigned long long plan = load_status(a.status + SS_PLAN);
     const int wv = uniform(threadIdx.x / kWave);
+    int need = 0;  // the longest hit-mask row this wave's sources wanted
     if (plan & 2) {
         constexpr int kCountParts = CountParts<T>::value;
         const int64_t W = a.struct_bin_off[a.nb] * kCountParts;
@@ -403,7 +404,8 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
             const int h = (cb.se - cb.sb + kCountParts - 1) / kCountParts;
             const int s0 = cb.sb + part * h, s1 = min(cb.se, s0 + h);
             if (s0 >= s1) continue;
-            if (cb.C <= kMapCap) {
+            if (cb.C <= kMapCap) need = max(need, cb.nch);
+            if (cb.nch <= a.mask_words) {
                 count_wave_bin<T, MODE>(a, s_lds[wv].st, cb, s0, s1);
             } else {
                 cb.sb = s0;
@@ -422,12 +424,14 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
         for (int64_t u = (int64_t)blockIdx.x * kWavesPerBlock + wv; u < units; u += nwaves) {
             const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
             const StructRec& r = a.recs[b];
-            if (molecule_path(r.active, r.natoms))
+            need = max(need, r.mneed);
+            if (molecule_rec(r))
                 molecule_count<T, MODE>(a, r, u);
             else
                 brute_unit<T, MODE, false, false>(a, u, b, nullptr, s_lds[wv].cur);
         }
     }
+    report_mask_need(a.status, need);
 }
 
 }  // namespace tnr

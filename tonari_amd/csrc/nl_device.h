@@ -78,10 +78,11 @@ enum StatusSlot : int {
                           // bit 2: every brute-force structure is a molecule,
                           // bit 3: the periodic fast prologue applies
     SS_TOTAL_BINS = 4,
-    SS_TICKET_BINS = 5,   // tile tickets of the bin-count scan
+    SS_MASK_NEED = 5,     // hit-mask words per atom the count's sources wanted (maximum)
     SS_TICKET_PAIRS = 6,  // tile tickets of the pair-count scan
     SS_TOTAL_UNITS = 7,   // brute-force work units of the batch
     SS_ANY_WRAP = 8,      // some cell-list atom has a nonzero wrap: binned_w / binned_p are written
+    SS_TICKET_BINS = 9,   // tile tickets of the bin-count scan
     SS_SLOTS = 64,
     kHostResultSlots = 8,  // status words copied to the caller's host buffer
 };
@@ -128,6 +129,8 @@ struct alignas(16) StructRec {
     int32_t bgroup;      // brute force: sources per work unit
     int32_t bslices;     // brute force: work units per source group (slices of k0)
     int32_t bwidth;      // brute force: k0 values per slice
+    int32_t mwords;      // hit-mask words per atom of the request's workspace (1-kMaskWords)
+    int32_t mneed;       // brute force: hit-mask words per atom the structure wants
 };
 
 // The 14 per-structure reductions over atoms, all kept as maxima of
@@ -170,14 +173,20 @@ struct Layout {
 };
 
 // Hit masks stored per cell-list source: one 64-bit word per chunk of 64
-// stencil candidates, for stencils of up to kMaskWords * 64 candidates.
-// Brute-force structures use the same buffer, in slots counted down from
-// the top: the cell-list sources of a request fill slots [0, cell-list
-// atoms) by binned position, its brute-force atoms slots [n - brute-force
-// atoms, n), so the two never meet.  A molecule (below) stores its hit masks
-// there, one word per chunk of 64 targets; a periodic structure whose
-// sources are split into k0 slices stores each slice's pair count.
+// stencil candidates, in a row of `mask words` (the request's, 1 to
+// kMaskWords, 32 by default) per atom.  A bin whose stencil has more chunks
+// than a row holds takes the slow path, which stores no masks, in both
+// passes.  Brute-force structures use the same buffer, in slots counted
+// down from the top: the cell-list sources of a request fill slots [0,
+// cell-list atoms) by binned position, its brute-force atoms slots [n -
+// brute-force atoms, n), so the two never meet.  A molecule (below) stores
+// its hit masks there, one word per chunk of 64 targets; a periodic
+// structure whose sources are split into k0 slices (no more than a row's
+// words) stores each slice's pair count.  The counting passes report the
+// largest row any source wanted (SS_MASK_NEED), so that a caller can size
+// the next call's rows to it.
 constexpr int kMaskWords = 64;
+constexpr int kDefaultMaskWords = 32;
 
 // Molecules: brute-force structures with no periodic axis and at most
 // kMoleculeCap atoms.  They take the hit-mask form of the brute-force
@@ -188,6 +197,15 @@ constexpr int kMoleculeCap = 2048;
 constexpr int kMolUnitWork = 28;
 __host__ __device__ inline bool molecule_path(int active, int64_t natoms) {
     return active == 0 && natoms <= (int64_t)kMoleculeCap;
+}
+// Words of a molecule's hit-mask row (chunks of 64 targets).
+__host__ __device__ inline int molecule_words(int64_t natoms) {
+    return (int)((natoms + 63) / 64);
+}
+// A planned structure takes the molecule passes: a molecule whose row of
+// hit masks fits the request's (otherwise the general brute-force passes).
+__host__ __device__ inline bool molecule_rec(const StructRec& r) {
+    return molecule_path(r.active, r.natoms) && molecule_words(r.natoms) <= r.mwords;
 }
 
 // k0 slices of a periodic brute-force structure, at most (each source's
@@ -202,7 +220,7 @@ constexpr int64_t kScanTile = kBlock * kTileItems;
 
 inline size_t align_up(size_t x) { return (x + 255) & ~size_t(255); }
 
-inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
+inline Layout make_layout(int64_t n, int64_t b, size_t tsize, int mask_words) {
     Layout L{};
     L.cap_bins = 2 * n + 64 * b + 64;
     size_t o = 0;
@@ -231,7 +249,7 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize) {
     L.offsets = take(sizeof(int64_t) * (size_t)(n + 2));
     L.n_atom_blocks = (n + kBlock - 1) / kBlock;
     L.block_partials = take(sizeof(BlockPartial) * (size_t)(L.n_atom_blocks + 1));
-    L.masks = take(sizeof(unsigned long long) * kMaskWords * (size_t)(n + 1));
+    L.masks = take(sizeof(unsigned long long) * (size_t)mask_words * (size_t)(n + 1));
     L.n_tiles_bins = (L.cap_bins + kScanTile - 1) / kScanTile + 1;
     L.n_tiles_pairs = (n + kScanTile - 1) / kScanTile + 1;
     L.tiles_bins = take(sizeof(unsigned long long) * (size_t)L.n_tiles_bins);

@@ -121,7 +121,7 @@ __device__ inline void normalize3(double v[3]) {
 template <typename T, bool OPEN = false>
 __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cells,
                                                 const uint8_t* pbc, int64_t nb, int64_t n_atoms,
-                                                double cutoff, int64_t b, StructRec& r) {
+                                                double cutoff, int mw, int64_t b, StructRec& r) {
     unsigned long long st = 0;
     const int64_t lo = bp[b], hi = bp[b + 1];
     if (b == 0 && lo != 0) st |= ST_BP_START;
@@ -137,6 +137,8 @@ __device__ __forceinline__ void setup_structure(const int64_t* bp, const T* cell
     r.bgroup = 1;
     r.bslices = 1;
     r.bwidth = 1;
+    r.mwords = mw;
+    r.mneed = 0;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         r.lo[a] = 0.0;
@@ -339,7 +341,7 @@ __device__ __forceinline__ void store_records(const StructRec* s_recs, StructRec
 template <typename T>
 __global__ __launch_bounds__(kSetupBlock) void k_setup(const int64_t* bp, const T* cells,
                                                        const uint8_t* pbc, int64_t nb,
-                                                       int64_t n_atoms, double cutoff,
+                                                       int64_t n_atoms, double cutoff, int mw,
                                                        StructRec* recs,
                                                        unsigned long long* status) {
     __shared__ StructRec s_recs[kSetupBlock];
@@ -355,7 +357,8 @@ __global__ __launch_bounds__(kSetupBlock) void k_setup(const int64_t* bp, const 
             status[SS_FLAGS] = st;
         }
     }
-    if (b < nb) setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, b, s_recs[threadIdx.x]);
+    if (b < nb)
+        setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, mw, b, s_recs[threadIdx.x]);
     if (b0 < nb) store_records(s_recs, recs, b0, min((int64_t)kSetupBlock, nb - b0));
 }
 
@@ -443,7 +446,8 @@ __device__ __forceinline__ void grid_coords(const StructRec& r, const T q[3], do
 template <typename T, bool SINGLE>
 __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* bp,
                                                    const T* cells, const uint8_t* pbc,
-                                                   double cutoff, int64_t nb, int64_t n_atoms,
+                                                   double cutoff, int mw, int64_t nb,
+                                                   int64_t n_atoms,
                                                    StructRec* recs, BlockPartial* partials,
                                                    int* atom_struct, int4* atom_wrap,
                                                    Vec4<T>* atom_q, unsigned long long* status,
@@ -472,7 +476,7 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
     // Block-uniform early exit (the barrier below needs every thread).
     if (threadIdx.x == 0) {
         if constexpr (SINGLE) {
-            setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, 0, s_rec);
+            setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, mw, 0, s_rec);
             if (blockIdx.x == 0) recs[0] = s_rec;
             s_flags = s_rec.flags;
             s_atom_flags = 0;
@@ -813,7 +817,8 @@ __device__ __forceinline__ bool choose_grid(const StructRec& r, const unsigned l
 // bgroup consecutive sources, and for periodic structures k0 slices.
 __device__ __forceinline__ int64_t plan_brute_units(StructRec& r, int64_t n) {
     int64_t units = 0;
-    if (molecule_path(r.active, n)) {
+    if (molecule_path(r.active, n)) r.mneed = molecule_words(n);
+    if (molecule_rec(r)) {
         // a molecule: sources x chunks of 64 targets per unit
         const int chunks = (int)((n + kWave - 1) / kWave);
         const int g = (int)min((int64_t)max(kMolUnitWork / chunks, 1), n);
@@ -823,8 +828,9 @@ __device__ __forceinline__ int64_t plan_brute_units(StructRec& r, int64_t n) {
         // a round: 64 (source, k0, target) triples, each walking the
         // K1 x K2 images of its k0 plane, costing about 1 + K1 K2 / 4.
         // A source whose K0 planes exceed a unit's work is split into
-        // slices of k0 (at most kMaskWords: their counts are kept in the
-        // source's hit-mask slot).
+        // slices of k0 (at most kMaxSlices, and no more than the words of
+        // an atom's hit-mask row: their counts are kept in the source's
+        // row).
         const int64_t K0 = 2 * (int64_t)r.reps[0] + 1;
         const double round = 1.0 + 0.25 * (double)r.nimages / (double)K0;
         const double want = fmax(kBruteUnitWork / round, 1.0);     // rounds per unit
@@ -833,8 +839,10 @@ __device__ __forceinline__ int64_t plan_brute_units(StructRec& r, int64_t n) {
         int64_t nsl = 1, width = K0;
         if (g < 1.0) {
             g = 1.0;
-            nsl = (int64_t)fmin(ceil(per_source / want),
-                                (double)(K0 < kMaxSlices ? K0 : kMaxSlices));
+            const int64_t cap = K0 < kMaxSlices ? K0 : kMaxSlices;
+            const int64_t wanted = (int64_t)fmin(ceil(per_source / want), (double)cap);
+            if (wanted > 1) r.mneed = max(r.mneed, (int32_t)wanted);
+            nsl = min(wanted, (int64_t)r.mwords);
             width = (K0 + nsl - 1) / nsl;
             nsl = (K0 + width - 1) / width;
         }
@@ -1031,15 +1039,17 @@ __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_
 template <typename T>
 __device__ __forceinline__ void molecule_setup_one(const int64_t* bp, const T* cells,
                                                    const uint8_t* pbc, int64_t nb,
-                                                   int64_t n_atoms, double cutoff, int requested,
+                                                   int64_t n_atoms, double cutoff, int mw,
+                                                   int requested,
                                                    StructRec& r, long long* struct_bins,
                                                    long long* struct_units, PlanSummary* meta,
                                                    int64_t b) {
-    setup_structure<T, true>(bp, cells, pbc, nb, n_atoms, cutoff, b, r);
+    setup_structure<T, true>(bp, cells, pbc, nb, n_atoms, cutoff, mw, b, r);
     const int64_t n = r.natoms;
     long long units = 0;
     if (!(r.flags & kAbortBits) && n > 0) {
-        const bool molecule = molecule_path(r.active, n) &&
+        if (molecule_path(r.active, n)) r.mneed = molecule_words(n);
+        const bool molecule = molecule_rec(r) &&
                               (requested == TNR_BRUTE_FORCE || n <= kAutoBruteIsolated);
         if (molecule) {
             r.algo = ALGO_BRUTE;
@@ -1072,7 +1082,7 @@ __device__ __forceinline__ void molecule_setup_one(const int64_t* bp, const T* c
 template <typename T>
 __global__ __launch_bounds__(kSetupBlock) void k_molecule_setup(
     const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb, int64_t n_atoms,
-    double cutoff, int requested, StructRec* recs, long long* struct_bins,
+    double cutoff, int mw, int requested, StructRec* recs, long long* struct_bins,
     long long* struct_units, PlanSummary* meta, unsigned long long* status,
     unsigned long long* tiles, int64_t n_tiles) {
     __shared__ StructRec s_recs[kSetupBlock];
@@ -1083,7 +1093,7 @@ __global__ __launch_bounds__(kSetupBlock) void k_molecule_setup(
         for (int64_t k = threadIdx.x; k < n_tiles; k += blockDim.x) tiles[k] = 0;
     }
     if (b < nb)
-        molecule_setup_one<T>(bp, cells, pbc, nb, n_atoms, cutoff, requested,
+        molecule_setup_one<T>(bp, cells, pbc, nb, n_atoms, cutoff, mw, requested,
                               s_recs[threadIdx.x], struct_bins, struct_units, meta, b);
     if (b0 < nb) store_records(s_recs, recs, b0, min((int64_t)kSetupBlock, nb - b0));
 }
@@ -1239,7 +1249,7 @@ __global__ __launch_bounds__(kBlock) void k_single_bin(
             status[SS_PLAN] = r.algo == ALGO_CELL
                                   ? (s_fast ? 2ull | kPlanPeriodicGrid : 2ull)
                                   : (r.algo == ALGO_BRUTE
-                                         ? (molecule_path(r.active, r.natoms) ? 1ull | kPlanMolecules
+                                         ? (molecule_rec(r) ? 1ull | kPlanMolecules
                                                                               : 1ull)
                                          : 0ull);
             status[SS_TOTAL_IMAGES] = images;
@@ -1322,7 +1332,7 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
 // per-source pair counts.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
-    const T* pos, const int64_t* bp, const T* cells, const uint8_t* pbc, double cutoff,
+    const T* pos, const int64_t* bp, const T* cells, const uint8_t* pbc, double cutoff, int mw,
     int64_t n_atoms, int requested, int reach_target, StructRec* recs, BlockPartial* partials,
     int* atom_struct, int4* atom_wrap, Vec4<T>* atom_q, int* atom_bin,
     unsigned long long* status, int* bin_count, int64_t n_bin_count, unsigned long long* tiles,
@@ -1346,7 +1356,7 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
 #pragma unroll
     for (int c = 0; c < 3; ++c) p_pre[c] = pos[3 * ic + c];
     if (tid == 0) {
-        setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, 0, s_rec);
+        setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, mw, 0, s_rec);
         s_atom_flags = 0;
     }
     __syncthreads();

@@ -30,9 +30,10 @@ struct QueryArgs {
     long long* counts;
     const long long* offsets;
     unsigned long long* status;
-    unsigned long long* masks;      // kMaskWords hit masks per binned cell-list source
+    unsigned long long* masks;      // mask_words hit masks per atom slot
     int64_t n_atoms;
     int64_t nb;
+    int mask_words;  // words of an atom's hit-mask row (1 to kMaskWords)
     // without `sorted`: when every structure is searched with a cell list
     // (status plan 2), pair counts and output offsets are indexed by binned
     // position, so sources take the outputs in binned order and every
@@ -70,6 +71,16 @@ __device__ __forceinline__ void place_edge_index(QueryArgs<T>& a) {
 
 // Value of x held by the first active lane, as a wave-uniform (scalar) value.
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// A counting wave's longest wanted hit-mask row (wave-uniform) into the
+// status word SS_MASK_NEED, by one atomic maximum from the waves that raise it.
+__device__ __forceinline__ void report_mask_need(unsigned long long* status, int need) {
+    if (need <= 0 || lane_id() != 0) return;
+    unsigned long long* slot = status + SS_MASK_NEED;
+    if ((unsigned long long)need >
+        __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        atomicMax(slot, (unsigned long long)need);
+}
 
 template <typename T>
 struct Triple {
@@ -485,7 +496,7 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
     const int k0a = -g.R0 + sl * r.bwidth;
     const int W = min(r.bwidth, g.R0 - k0a + 1);  // k0 values of the slice
     // slice counts of the unit's sources: hit-mask slot words
-    unsigned long long* slice_cnt = a.masks + (r.mask0 + f) * kMaskWords;
+    unsigned long long* slice_cnt = a.masks + (r.mask0 + f) * a.mask_words;
     const int lane = lane_id();
     const bool staged = STAGE && n <= kBruteStage;
     if (staged) {
@@ -499,7 +510,7 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
     for (int x = lane; x < G; x += kWave) {
         if (EMIT) {
             long long o = a.offsets[a0 + f + x];
-            for (int j = 0; j < sl; ++j) o += (long long)slice_cnt[(int64_t)x * kMaskWords + j];
+            for (int j = 0; j < sl; ++j) o += (long long)slice_cnt[(int64_t)x * a.mask_words + j];
             C.cur[x] = o;
         } else {
             C.cnt[x] = 0;
@@ -593,7 +604,7 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
             if (nsl == 1) {
                 a.counts[a0 + f + x] = c;
             } else {
-                slice_cnt[(int64_t)x * kMaskWords + sl] = (unsigned long long)c;
+                slice_cnt[(int64_t)x * a.mask_words + sl] = (unsigned long long)c;
                 atomicAdd(reinterpret_cast<unsigned long long*>(a.counts + a0 + f + x),
                           (unsigned long long)c);
             }
@@ -619,7 +630,7 @@ __device__ __forceinline__ void brute_unit(const QueryArgs<T>& a, int64_t u, int
 //   Counting: lane l holds target 64 c + l of each chunk c of a register
 //   pass; each source is read from the lane that holds it, and one ballot
 //   per (source, chunk) gives the hit mask, stored in the hit-mask buffer
-//   from the structure's slot mask0 on (kMaskWords words per atom).
+//   from the structure's slot mask0 on (a row of mask_words words per atom).
 //   Emitting: the unit's masks are decoded into a list of (source, target)
 //   entries in the wave's LDS, in source and target order, and written 64
 //   pairs per round.  The unit's sources are consecutive atoms, so their
@@ -692,7 +703,7 @@ __device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const Stru
                 }
             });
             if (lane < np)
-                a.masks[(r.mask0 + s) * kMaskWords + c0 + lane] =
+                a.masks[(r.mask0 + s) * a.mask_words + c0 + lane] =
                     ((unsigned long long)(unsigned)mhi << 32) | (unsigned)mlo;
             cnt += lane == g ? hits : 0;
         }
@@ -713,7 +724,7 @@ __device__ __forceinline__ void molecule_emit(const QueryArgs<T>& a, const Struc
     unsigned long long mw = 0;  // lane g * nch + j: mask of source f + g, chunk j
     if (lane < nw) {
         const int g = lane / nch;
-        mw = a.masks[(r.mask0 + f + g) * kMaskWords + (lane - g * nch)];
+        mw = a.masks[(r.mask0 + f + g) * a.mask_words + (lane - g * nch)];
     }
     const T* cell = a.cells + 9 * b;
     T c[9];
@@ -766,10 +777,12 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
     const int wv = uniform(threadIdx.x / kWave);
     const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    int need = 0;  // counting: the longest hit-mask row the wave's structures want
     for (int64_t u = wave0; u < units; u += nwaves) {
         const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
         const StructRec& r = a.recs[b];
-        if (molecule_path(r.active, r.natoms)) {
+        if constexpr (!EMIT) need = max(need, r.mneed);
+        if (molecule_rec(r)) {
             if constexpr (EMIT)
                 molecule_emit<T, MODE>(a, r, b, u, s_lds[wv].mol);
             else
@@ -778,17 +791,22 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
             brute_unit<T, MODE, EMIT>(a, u, b, &s_lds[wv].walk, s_lds[wv].walk.c);
         }
     }
+    if constexpr (!EMIT) report_mask_need(a.status, need);
 }
 
 // Counting or emitting pass of a request whose brute-force structures are
 // all molecules (plan bit kPlanMolecules, or a molecule plan hint): the
 // molecule passes alone, without the registers of the periodic image walk
 // that k_brute also holds, so every unit of a large batch is resident at
-// once.  Exits at once when the request has no brute-force structure.
+// once.  Exits at once when the request has no brute-force structure, or
+// when the count found one that is not a molecule (an emit launched with an
+// earlier call's plan: it writes nothing, and the caller, seeing the
+// count's plan, emits again).
 template <typename T, int MODE, bool EMIT>
 __global__ __launch_bounds__(kBlock) void k_molecules(QueryArgs<T> a) {
-    if ((load_status(a.status + SS_FLAGS) & kAbortBits) ||
-        !(load_status(a.status + SS_PLAN) & 1))
+    const unsigned long long plan = load_status(a.status + SS_PLAN);
+    if ((load_status(a.status + SS_FLAGS) & kAbortBits) || !(plan & 1) ||
+        !(plan & kPlanMolecules))
         return;
     if constexpr (EMIT) place_edge_index(a);
     __shared__ int s_list[kWavesPerBlock][EMIT ? kMolList : 1];
@@ -796,14 +814,18 @@ __global__ __launch_bounds__(kBlock) void k_molecules(QueryArgs<T> a) {
     const int wv = uniform(threadIdx.x / kWave);
     const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    int need = 0;  // counting: the longest hit-mask row the wave's molecules want
     for (int64_t u = wave0; u < units; u += nwaves) {
         const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
         const StructRec& r = a.recs[b];
-        if constexpr (EMIT)
+        if constexpr (EMIT) {
             molecule_emit<T, MODE>(a, r, b, u, s_list[wv]);
-        else
+        } else {
+            need = max(need, r.mneed);
             molecule_count<T, MODE>(a, r, u);
+        }
     }
+    if constexpr (!EMIT) report_mask_need(a.status, need);
 }
 
 }  // namespace tnr

@@ -179,7 +179,7 @@ __device__ __forceinline__ void write_summary(PlanSummary* s, const StructRec& r
     x.img_total = r.img_total;
     x.natoms = r.natoms;
     x.kind = (long long)r.algo | (r.any_wrap ? 1ll << 8 : 0ll) |
-             (molecule_path(r.active, r.natoms) ? 1ll << 9 : 0ll);
+             (molecule_rec(r) ? 1ll << 9 : 0ll);
     *s = x;
 }
 

@@ -196,6 +196,11 @@ static void launch_brute(const QueryArgs<T>& q, int64_t n, bool molecules, hipSt
         k_brute<T, MODE, EMIT><<<brute_blocks<T, MODE, EMIT>(n), kBlock, 0, stream>>>(q);
 }
 
+// Words of an atom's hit-mask row: the request's, or the default.
+static int mask_words(const tnr_request* req) {
+    return req->mask_words > 0 ? (int)req->mask_words : kDefaultMaskWords;
+}
+
 template <typename T>
 static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     QueryArgs<T> q{};
@@ -215,6 +220,7 @@ static QueryArgs<T> query_args(const tnr_request* req, const Views& v) {
     q.offsets = v.offsets;
     q.status = v.status;
     q.masks = v.masks;
+    q.mask_words = mask_words(req);
     q.n_atoms = req->n_atoms;
     q.nb = req->n_structures;
     q.by_bin = req->sorted ? 0 : 1;
@@ -300,11 +306,12 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     const Views v = views(ws, L);
     const int64_t n = req->n_atoms, nb = req->n_structures;
     const int reach = req->stencil_reach;  // 0: chosen per structure
+    const int mw = mask_words(req);
     const int64_t n_tiles =
         (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) + L.n_tiles_pairs;
     if (hint == HINT_MOLECULES) {
         k_molecule_setup<T><<<blocks_for(nb, kSetupBlock), kSetupBlock, 0, stream>>>(
-            req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, req->algorithm,
+            req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, mw, req->algorithm,
             v.recs, v.struct_bins, v.struct_units, v.struct_meta, v.status, v.tiles_pairs,
             L.n_tiles_pairs);
         k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, v.struct_meta,
@@ -316,7 +323,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         const unsigned nblk = blocks_for(n);
         k_periodic_atoms<T><<<nblk, kBlock, 0, stream>>>(
             (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc, req->cutoff,
-            n, req->algorithm, reach, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
+            mw, n, req->algorithm, reach, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
             (Vec4<T>*)v.atom_q, v.atom_bin, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins,
             n_tiles, v.counts, v.struct_bins, v.struct_bin_off, v.struct_units,
             v.struct_unit_off);
@@ -330,7 +337,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         // launches; k_single_bin writes the status words
         k_atoms<T, true><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc, req->cutoff,
-            nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q,
+            mw, nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap, (Vec4<T>*)v.atom_q,
             v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles, v.counts);
         k_single_bin<T><<<blocks_for(n), kBlock, 0, stream>>>(
             (const T*)req->cell, n, req->cutoff, req->algorithm, reach, v.recs, v.block_partials,
@@ -341,11 +348,12 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         // k_setup zeroes the status words; k_atoms zeroes the bin counters and
         // the tile states of both single-pass scans.
         k_setup<T><<<blocks_for(nb > 0 ? nb : 1, kSetupBlock), kSetupBlock, 0, stream>>>(
-            req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, v.recs, v.status);
+            req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, mw, v.recs,
+            v.status);
         if (n > 0)
             k_atoms<T, false><<<blocks_for(n), kBlock, 0, stream>>>(
                 (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc,
-                req->cutoff, nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
+                req->cutoff, mw, nb, n, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
                 (Vec4<T>*)v.atom_q, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins, n_tiles,
                 v.counts);
         // a single structure is planned and scanned by one workgroup
@@ -455,6 +463,8 @@ static int check_request(const tnr_request* req, size_t ws_bytes, const void* ws
                          "positions must have dtype float32 or float64");
     if (req->stencil_reach < 0 || req->stencil_reach > 4)
         return put_error(err, err_len, TNR_INPUT_ERROR, "stencil_reach must be in [0, 4]");
+    if (req->mask_words < 0 || req->mask_words > kMaskWords)
+        return put_error(err, err_len, TNR_INPUT_ERROR, "mask_words must be in [0, 64]");
     if (req->algorithm < TNR_AUTO || req->algorithm > TNR_CELL_LIST)
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "algorithm must be 'auto', 'brute_force', or 'cell_list'");
@@ -466,7 +476,8 @@ static int check_request(const tnr_request* req, size_t ws_bytes, const void* ws
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "the current implementation supports fewer than 2^31 atoms");
     *L = make_layout(req->n_atoms, req->n_structures,
-                     req->dtype == TNR_FLOAT32 ? sizeof(float) : sizeof(double));
+                     req->dtype == TNR_FLOAT32 ? sizeof(float) : sizeof(double),
+                     mask_words(req));
     if (L->cap_bins >= (int64_t{1} << 31))
         return put_error(err, err_len, TNR_INPUT_ERROR,
                          "the current implementation supports fewer than 2^31 atoms");
@@ -787,9 +798,12 @@ const char* tnr_device_arch(void) { return TNR_OFFLOAD_ARCH; }
 int tnr_hip_version(void) { return HIP_VERSION_MAJOR * 100 + HIP_VERSION_MINOR; }
 
 size_t tnr_workspace_size(const tnr_request* req) {
-    if (!req || req->n_atoms < 0 || req->n_structures < 0) return 0;
+    if (!req || req->n_atoms < 0 || req->n_structures < 0 || req->mask_words < 0 ||
+        req->mask_words > tnr::kMaskWords)
+        return 0;
     return tnr::make_layout(req->n_atoms, req->n_structures,
-                            req->dtype == TNR_FLOAT32 ? sizeof(float) : sizeof(double))
+                            req->dtype == TNR_FLOAT32 ? sizeof(float) : sizeof(double),
+                            tnr::mask_words(req))
         .total;
 }
 
