@@ -87,13 +87,16 @@ def time_phases(cfg, t, reps: int):
 
     Drives the C ABI as a repeated call of the frontend does, on torch's
     current stream: events around tnr_count_async and around the tnr_emit
-    queued right behind it, one request per repetition.  For a cell-list
+    queued right behind it, one request per repetition, with the hit-mask
+    rows the frontend gives a repeat (the first, untimed repetition's
+    reported width plus one).  For a cell-list
     workload tnr_emit launches one kernel (the cell-list emit), so the second
     interval is that kernel's duration in its place in the request.
     """
     import torch
 
     from tonari_amd._extensions import ALGORITHMS, Outputs, Request, load_torch_hip
+    from tonari_amd._torch_frontend import _mask_words
 
     lib = load_torch_hip()
     pos = t["positions"]
@@ -143,6 +146,11 @@ def time_phases(cfg, t, reps: int):
             shapes = {"P": ((E, 2), torch.int64), "S": ((E, 3), torch.int32),
                       "i": ((E,), torch.int64), "j": ((E,), torch.int64),
                       "d": ((E,), dt), "D": ((E, 3), dt)}
+            # hit-mask rows as the frontend sizes a repeat: the width this
+            # count reported, plus one
+            req.mask_words = _mask_words(int(host[5]))
+            ws_bytes = int(lib.tnr_workspace_size(ctypes.byref(req)))
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
             o = []
             for _ in range(2):
                 out = {q: torch.empty(shapes[q][0], dtype=shapes[q][1], device=dev)

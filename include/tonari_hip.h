@@ -77,7 +77,7 @@ typedef struct tnr_request {
     int32_t include_self;     /* 0 / 1 */
     int32_t sorted;           /* 0 / 1: sources in index order (see tnr_emit) */
     int32_t stencil_reach;    /* cell-list bins per cutoff along each axis, 1-4; 0 = chosen per structure */
-    int32_t mask_words;       /* 64-bit hit-mask words of workspace per atom, 0-64; 0 = 32.  A
+    int32_t mask_words;       /* 64-bit hit-mask words of workspace per atom, 0-64; 0 = 64.  A
                                  cell-list bin whose stencil has more chunks of 64 candidates,
                                  a molecule of more than 64 x mask_words atoms, and k0 slices
                                  beyond mask_words take paths that store no masks: the results

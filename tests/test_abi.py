@@ -92,13 +92,13 @@ def test_workspace_size(lib):
 
 def test_workspace_size_follows_mask_words(lib):
     # the hit-mask area is mask_words 8-byte words per atom (plus one row),
-    # 32 by default; every other sub-buffer is independent of it
+    # 64 by default; every other sub-buffer is independent of it
     n = 100_000
 
     def size(mw):
         return lib.tnr_workspace_size(ctypes.byref(_request(n_atoms=n, mask_words=mw)))
 
-    assert size(0) == size(32)
+    assert size(0) == size(64)
     for mw in (1, 11, 32, 63):
         grown = size(64) - size(mw)
         exact = 8 * (n + 1) * (64 - mw)

@@ -106,8 +106,8 @@ def sweep(cfg, algorithm, widths, **kw):
     # the workspace grows with the width, 8 bytes per atom and word
     ordered = [sizes[w] for w in sorted(sizes)]
     assert ordered == sorted(ordered)
-    if 32 in sizes:
-        assert sizes[32] == ws_default
+    if 64 in sizes:
+        assert sizes[64] == ws_default
     return need
 
 

@@ -174,7 +174,7 @@ struct Layout {
 
 // Hit masks stored per cell-list source: one 64-bit word per chunk of 64
 // stencil candidates, in a row of `mask words` (the request's, 1 to
-// kMaskWords, 32 by default) per atom.  A bin whose stencil has more chunks
+// kMaskWords, kMaskWords by default) per atom.  A bin whose stencil has more chunks
 // than a row holds takes the slow path, which stores no masks, in both
 // passes.  Brute-force structures use the same buffer, in slots counted
 // down from the top: the cell-list sources of a request fill slots [0,
@@ -186,7 +186,7 @@ struct Layout {
 // largest row any source wanted (SS_MASK_NEED), so that a caller can size
 // the next call's rows to it.
 constexpr int kMaskWords = 64;
-constexpr int kDefaultMaskWords = 32;
+constexpr int kDefaultMaskWords = kMaskWords;
 
 // Molecules: brute-force structures with no periodic axis and at most
 // kMoleculeCap atoms.  They take the hit-mask form of the brute-force
