@@ -4,9 +4,10 @@ The reference's CPU path refuses an explicit cell_list when its dense bin
 layout would hold more than 64 bins per atom image (or more than 2^26 bins)
 (``csrc/core/neighbors_cpu.cpp:380-430``), with a search cutoff padded in
 long double and rounded up to the input type (``neighbors_cpu.cpp:157-218``).
-This script finds, for a few non-periodic shapes whose layout grows with one
-length L, the last L (to the ulp of the input type) that the reference
-accepts, and records that L and its neighbours a few ulps either side with
+This script finds, for a few shapes whose layout grows with one length L
+(non-periodic lines, a slab periodic in x and y whose padding comes from
+wrapped atoms and images, and a sparse fully periodic box), the last L (to the ulp of the input type) that
+the reference accepts, and records that L and its neighbours a few ulps either side with
 the reference's outcome: the pair count, or "refused".  Inputs are written
 as exact hexadecimal floats, so the fixture holds only data.
 
@@ -42,6 +43,33 @@ def shape(kind: str, L: float, dtype) -> dict:
         # three atoms up to L apart on x, one off-axis at 0.75 (a pair)
         pos = [[0.0, 0.0, 0.0], [L, 0.0, 0.0], [0.0, 0.75, 0.0]]
         rc = 1.0
+    elif kind == "slab":
+        # a skewed slab periodic in x and y (9 images) whose layout grows
+        # with the z extent L; one atom far along x, wrapped by hundreds
+        # (float32) or tens of thousands (float64) of cells, makes the x
+        # component of the operation scale, with its image and wrap terms,
+        # set the padding
+        far = 1000.37 if np.dtype(dtype) == np.float32 else 123456.789
+        pos = [[far, 0.5, 0.0], [0.25, 0.61, L], [-77.3, 2.9, 0.4]]
+        cell = np.array([[[4.1, 0.3, 0.0], [0.2, 3.9, 0.0], [0.0, 0.0, 0.0]]], dtype=dtype)
+        return {
+            "positions": np.asarray(pos, dtype=dtype),
+            "cell": cell,
+            "pbc": np.array([[True, True, False]]),
+            "batch_ptr": np.array([0, len(pos)], dtype=np.int64),
+            "cutoff": 1.0,
+        }
+    elif kind == "box":
+        # a fully periodic cubic cell of edge L (27 images) holding three
+        # atoms, one of them wrapped by (1, -1, 2) cells, spread over the cell
+        pos = [[0.1, 0.2, 0.3], [0.93 * L, 0.91 * L, 0.95 * L], [L + 0.3, -0.2, 2 * L + 0.5]]
+        return {
+            "positions": np.asarray(pos, dtype=dtype),
+            "cell": (np.eye(3)[None] * L).astype(dtype),
+            "pbc": np.ones((1, 3), dtype=bool),
+            "batch_ptr": np.array([0, len(pos)], dtype=np.int64),
+            "cutoff": 1.0,
+        }
     else:  # "offset": the line of two atoms 1000 A from the origin
         pos = [[1000.0, -3.0, 2.0], [1000.0 + L, -3.0, 2.0]]
         rc = 1.5
@@ -87,7 +115,8 @@ def main() -> None:
     if not oracle.available("reference"):
         oracle.build(reference=True)
     cases = []
-    for kind, lo, hi in (("line2", 29.0, 31.0), ("line3", 28.0, 33.0), ("offset", 43.0, 47.0)):
+    for kind, lo, hi in (("line2", 29.0, 31.0), ("line3", 28.0, 33.0), ("offset", 43.0, 47.0),
+                         ("slab", 80.0, 120.0), ("box", 15.0, 16.0)):
         for dtype in (np.float32, np.float64):
             t = np.dtype(dtype).type
             last = t(boundary(kind, dtype, lo, hi))

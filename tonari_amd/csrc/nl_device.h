@@ -94,6 +94,18 @@ constexpr unsigned long long kPlanMolecules = 4;  // plan bit 2
 // fast prologue chooses (periodic_grid holds), a hint for the next count
 constexpr unsigned long long kPlanPeriodicGrid = 8;
 
+// The 18 per-structure reductions over atoms, all kept as maxima of
+// "max-keys": kRedUlo + a / kRedUhi + a are the lower / upper bounds of the
+// grid coordinate on axis a, kRedClo + c / kRedChi + c those of the wrapped
+// Cartesian coordinate c, kRedP + c is max |p_c| and kRedW + a max |wrap_a|
+// (per component and axis, as the reference's cell-list padding takes them).
+// Lower bounds are stored complemented so that every reduction is a
+// maximum and 0 is the identity.  For float inputs the keys are 32-bit
+// (grid bounds rounded outward; Cartesian bounds and |p| exact); for double
+// inputs they are 64-bit and exact.
+enum RedSlot : int { kRedUlo = 0, kRedUhi = 3, kRedClo = 6, kRedChi = 9, kRedP = 12, kRedW = 15,
+                     kRedCount = 18 };
+
 // One record per structure.  Filled by k_setup (geometry), k_atoms
 // (reductions of atoms in blocks that span several structures) and k_plan
 // (margins, algorithm and bin grid).
@@ -113,7 +125,7 @@ struct alignas(16) StructRec {
     double inner2;       // broad d2 below this: inside for sure
     double outer2;       // broad d2 at or above this: outside for sure
     double cut2;         // (T)(cutoff * cutoff) as double
-    unsigned long long red[14];  // max-keys of the atom reductions of shared blocks (kRed*)
+    unsigned long long red[kRedCount];  // max-keys of the atom reductions of shared blocks
     unsigned long long maxp;     // bits of max_c |p_c| (non-negative double), set by k_plan
     unsigned long long flags;   // input-error bits found by k_setup for this structure
     int64_t img_total;   // images this structure adds to the batch total (0 if invalid)
@@ -132,17 +144,6 @@ struct alignas(16) StructRec {
     int32_t mwords;      // hit-mask words per atom of the request's workspace (1-kMaskWords)
     int32_t mneed;       // brute force: hit-mask words per atom the structure wants
 };
-
-// The 14 per-structure reductions over atoms, all kept as maxima of
-// "max-keys": kRedUlo + a / kRedUhi + a are the lower / upper bounds of the
-// grid coordinate on axis a, kRedClo + c / kRedChi + c those of the wrapped
-// Cartesian coordinate c, kRedP is max_c |p_c| and kRedW max_a |wrap_a|.
-// Lower bounds are stored complemented so that every reduction is a
-// maximum and 0 is the identity.  For float inputs the keys are 32-bit
-// (bounds rounded outward, Cartesian bounds exact, |p| rounded up); for
-// double inputs they are 64-bit and exact.
-enum RedSlot : int { kRedUlo = 0, kRedUhi = 3, kRedClo = 6, kRedChi = 9, kRedP = 12, kRedW = 13,
-                     kRedCount = 14 };
 
 // Per-block reduction record written by k_atoms for blocks whose atoms all
 // lie in one structure (k_plan combines them without atomics); for a

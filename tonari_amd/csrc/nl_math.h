@@ -252,4 +252,90 @@ struct RedKeys<double> {
     __device__ static unsigned long long wave_max(unsigned long long x) { return wave_max_u64(x); }
 };
 
+// ------------------------------------------- x87 extended precision, emulated
+// The reference evaluates its cell-list padding in long double, the x87
+// 80-bit format of its x86-64 builds: a 64-bit significand, every operation
+// rounded to nearest even.  Ext holds such a value exactly as an unevaluated
+// sum hi + lo of two doubles (hi the double nearest the value), for the
+// finite, normal magnitudes of that computation.  Sums are formed exactly
+// (two_sum) before the rounding to 64 bits; a sum of two values whose
+// exponents lie more than about 40 apart is rounded from a 106-bit
+// approximation, which differs from the x87 result only when the exact sum
+// lies within 2^-106 of a rounding boundary.
+struct Ext {
+    double hi, lo;
+};
+
+__device__ __forceinline__ Ext two_sum(double a, double b) {
+    const double s = __dadd_rn(a, b);
+    const double bb = __dsub_rn(s, a);
+    const double e = __dadd_rn(__dsub_rn(a, __dsub_rn(s, bb)), __dsub_rn(b, bb));
+    return Ext{s, e};
+}
+
+// hi + lo rounded to a 64-bit significand (nearest even); |lo| <= ulp(hi) / 2.
+__device__ __forceinline__ Ext ext_round(double hi, double lo) {
+    if (lo == 0.0 || hi == 0.0 || !isfinite(hi)) return Ext{hi, lo};
+    const unsigned long long bits = (unsigned long long)__double_as_longlong(hi);
+    const int e = (int)((bits >> 52) & 0x7ff);
+    // spacing of 64-bit significands in hi's binade, halved just below a
+    // power of two
+    double q = ldexp(1.0, e - 1086);
+    if ((bits & 0xfffffffffffffull) == 0 && ((lo < 0) != (hi < 0))) q *= 0.5;
+    // lo / q is exact (a power-of-two scaling); rint rounds half to even,
+    // and the 64-bit significand's parity is that of the multiple of q
+    const double k = rint(lo / q);
+    return two_sum(hi, k * q);
+}
+
+__device__ __forceinline__ Ext ext_exact(double x) { return Ext{x, 0.0}; }
+
+// a * b rounded to 64 bits (a and b doubles, so the product is exact in Ext).
+__device__ __forceinline__ Ext ext_mul(double a, double b) {
+    const double p = __dmul_rn(a, b);
+    return ext_round(p, __fma_rn(a, b, -p));
+}
+
+// a * 2^k, exact.
+__device__ __forceinline__ Ext ext_scale(Ext a, int k) { return Ext{ldexp(a.hi, k), ldexp(a.lo, k)}; }
+
+// a + b rounded to 64 bits.
+__device__ __forceinline__ Ext ext_add(Ext a, Ext b) {
+    const Ext s = two_sum(a.hi, b.hi);
+    const Ext t = two_sum(a.lo, b.lo);
+    const Ext u = two_sum(s.hi, __dadd_rn(s.lo, t.hi));
+    const Ext v = two_sum(u.hi, __dadd_rn(u.lo, t.lo));
+    return ext_round(v.hi, v.lo);
+}
+
+__device__ __forceinline__ bool ext_less(Ext a, Ext b) {
+    return a.hi < b.hi || (a.hi == b.hi && a.lo < b.lo);
+}
+
+// The value rounded to nearest even in T (a C++ conversion of a long double).
+template <typename T>
+__device__ __forceinline__ T ext_to(Ext a);
+
+template <>
+__device__ __forceinline__ double ext_to<double>(Ext a) {
+    // hi + lo is the exact value: the hardware sum rounds it once
+    return __dadd_rn(a.hi, a.lo);
+}
+
+template <>
+__device__ __forceinline__ float ext_to<float>(Ext a) {
+    // hi is the double nearest the value, and every float midpoint is a
+    // double: hi rounds as the value does unless hi is a midpoint itself,
+    // where the sign of lo decides
+    float f = __double2float_rn(a.hi);
+    const double df = (double)f;
+    if (df != a.hi && a.lo != 0.0) {
+        const float g = nextafterf(f, a.hi > df ? INFINITY : -INFINITY);
+        const double dg = (double)g;
+        if (fabs(dg - a.hi) == fabs(df - a.hi))
+            f = (a.lo > 0.0) == (dg > df) ? g : f;
+    }
+    return f;
+}
+
 }  // namespace tnr

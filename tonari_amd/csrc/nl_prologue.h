@@ -501,7 +501,7 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
     T q[3] = {T(0), T(0), T(0)};
     int w[3] = {0, 0, 0};
     double u[3] = {0, 0, 0};
-    double pmax = 0;
+    double pabs[3] = {0, 0, 0};
     unsigned long long st = 0;
     if (valid) {
         b = uniform ? bfirst : structure_of(bp, bfirst, (int64_t)blast + 1, i);
@@ -540,7 +540,8 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
                     q[c] = x;
                 }
                 grid_coords(r, q, u);
-                pmax = fmax(fabs(pd[0]), fmax(fabs(pd[1]), fabs(pd[2])));
+#pragma unroll
+                for (int c = 0; c < 3; ++c) pabs[c] = fabs(pd[c]);
                 good = true;
             }
         }
@@ -554,7 +555,7 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
             atomicOr(status + SS_FLAGS, st);
     }
 
-    // the 14 reductions as max-keys (0 = identity for atoms that contribute nothing)
+    // the 18 reductions as max-keys (0 = identity for atoms that contribute nothing)
     using K = RedKeys<T>;
     unsigned long long v[kRedCount];
 #pragma unroll
@@ -564,8 +565,11 @@ __global__ __launch_bounds__(kBlock) void k_atoms(const T* pos, const int64_t* b
         v[kRedClo + a] = good ? K::lower_exact(q[a]) : 0ull;
         v[kRedChi + a] = good ? K::upper_exact(q[a]) : 0ull;
     }
-    v[kRedP] = good ? K::magnitude(pmax) : 0ull;
-    v[kRedW] = good ? (unsigned long long)max(max(abs(w[0]), abs(w[1])), abs(w[2])) : 0ull;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        v[kRedP + c] = good ? K::magnitude(pabs[c]) : 0ull;
+        v[kRedW + c] = good ? (unsigned long long)abs(w[c]) : 0ull;
+    }
     if (uniform) {
         const int wv = threadIdx.x / kWave;
 #pragma unroll
@@ -663,25 +667,72 @@ __device__ __forceinline__ void write_margins(StructRec& r, const Margins& m, do
     r.cut2 = (double)(T)(cutoff * cutoff);
 }
 
-// The reference CPU layout rule for an explicit cell_list
-// (neighbors_cpu.cpp:379-430): bins of the padded cutoff over the bounding
-// box of the wrapped positions.  True when the structure is refused.
+// Largest |p_c| over the components and largest |wrap_a| over the axes,
+// from the per-component reductions (the keys order as the values do).
 template <typename T>
-__device__ __forceinline__ bool cell_unsafe(const unsigned long long red[kRedCount], double rc,
-                                            const Margins& m, int64_t n, int64_t nimages) {
+__device__ __forceinline__ double red_pmax(const unsigned long long red[kRedCount]) {
+    unsigned long long k = red[kRedP];
+    k = red[kRedP + 1] > k ? red[kRedP + 1] : k;
+    k = red[kRedP + 2] > k ? red[kRedP + 2] : k;
+    return RedKeys<T>::magnitude_value(k);
+}
+__device__ __forceinline__ unsigned red_wmax(const unsigned long long red[kRedCount]) {
+    unsigned long long k = red[kRedW];
+    k = red[kRedW + 1] > k ? red[kRedW + 1] : k;
+    k = red[kRedW + 2] > k ? red[kRedW + 2] : k;
+    return (unsigned)k;
+}
+
+// The reference's CPU refusal of an explicit cell_list ("cell_list cannot
+// safely process this structure"), evaluated as it does.  The padded search
+// cutoff (neighbors_cpu.cpp:157-218): the operation scale, max over c of
+// 2 max|p_c| + sum_a (R_a + 2 max|w_a|) |cell_ac|, and cutoff + 64 eps_T
+// scale in x87 long double (emulated, Ext), rounded to T and moved up one
+// ulp; refused when that is not finite or exceeds 2 cutoff or T's maximum.
+// Then the dense bin layout over the wrapped positions' bounding box in T
+// arithmetic (neighbors_cpu.cpp:379-430): per axis span = (max - min) + 2
+// size and span / size bins, refused beyond 2^26 bins in all or more than
+// 64 bins per atom image.  cell holds the structure's cell entries (values
+// of T); n atoms, r.nimages images.  True when refused.
+template <typename T>
+__device__ __forceinline__ bool cell_unsafe(const unsigned long long red[kRedCount],
+                                            const StructRec& r, const double cell[9],
+                                            double cutoff, int64_t n) {
     using K = RedKeys<T>;
-    const double size = rc + m.pad;
-    double count = 1;
-    bool ok = m.safe;
+    using O = Ops<T>;
+    constexpr int64_t kDenseBins = int64_t{1} << 26;
+    const T rc = (T)cutoff;
+    Ext scale = ext_exact(0.0);
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
-        const double span =
-            K::upper_value(red[kRedChi + c]) - K::lower_value(red[kRedClo + c]) + 2 * size;
-        const double dim = span / size;
-        if (!isfinite(dim) || dim > 67108864.0) ok = false;
-        count *= fmax(1.0, ceil(dim));
+        Ext comp = ext_exact(2.0 * K::magnitude_value(red[kRedP + c]));
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const double shift = (double)r.reps[a] + 2.0 * (double)(unsigned)red[kRedW + a];
+            comp = ext_add(comp, ext_mul(shift, fabs(cell[3 * a + c])));
+        }
+        if (ext_less(scale, comp)) scale = comp;
     }
-    return !ok || count > 67108864.0 || ceil(count / 64.0) > (double)n * (double)nimages;
+    // 64 eps_T = 2^-17 (float) or 2^-46 (double): the product is exact
+    const Ext padded = ext_add(ext_exact((double)rc), ext_scale(scale, sizeof(T) == 4 ? -17 : -46));
+    if (!isfinite(padded.hi) || ext_less(ext_exact(2.0 * (double)rc), padded) ||
+        ext_less(ext_exact((double)O::max), padded))
+        return true;
+    const T size = nextafter(ext_to<T>(padded), (T)INFINITY);
+    if (!isfinite((double)size)) return true;
+    int64_t count = 1;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const T lo = (T)K::lower_value(red[kRedClo + c]);
+        const T hi = (T)K::upper_value(red[kRedChi + c]);
+        const T span = O::add(O::sub(hi, lo), O::mul(T(2), size));
+        const T dim = span / size;  // correctly rounded (IEEE division)
+        if (!isfinite((double)dim) || (double)dim > (double)kDenseBins) return true;
+        const int64_t d = max((int64_t)1, (int64_t)ceil((double)dim));
+        if (count > kDenseBins / d) return true;
+        count *= d;
+    }
+    return !(count <= kDenseBins && (count + 63) / 64 <= n * r.nimages);
 }
 
 // A bin grid of a cell-list structure: bins per axis, bins per grid unit,
@@ -880,15 +931,14 @@ __device__ __forceinline__ void plan_structure(const T* cells, int64_t b, Struct
 #pragma unroll
     for (int e = 0; e < 9; ++e) cell[e] = (double)cells[9 * b + e];
     const double rc = cutoff;
-    const Margins m = plan_margins<T>(cell, r, K::magnitude_value(red[kRedP]),
-                                      (unsigned)red[kRedW], rc);
+    const Margins m = plan_margins<T>(cell, r, red_pmax<T>(red), red_wmax(red), rc);
     if (writer) write_margins<T>(r, m, cutoff);
     const int64_t nimages = r.nimages;
     // n > floor(limit / nimages), as a product (nimages <= 2^24)
     const bool large = r.active != 0 ? n * nimages > kAutoBrutePeriodic : n > kAutoBruteIsolated;
     bool want_cell = requested == TNR_CELL_LIST || (requested == TNR_AUTO && large);
     unsigned long long st = 0;
-    if (requested == TNR_CELL_LIST && cell_unsafe<T>(red, rc, m, n, nimages)) st |= ST_CELL_UNSAFE;
+    if (requested == TNR_CELL_LIST && cell_unsafe<T>(red, r, cell, cutoff, n)) st |= ST_CELL_UNSAFE;
     if (!m.safe) want_cell = false;
     int algo = ALGO_BRUTE;
     int64_t nbins = 0;
@@ -1407,7 +1457,7 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
     T q[3] = {T(0), T(0), T(0)};
     int w[3] = {0, 0, 0};
     double u[3] = {0, 0, 0};
-    double pmax = 0;
+    double pabs[3] = {0, 0, 0};
     unsigned long long st = 0;
     if (valid) {
         atom_struct[i] = 0;
@@ -1437,7 +1487,8 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
                     q[c] = x;
                 }
                 grid_coords(r, q, u);
-                pmax = fmax(fabs(pd[0]), fmax(fabs(pd[1]), fabs(pd[2])));
+#pragma unroll
+                for (int c = 0; c < 3; ++c) pabs[c] = fabs(pd[c]);
                 good = true;
             }
         }
@@ -1455,8 +1506,11 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
         v[kRedClo + a] = good ? K::lower_exact(q[a]) : 0ull;
         v[kRedChi + a] = good ? K::upper_exact(q[a]) : 0ull;
     }
-    v[kRedP] = good ? K::magnitude(pmax) : 0ull;
-    v[kRedW] = good ? (unsigned long long)max(max(abs(w[0]), abs(w[1])), abs(w[2])) : 0ull;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        v[kRedP + c] = good ? K::magnitude(pabs[c]) : 0ull;
+        v[kRedW + c] = good ? (unsigned long long)abs(w[c]) : 0ull;
+    }
 #pragma unroll
     for (int e = 0; e < kRedCount; ++e) v[e] = K::wave_max(v[e]);
     if (lane == 0)
@@ -1538,8 +1592,8 @@ __device__ __forceinline__ void periodic_finish(const T* cells, int64_t n_atoms,
 #pragma unroll
         for (int e = 0; e < 9; ++e) cell[e] = (double)cells[e];
         const double rc = cutoff;
-        const Margins m = plan_margins<T>(cell, r, K::magnitude_value(v[kRedP]), (unsigned)v[kRedW], rc);
-        if (requested == TNR_CELL_LIST && cell_unsafe<T>(v, rc, m, n, r.nimages))
+        const Margins m = plan_margins<T>(cell, r, red_pmax<T>(v), red_wmax(v), rc);
+        if (requested == TNR_CELL_LIST && cell_unsafe<T>(v, r, cell, cutoff, n))
             st |= ST_CELL_UNSAFE;
         // the reach that bins of the chosen grid need for the true margin
         bool fits = m.safe;
