@@ -702,6 +702,35 @@ __device__ __forceinline__ bool cell_unsafe(const unsigned long long red[kRedCou
     using O = Ops<T>;
     constexpr int64_t kDenseBins = int64_t{1} << 26;
     const T rc = (T)cutoff;
+    {
+        // Far from the limits, as nearly every structure is: the search
+        // cutoff is at least rc (the pad is not negative and the rounding
+        // monotone), so the bins per axis are at most ceil((max - min) / rc
+        // + 2), widened by 1e-6 for T's roundings; with the padding bounded
+        // above in double (1e-9 beyond its roundings), a layout that fits
+        // the limits is accepted without the long double evaluation.
+        double scale_hi = 0.0;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            double comp = 2.0 * K::magnitude_value(red[kRedP + c]);
+#pragma unroll
+            for (int a = 0; a < 3; ++a)
+                comp += ((double)r.reps[a] + 2.0 * (double)(unsigned)red[kRedW + a]) *
+                        fabs(cell[3 * a + c]);
+            scale_hi = fmax(scale_hi, comp);
+        }
+        const double padded_hi = ((double)rc + 64.0 * O::eps * scale_hi) * (1.0 + 1e-9);
+        if (padded_hi < 2.0 * (double)rc && padded_hi <= (double)O::max) {
+            double bins = 1.0;
+#pragma unroll
+            for (int c = 0; c < 3; ++c) {
+                const double span = K::upper_value(red[kRedChi + c]) - K::lower_value(red[kRedClo + c]);
+                bins *= fmax(1.0, ceil((span / (double)rc + 2.0) * (1.0 + 1e-6)));
+            }
+            if (bins <= (double)kDenseBins && ceil(bins / 64.0) <= (double)n * (double)r.nimages)
+                return false;
+        }
+    }
     Ext scale = ext_exact(0.0);
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
