@@ -426,7 +426,7 @@ __global__ __launch_bounds__(kBlock) void k_cell_count(QueryArgs<T> a) {
             const StructRec& r = a.recs[b];
             need = max(need, r.mneed);
             if (molecule_rec(r))
-                molecule_count<T, MODE>(a, r, u);
+                molecule_count<T, MODE>(a, r, u, r.unit0);
             else
                 brute_unit<T, MODE, false, false>(a, u, b, nullptr, s_lds[wv].cur);
         }

@@ -209,6 +209,21 @@ __host__ __device__ inline bool molecule_rec(const StructRec& r) {
     return molecule_path(r.active, r.natoms) && molecule_words(r.natoms) <= r.mwords;
 }
 
+// Summary of one workgroup of the molecule prologue (kSetupBlock structures):
+// their work units, periodic images and error bits.  A molecules-only request
+// of at most kMolLocalMax structures is planned without the batch scan: the
+// set-up leaves block-local unit offsets and one summary per workgroup (in the
+// plan-summary area), and the molecule counting kernel, whose waves scan the
+// summaries, makes the offsets global.
+struct alignas(32) MoleculeBlock {
+    long long units;
+    unsigned long long flags;
+    long long images;
+    long long pad;
+};
+static_assert(sizeof(MoleculeBlock) == sizeof(PlanSummary), "one summary per plan-summary slot");
+constexpr int64_t kMolLocalMax = 64 * 64;  // 64 workgroups of 64 structures: one wave's lanes
+
 // k0 slices of a periodic brute-force structure, at most (each source's
 // slice pair counts fill the first words of its hit-mask slot).
 constexpr int kMaxSlices = 32;

@@ -1116,14 +1116,16 @@ __global__ __launch_bounds__(kBlock) void k_struct_scan(const long long* struct_
 // under the request's algorithm raises ST_PLAN_HINT in its record, which the
 // batch scan folds into the status words.
 template <typename T>
-__device__ __forceinline__ void molecule_setup_one(const int64_t* bp, const T* cells,
-                                                   const uint8_t* pbc, int64_t nb,
-                                                   int64_t n_atoms, double cutoff, int mw,
-                                                   int requested,
-                                                   StructRec& r, long long* struct_bins,
-                                                   long long* struct_units, PlanSummary* meta,
-                                                   int64_t b) {
+__device__ __forceinline__ long long molecule_setup_one(const int64_t* bp, const T* cells,
+                                                        const uint8_t* pbc, int64_t nb,
+                                                        int64_t n_atoms, double cutoff, int mw,
+                                                        int requested, StructRec& r,
+                                                        long long* struct_bins,
+                                                        long long* struct_units,
+                                                        PlanSummary* meta, int64_t b) {
     setup_structure<T, true>(bp, cells, pbc, nb, n_atoms, cutoff, mw, b, r);
+    // no cell-list atoms share the hit-mask rows: each atom takes its own
+    r.mask0 = r.atom0;
     const int64_t n = r.natoms;
     long long units = 0;
     if (!(r.flags & kAbortBits) && n > 0) {
@@ -1151,29 +1153,59 @@ __device__ __forceinline__ void molecule_setup_one(const int64_t* bp, const T* c
     }
     struct_bins[b] = 0;
     struct_units[b] = units;
-    write_summary(meta + b, r);
+    if (meta) write_summary(meta + b, r);
+    return units;
 }
 
 // Molecule plan, one thread per structure (molecule_setup_one), kSetupBlock
-// per workgroup with the records built in LDS (store_records); block 0
-// first zeroes the status words and the pair scan's tile states.
-// k_struct_scan follows.
+// (one wave) per workgroup with the records built in LDS (store_records);
+// block 0 first zeroes the status words and the pair scan's tile states.
+// k_struct_scan follows, unless `local`: then each workgroup writes its
+// structures' block-local unit offsets to local_off and its summary to
+// blocks[blockIdx.x], block 0 writes the plan, and the molecule counting
+// kernel finishes the offsets and the status words (MoleculeBlock).
 template <typename T>
 __global__ __launch_bounds__(kSetupBlock) void k_molecule_setup(
     const int64_t* bp, const T* cells, const uint8_t* pbc, int64_t nb, int64_t n_atoms,
     double cutoff, int mw, int requested, StructRec* recs, long long* struct_bins,
     long long* struct_units, PlanSummary* meta, unsigned long long* status,
-    unsigned long long* tiles, int64_t n_tiles) {
+    unsigned long long* tiles, int64_t n_tiles, int local, long long* local_off) {
+    static_assert(kSetupBlock == kWave, "the local scan is one wave's");
+    static_assert(kMolLocalMax == (int64_t)kSetupBlock * kWave, "one summary per lane");
     __shared__ StructRec s_recs[kSetupBlock];
     const int64_t b0 = (int64_t)blockIdx.x * kSetupBlock;
     const int64_t b = b0 + threadIdx.x;
     if (blockIdx.x == 0) {
         for (int k = threadIdx.x; k < SS_SLOTS; k += blockDim.x) status[k] = 0;
         for (int64_t k = threadIdx.x; k < n_tiles; k += blockDim.x) tiles[k] = 0;
+        if (local && threadIdx.x == 0) status[SS_PLAN] = 1ull | kPlanMolecules;
     }
+    long long units = 0;
     if (b < nb)
-        molecule_setup_one<T>(bp, cells, pbc, nb, n_atoms, cutoff, mw, requested,
-                              s_recs[threadIdx.x], struct_bins, struct_units, meta, b);
+        units = molecule_setup_one<T>(bp, cells, pbc, nb, n_atoms, cutoff, mw, requested,
+                                      s_recs[threadIdx.x], struct_bins, struct_units,
+                                      local ? nullptr : meta, b);
+    if (local) {
+        // the workgroup's exclusive scan of units (its structures' offsets
+        // within it) and its summary
+        const int inc = wave_inclusive_scan_i32((int)units);
+        unsigned long long fl = b < nb ? s_recs[threadIdx.x].flags : 0ull;
+        long long img = b < nb ? (long long)s_recs[threadIdx.x].img_total : 0ll;
+#pragma unroll
+        for (int d = kWave / 2; d > 0; d >>= 1) {
+            fl |= __shfl_xor(fl, d);
+            img += __shfl_xor(img, d);
+        }
+        if (b < nb) local_off[b] = (long long)(inc - (int)units);
+        if (threadIdx.x == kWave - 1) {
+            MoleculeBlock mb;
+            mb.units = (long long)inc;
+            mb.flags = fl;
+            mb.images = img;
+            mb.pad = 0;
+            reinterpret_cast<MoleculeBlock*>(meta)[blockIdx.x] = mb;
+        }
+    }
     if (b0 < nb) store_records(s_recs, recs, b0, min((int64_t)kSetupBlock, nb - b0));
 }
 

@@ -34,6 +34,12 @@ struct QueryArgs {
     int64_t n_atoms;
     int64_t nb;
     int mask_words;  // words of an atom's hit-mask row (1 to kMaskWords)
+    // count of a molecules-only request planned without the batch scan
+    // (k_molecule_setup with `local`): struct_bin_off holds block-local unit
+    // offsets and mol_blocks the workgroups' summaries; the counting kernel
+    // makes the offsets global for the emitting pass
+    int mol_local;
+    const MoleculeBlock* mol_blocks;
     // without `sorted`: when every structure is searched with a cell list
     // (status plan 2), pair counts and output offsets are indexed by binned
     // position, so sources take the outputs in binned order and every
@@ -643,11 +649,11 @@ static_assert(kMoleculeCap <= 2048 && kMoleculeCap <= kMaskWords * kWave,
 
 template <typename T, int MODE>
 __device__ __forceinline__ void molecule_count(const QueryArgs<T>& a, const StructRec& r,
-                                               int64_t u) {
+                                               int64_t u, int64_t unit0) {
     using O = Ops<T>;
     const int lane = lane_id();
     const int a0 = (int)r.atom0, n = (int)r.natoms;
-    const int f = (int)(u - r.unit0) * r.bgroup;
+    const int f = (int)(u - unit0) * r.bgroup;
     const int G = min(r.bgroup, n - f);  // <= kMolUnitWork
     const int nch = (n + kWave - 1) / kWave;
     const T cut2 = (T)r.cut2;
@@ -786,12 +792,64 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
             if constexpr (EMIT)
                 molecule_emit<T, MODE>(a, r, b, u, s_lds[wv].mol);
             else
-                molecule_count<T, MODE>(a, r, u);
+                molecule_count<T, MODE>(a, r, u, r.unit0);
         } else {
             brute_unit<T, MODE, EMIT>(a, u, b, &s_lds[wv].walk, s_lds[wv].walk.c);
         }
     }
     if constexpr (!EMIT) report_mask_need(a.status, need);
+}
+
+// The workgroup summaries of a molecule prologue without the batch scan
+// (QueryArgs::mol_local), as every counting wave reads them: lane l holds
+// workgroup l's exclusive unit offset.
+struct MolScan {
+    int off;                   // lane l: units of workgroups before l
+    int total;                 // units of the request
+    int nblk;                  // workgroups of the prologue (at most kWave)
+    unsigned long long flags;  // every structure's error bits
+    long long images;
+};
+
+template <typename T>
+__device__ __forceinline__ MolScan mol_scan(const QueryArgs<T>& a) {
+    const int lane = lane_id();
+    MolScan m;
+    m.nblk = (int)((a.nb + kWave - 1) / kWave);
+    MoleculeBlock mb{0, 0ull, 0, 0};
+    if (lane < m.nblk) mb = a.mol_blocks[lane];
+    const int inc = wave_inclusive_scan_i32((int)mb.units);
+    m.off = inc - (int)mb.units;
+    m.total = __builtin_amdgcn_readlane(inc, kWave - 1);
+    unsigned long long fl = mb.flags;
+    long long img = mb.images;
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) {
+        fl |= __shfl_xor(fl, d);
+        img += __shfl_xor(img, d);
+    }
+    m.flags = fl;
+    m.images = img;
+    return m;
+}
+
+// Structure of unit u and its first unit under mol_local: the workgroup
+// from the lanes' offsets, then the structure from its block-local offsets
+// (one load per lane).
+template <typename T>
+__device__ __forceinline__ int mol_unit_structure(const QueryArgs<T>& a, const MolScan& m,
+                                                  int64_t u, int64_t& unit0) {
+    const int lane = lane_id();
+    const unsigned long long mb = ballot(lane < m.nblk && (int64_t)m.off <= u);
+    const int B = 63 - __builtin_clzll(mb | 1ull);
+    const int64_t base = (int64_t)__builtin_amdgcn_readlane(m.off, B);
+    const int64_t b0 = (int64_t)B * kWave;
+    const int cnt = (int)min((int64_t)kWave, a.nb - b0);
+    const long long lo = lane < cnt ? a.struct_bin_off[b0 + lane] : 0ll;
+    const unsigned long long ms = ballot(lane < cnt && base + lo <= u);
+    const int k = 63 - __builtin_clzll(ms | 1ull);
+    unit0 = base + (int64_t)__builtin_amdgcn_readlane((int)lo, k);
+    return (int)(b0 + k);
 }
 
 // Counting or emitting pass of a request whose brute-force structures are
@@ -801,7 +859,11 @@ __global__ __launch_bounds__(kBlock) void k_brute(QueryArgs<T> a) {
 // once.  Exits at once when the request has no brute-force structure, or
 // when the count found one that is not a molecule (an emit launched with an
 // earlier call's plan: it writes nothing, and the caller, seeing the
-// count's plan, emits again).
+// count's plan, emits again).  Counting under mol_local, each wave first
+// scans the prologue's workgroup summaries (mol_scan); the first waves then
+// write the global unit offsets (struct_unit_off and each record's unit0)
+// for the emitting pass, and wave 0 the status words the batch scan would
+// have written.
 template <typename T, int MODE, bool EMIT>
 __global__ __launch_bounds__(kBlock) void k_molecules(QueryArgs<T> a) {
     const unsigned long long plan = load_status(a.status + SS_PLAN);
@@ -810,19 +872,52 @@ __global__ __launch_bounds__(kBlock) void k_molecules(QueryArgs<T> a) {
         return;
     if constexpr (EMIT) place_edge_index(a);
     __shared__ int s_list[kWavesPerBlock][EMIT ? kMolList : 1];
-    const int64_t units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
     const int wv = uniform(threadIdx.x / kWave);
     const int64_t wave0 = (int64_t)blockIdx.x * kWavesPerBlock + wv;
     const int64_t nwaves = (int64_t)gridDim.x * kWavesPerBlock;
+    int64_t units = 0;
+    MolScan ms{0, 0, 0, 0ull, 0};
+    if (!EMIT && a.mol_local) {
+        ms = mol_scan(a);
+        if (wave0 == 0 && lane_id() == 0) {
+            a.status[SS_TOTAL_UNITS] = (unsigned long long)ms.total;
+            a.status[SS_TOTAL_IMAGES] = (unsigned long long)ms.images;
+            if (ms.flags) atomicOr(a.status + SS_FLAGS, ms.flags);
+        }
+        if (ms.flags & kAbortBits) return;
+        // global unit offsets for the emitting pass (workgroup w of the
+        // prologue by wave w, striding when the grid holds fewer waves)
+        for (int64_t w = wave0; w < ms.nblk; w += nwaves) {
+            const int base = __builtin_amdgcn_readlane(ms.off, (int)w);
+            const int64_t b = w * kWave + lane_id();
+            if (b < a.nb) {
+                const long long off = a.struct_bin_off[b] + (long long)base;
+                const_cast<int64_t*>(a.struct_unit_off)[b] = off;
+                const_cast<StructRec*>(a.recs)[b].unit0 = off;
+            }
+            if (w == ms.nblk - 1 && lane_id() == 0)
+                const_cast<int64_t*>(a.struct_unit_off)[a.nb] = (int64_t)ms.total;
+        }
+        units = ms.total;
+    } else {
+        units = (int64_t)load_status(a.status + SS_TOTAL_UNITS);
+    }
     int need = 0;  // counting: the longest hit-mask row the wave's molecules want
     for (int64_t u = wave0; u < units; u += nwaves) {
-        const int b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+        int b;
+        int64_t unit0;
+        if (!EMIT && a.mol_local) {
+            b = uniform(mol_unit_structure(a, ms, u, unit0));
+        } else {
+            b = uniform(unit_structure(a.struct_unit_off, a.nb, u));
+            unit0 = a.recs[b].unit0;
+        }
         const StructRec& r = a.recs[b];
         if constexpr (EMIT) {
             molecule_emit<T, MODE>(a, r, b, u, s_list[wv]);
         } else {
             need = max(need, r.mneed);
-            molecule_count<T, MODE>(a, r, u);
+            molecule_count<T, MODE>(a, r, u, unit0);
         }
     }
     if constexpr (!EMIT) report_mask_need(a.status, need);

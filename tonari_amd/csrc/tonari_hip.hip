@@ -287,13 +287,16 @@ static void dispatch_queries(const tnr_request* req, const Layout& L, const Quer
 //   HINT_BRUTE      no cell-list structure: the cell-list kernels are not
 //                   launched, and the planner raises ST_PLAN_HINT if a
 //                   structure is planned as a cell list after all;
-//   HINT_MOLECULES  every structure a molecule: k_molecule_setup and
-//                   k_struct_scan are the whole prologue (ST_PLAN_HINT for
-//                   any other structure).
+//   HINT_MOLECULES  every structure a molecule: k_molecule_setup is the
+//                   whole prologue (ST_PLAN_HINT for any other structure),
+//                   followed by k_struct_scan only for more than
+//                   kMolLocalMax structures (below that the molecule
+//                   counting kernel finishes the plan from the workgroups'
+//                   summaries);
 //   HINT_PERIODIC   one fully periodic structure planned as a cell list
 //                   whose grid periodic_grid chooses: the periodic fast
 //                   prologue (k_periodic_atoms, k_periodic_rank,
-//                   k_periodic_scatter; ST_PLAN_HINT if it does not apply).
+//                   k_periodic_bin_scan; ST_PLAN_HINT if it does not apply).
 enum CountHint : int { HINT_NONE = 0, HINT_BRUTE = 1, HINT_MOLECULES = 2, HINT_PERIODIC = 3 };
 
 template <typename T>
@@ -309,14 +312,19 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
     const int mw = mask_words(req);
     const int64_t n_tiles =
         (int64_t)((L.tiles_pairs - L.tiles_bins) / sizeof(unsigned long long)) + L.n_tiles_pairs;
+    // a molecules-only batch of up to kMolLocalMax structures: no batch scan
+    // (the molecule counting kernel finishes the plan, MoleculeBlock)
+    const bool mol_local = hint == HINT_MOLECULES && nb >= 1 && nb <= kMolLocalMax;
     if (hint == HINT_MOLECULES) {
         k_molecule_setup<T><<<blocks_for(nb, kSetupBlock), kSetupBlock, 0, stream>>>(
             req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, mw, req->algorithm,
             v.recs, v.struct_bins, v.struct_units, v.struct_meta, v.status, v.tiles_pairs,
-            L.n_tiles_pairs);
-        k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units, v.struct_meta,
-                                                nb, n, v.struct_bin_off, v.struct_unit_off,
-                                                v.recs, v.status, L.cap_bins, 0);
+            L.n_tiles_pairs, mol_local ? 1 : 0, v.struct_bin_off);
+        if (!mol_local)
+            k_struct_scan<<<1, kBlock, 0, stream>>>(v.struct_bins, v.struct_units,
+                                                    v.struct_meta, nb, n, v.struct_bin_off,
+                                                    v.struct_unit_off, v.recs, v.status,
+                                                    L.cap_bins, 0);
     } else if (periodic) {
         // one fully periodic structure: set-up, grid, atoms and bins; ranks;
         // the bin scan beside the finished plan (k_scatter follows below)
@@ -383,7 +391,11 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                                                            v.binned_w, (Vec4<T>*)v.binned_p,
                                                            v.status);
     }
-    const QueryArgs<T> q = query_args<T>(req, v);
+    QueryArgs<T> q = query_args<T>(req, v);
+    if (mol_local) {
+        q.mol_local = 1;
+        q.mol_blocks = reinterpret_cast<const MoleculeBlock*>(v.struct_meta);
+    }
     dispatch_queries<T, false>(
         req, L, q, cell_kernels ? 0 : (hint == HINT_MOLECULES ? 1 | (int64_t)kPlanMolecules : 1), 0,
         stream);
