@@ -440,16 +440,93 @@ def test_thread_count_invariance():
     assert np.array_equal(one, many)
 
 
-def test_quantities_closed_form():
-    # tests/test_quantities.py:10-33: D = pos[j] - pos[i] + S @ cell[b], d = |D|
-    cfg = _random_cfg(55, 60, [1, 0, 1], np.float64)
+def _quantities(cfg, which="dD"):
     pairs, shifts = oracle_call(cfg)
-    i, j, d, D = oracle.quantities("ijdD", cfg["positions"], cfg["cell"], cfg["batch_ptr"],
-                                   pairs, shifts)
-    ref = cfg["positions"][j] - cfg["positions"][i] + shifts @ cfg["cell"][0]
-    np.testing.assert_allclose(D, ref, rtol=0, atol=1e-12)
-    np.testing.assert_allclose(d, np.linalg.norm(ref, axis=1), rtol=1e-14)
+    return (pairs, shifts) + oracle.quantities(which, cfg["positions"], cfg["cell"],
+                                               cfg["batch_ptr"], pairs, shifts)
+
+
+def test_quantities_known_answer_of_the_reference():
+    # tests/test_quantities.py:10-33: two atoms 0.8 apart on a periodic x
+    # axis of length 1 and cutoff 0.3; the pairs go through the periodic
+    # image, D = -0.2 x (0 -> 1, S = -x) and +0.2 x (1 -> 0, S = +x)
+    cfg = _single([[0.1, 0.0, 0.0], [0.9, 0.0, 0.0]], np.diag([1.0, 4.0, 4.0]), [1, 0, 0], 0.3)
+    pairs, shifts, d, D = _quantities(cfg)
+    got = {(int(i), int(j), tuple(int(x) for x in s_)): (v, dd)
+           for (i, j), s_, v, dd in zip(pairs, shifts, D, d)}
+    assert set(got) == {(0, 1, (-1, 0, 0)), (1, 0, (1, 0, 0))}
+    np.testing.assert_allclose(got[(0, 1, (-1, 0, 0))][0], [-0.2, 0.0, 0.0], atol=1e-15)
+    np.testing.assert_allclose(got[(1, 0, (1, 0, 0))][0], [0.2, 0.0, 0.0], atol=1e-15)
+    np.testing.assert_allclose(d, [0.2, 0.2], atol=1e-15)
+
+
+def _half_lattice(rows, shift):
+    # the 8 points (i a1 + j a2 + k a3) / 2, i, j, k in {0, 1}, of a periodic
+    # cell with rows a1, a2, a3, moved by `shift` (all values binary-exact)
+    rows = np.asarray(rows, dtype=np.float64)
+    pts = [(i * rows[0] + j * rows[1] + k * rows[2]) / 2 + shift
+           for i in (0, 1) for j in (0, 1) for k in (0, 1)]
+    return np.array(pts), rows
+
+
+def test_quantities_of_exact_lattices_in_a_batch():
+    # Two periodic cells in one batch: a skewed one whose half-lattice
+    # vectors a_c / 2 (lengths 2, 2.06, 2.08) are the only ones within the
+    # cutoff 2.2 (the next, (a2 - a1) / 2, is 2.5 long), and a cube of edge
+    # 4 (neighbours at +-2 along each axis).  Every atom has exactly six
+    # pairs, with D = +-a_c / 2 of its own structure's cell, bit for bit:
+    # a transposed cell, a sign slip or another structure's cell changes
+    # these vectors.
+    skew, rows0 = _half_lattice([[4.0, 0.0, 0.0], [1.0, 4.0, 0.0], [0.5, 1.0, 4.0]], 0.25)
+    cube, rows1 = _half_lattice(np.diag([4.0, 4.0, 4.0]), -0.5)
+    cfg = {
+        "positions": np.concatenate([skew, cube]),
+        "cell": np.stack([rows0, rows1]),
+        "pbc": np.ones((2, 3), bool),
+        "batch_ptr": np.array([0, 8, 16], dtype=np.int64),
+        "cutoff": 2.2,
+    }
+    pairs, shifts, d, D = _quantities(cfg)
+    assert len(pairs) == 16 * 6
+    for s in range(16):
+        rows = rows0 if s < 8 else rows1
+        want = sorted(map(tuple, np.concatenate([rows / 2, -rows / 2])))
+        mine = pairs[:, 0] == s
+        assert sorted(map(tuple, D[mine])) == want, s
+        np.testing.assert_allclose(d[mine], np.linalg.norm(D[mine], axis=1), rtol=1e-15)
+
+
+def test_quantities_invariants():
+    # a skewed cell with unwrapped atoms, float64
+    cfg = _random_cfg(55, 60, [1, 0, 1], np.float64)
+    pairs, shifts, d, D = _quantities(cfg)
+    by_key = {(int(i), int(j), tuple(int(x) for x in s_)): v
+              for (i, j), s_, v in zip(pairs, shifts, D)}
+    np.testing.assert_allclose(d, np.sqrt((D * D).sum(axis=1)), rtol=1e-15)
     assert np.all(d < cfg["cutoff"])
+    # the reverse pair (j, i, -S) carries -D, bit for bit
+    for (i, j, s_), v in by_key.items():
+        assert np.array_equal(by_key[(j, i, tuple(-x for x in s_))], -v)
+    # a common translation of every atom leaves every (i, j, S) and D
+    moved = dict(cfg, positions=cfg["positions"] + np.array([3.75, -12.125, 0.5]))
+    p2, s2, d2, D2 = _quantities(moved)
+    moved_key = {(int(i), int(j), tuple(int(x) for x in s_)): v
+                 for (i, j), s_, v in zip(p2, s2, D2)}
+    assert set(moved_key) == set(by_key)
+    for k, v in by_key.items():
+        np.testing.assert_allclose(moved_key[k], v, rtol=0, atol=1e-12)
+    # atom 7 moved by the first cell vector a0: its pairs keep their D, with
+    # S one cell more along a0 as a source and one cell less as a target
+    pos = cfg["positions"].copy()
+    pos[7] += cfg["cell"][0][0]
+    p3, s3, d3, D3 = _quantities(dict(cfg, positions=pos))
+    e0 = np.array([1, 0, 0])
+    for (i, j), s_, v in zip(p3, s3, D3):
+        s_ = np.array(s_)
+        old = s_ - (e0 if i == 7 else 0) + (e0 if j == 7 else 0)
+        np.testing.assert_allclose(by_key[(int(i), int(j), tuple(int(x) for x in old))], v,
+                                   rtol=0, atol=1e-12)
+    assert len(p3) == len(pairs)
 
 
 # ------------------------------------------------ compiled reference core
