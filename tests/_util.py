@@ -186,3 +186,31 @@ def shifts_from_vectors(pairs, D, cfg):
     frac = D.to(torch.float64) - (pos[pairs[:, 1]] - pos[pairs[:, 0]])
     S = torch.bmm(frac.unsqueeze(1), inv[b].contiguous()).squeeze(1)
     return torch.round(S).to(torch.int32)
+
+
+def lattice_point_case(seed: int, dtype, pbc) -> dict:
+    """Atoms on the lattice of a skewed cell, where wraps are decided at the ulp.
+
+    The 125 points i a1 + j a2 + k a3 (i, j, k in -2..2) and 20 points on cell
+    faces and half-lattice sites, each rounded in `dtype`: their fractional
+    coordinates p . dual lie within rounding of an integer or half-integer,
+    so the floor that gives each wrap, and through it the image box a pair
+    is taken from, depends on the last bits of the pseudo-inverse.  Cutoff
+    0.9 of the largest cell entry.
+    """
+    import itertools
+
+    rng = np.random.Generator(np.random.PCG64(seed))
+    cell = (np.diag(2.0 + 2.0 * rng.random(3)) + 0.6 * (rng.random((3, 3)) - 0.5)).astype(dtype)
+    pts = [np.array(ijk, dtype) @ cell for ijk in itertools.product(range(-2, 3), repeat=3)]
+    for _ in range(20):
+        f = rng.integers(-3, 4, 3).astype(dtype) + rng.choice([0.0, 0.5, 0.25], 3).astype(dtype)
+        pts.append(f @ cell)
+    pos = np.array(pts, dtype)
+    return {
+        "positions": pos,
+        "cell": cell[None],
+        "pbc": np.array([pbc], dtype=bool),
+        "batch_ptr": np.array([0, len(pos)], dtype=np.int64),
+        "cutoff": float(cell.max()) * 0.9,
+    }

@@ -534,6 +534,27 @@ def test_quantities_invariants():
 
 @pytest.mark.skipif(not oracle.available("reference"),
                     reason="reference core not built (no reference checkout here)")
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("pbc", [[1, 1, 1], [1, 0, 1], [1, 1, 0]])
+def test_lattice_point_atoms_match_the_reference_core(dtype, pbc):
+    # atoms whose wraps are decided at the ulp (tests/_util.py,
+    # lattice_point_case): the long double pseudo-inverse and floor of the
+    # port give the reference core's pairs and shifts
+    from tests._util import lattice_point_case
+
+    for seed in range(12):
+        cfg = lattice_point_case(seed, dtype, pbc)
+        for algorithm in ("brute_force", "cell_list"):
+            args = (cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"])
+            port = keys_of(*oracle.neighbor_pairs(*args, algorithm=algorithm, threads=1,
+                                                  kind="port"))
+            ref = keys_of(*oracle.neighbor_pairs(*args, algorithm=algorithm, threads=1,
+                                                 kind="reference"))
+            assert np.array_equal(port, ref), (seed, algorithm)
+
+
+@pytest.mark.skipif(not oracle.available("reference"),
+                    reason="reference core not built (no reference checkout here)")
 @pytest.mark.parametrize("name", ["C1_brute", "C1_cell", "C3_128", "C5_3",
                                   "ref_unwrapped_1842_f32", "ref_mixed_5801",
                                   "ref_fallback_9041_half_self"])
