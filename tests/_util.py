@@ -188,7 +188,7 @@ def shifts_from_vectors(pairs, D, cfg):
     return torch.round(S).to(torch.int32)
 
 
-def lattice_point_case(seed: int, dtype, pbc) -> dict:
+def lattice_point_case(seed: int, dtype, pbc, heights: int = 0) -> dict:
     """Atoms on the lattice of a skewed cell, where wraps are decided at the ulp.
 
     The 125 points i a1 + j a2 + k a3 (i, j, k in -2..2) and 20 points on cell
@@ -196,7 +196,9 @@ def lattice_point_case(seed: int, dtype, pbc) -> dict:
     coordinates p . dual lie within rounding of an integer or half-integer,
     so the floor that gives each wrap, and through it the image box a pair
     is taken from, depends on the last bits of the pseudo-inverse.  Cutoff
-    0.9 of the largest cell entry.
+    0.9 of the largest cell entry; with `heights`, that many heights
+    1 / |dual_a| of one periodic axis a instead (computed in double), so that
+    the repeat count ceil(rc |dual_a|) is decided at the ulp too.
     """
     import itertools
 
@@ -207,10 +209,16 @@ def lattice_point_case(seed: int, dtype, pbc) -> dict:
         f = rng.integers(-3, 4, 3).astype(dtype) + rng.choice([0.0, 0.5, 0.25], 3).astype(dtype)
         pts.append(f @ cell)
     pos = np.array(pts, dtype)
+    cutoff = float(cell.max()) * 0.9
+    if heights:
+        act = [a for a in range(3) if pbc[a]]
+        dual = np.linalg.pinv(cell.astype(np.float64)[act])  # columns: the active rows' duals
+        axis = seed % len(act)
+        cutoff = float(heights / np.linalg.norm(dual[:, axis]))
     return {
         "positions": pos,
         "cell": cell[None],
         "pbc": np.array([pbc], dtype=bool),
         "batch_ptr": np.array([0, len(pos)], dtype=np.int64),
-        "cutoff": float(cell.max()) * 0.9,
+        "cutoff": cutoff,
     }

@@ -11,7 +11,9 @@ skewed cells, rounded in the input type.  The CPU oracle, checked against
 the reference core on the same inputs (``tests/test_oracle.py``), is the
 anchor: every case's (i, j, S) multiset must equal the oracle's bit for
 bit, with D within the float64 formula's tolerance, for 40 cells, both
-dtypes, three periodicity patterns, both algorithms and all pair modes.
+dtypes, three periodicity patterns, both algorithms and two pair modes; and
+with the cutoff at one cell height, where the repeat count ceil(rc |dual_a|)
+is decided at the ulp as well.
 """
 
 from __future__ import annotations
@@ -46,3 +48,21 @@ def test_lattice_point_atoms_match_the_oracle(dtype, pbc):
                 torch.cuda.synchronize()
                 assert_same_keys(keys_of(P, S), keys_of(*oracle_call(full, algorithm=algorithm)))
                 assert_geometry_close(P, S, None, D, full)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("pbc", [[1, 1, 1], [1, 0, 1], [1, 1, 0]])
+def test_cutoff_at_a_cell_height_matches_the_oracle(dtype, pbc):
+    # the cutoff one height 1 / |dual_a| of a periodic axis (double):
+    # rc |dual_a| lies within rounding of 1, so the repeat count R_a = ceil(...)
+    # is decided at the ulp
+    print(f"[cell heights] {np.dtype(dtype).name} pbc={pbc}", flush=True)
+    for seed in range(20):
+        cfg = lattice_point_case(seed, dtype, pbc, heights=1)
+        t = [torch.as_tensor(cfg[k]).to(DEV) for k in ("positions", "cell", "pbc")]
+        bp = torch.as_tensor(cfg["batch_ptr"]).to(DEV)
+        for algorithm in ("brute_force", "cell_list"):
+            P, S, D = neighbor_list("PSD", *t, cfg["cutoff"], bp, algorithm=algorithm)
+            torch.cuda.synchronize()
+            assert_same_keys(keys_of(P, S), keys_of(*oracle_call(cfg, algorithm=algorithm)))
+            assert_geometry_close(P, S, None, D, cfg)

@@ -537,13 +537,14 @@ def test_quantities_invariants():
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("pbc", [[1, 1, 1], [1, 0, 1], [1, 1, 0]])
 def test_lattice_point_atoms_match_the_reference_core(dtype, pbc):
-    # atoms whose wraps are decided at the ulp (tests/_util.py,
-    # lattice_point_case): the long double pseudo-inverse and floor of the
-    # port give the reference core's pairs and shifts
+    # atoms whose wraps, and cutoffs whose repeat counts, are decided at the
+    # ulp (tests/_util.py, lattice_point_case): the long double
+    # pseudo-inverse, floor and ceil of the port give the reference core's
+    # pairs and shifts
     from tests._util import lattice_point_case
 
-    for seed in range(12):
-        cfg = lattice_point_case(seed, dtype, pbc)
+    for seed, heights in [(s_, 0) for s_ in range(12)] + [(s_, 1 + s_ % 2) for s_ in range(8)]:
+        cfg = lattice_point_case(seed, dtype, pbc, heights)
         for algorithm in ("brute_force", "cell_list"):
             args = (cfg["positions"], cfg["cell"], cfg["pbc"], cfg["cutoff"], cfg["batch_ptr"])
             port = keys_of(*oracle.neighbor_pairs(*args, algorithm=algorithm, threads=1,
