@@ -8,6 +8,8 @@ a CPU search.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -122,3 +124,37 @@ def test_workloads_are_deterministic():
     c4 = W.c4(n_atoms=1000)
     assert c4["positions"].dtype == np.float32 and c4["positions"].shape == (1000, 3)
     assert W.algorithmic_bytes(100_000, 9_046_552, "PD", 4) == 100_000 * 12 + 9_046_552 * 28
+
+
+def test_numpy_frontend_does_not_import_torch():
+    # tests/packaging/test_import_boundaries.py:21-44: a NumPy caller works in
+    # a process where importing torch fails
+    import subprocess
+    import sys
+    import textwrap
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = textwrap.dedent("""
+        import importlib.abc
+        import sys
+
+        class BlockTorch(importlib.abc.MetaPathFinder):
+            def find_spec(self, fullname, path, target=None):
+                if fullname == "torch" or fullname.startswith("torch."):
+                    raise ModuleNotFoundError("Torch import deliberately blocked")
+                return None
+
+        sys.meta_path.insert(0, BlockTorch())
+        sys.path.insert(0, %r)
+        import numpy as np
+        from tonari_amd import neighbor_list
+
+        positions = np.array([[0.0, 0.0, 0.0], [0.8, 0.0, 0.0]])
+        cell = np.eye(3) * 4.0
+        pbc = np.zeros(3, dtype=np.bool_)
+        pair_indices, cell_shifts = neighbor_list("PS", positions, cell, pbc, 1.0)
+        assert pair_indices.shape == (2, 2)
+        assert cell_shifts.shape == (2, 3)
+        assert "torch" not in sys.modules
+    """) % root
+    subprocess.run([sys.executable, "-c", code], check=True, timeout=120)
