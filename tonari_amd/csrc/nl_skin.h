@@ -77,7 +77,7 @@ enum SkinSlot : int {
     SK_TICKET = 6,     // tile tickets of that scan
     SK_STORE = 7,      // nonzero: the stored list cannot be filtered (SkinStoreBit)
 };
-static_assert(SK_STORE < kHostResultSlots, "filter status words reach the host");
+static_assert((int)SK_STORE < (int)kHostResultSlots, "filter status words reach the host");
 
 // Words that persist from the store to every filter of it.  The store's
 // scans use them as their status block (a stall raises ST_SCAN_STALL in
@@ -87,7 +87,8 @@ enum SkinStoreBit : unsigned long long {
     SKB_RANGE = 1,  // an atom index out of range, or a shift beyond the 10-bit fields
     SKB_RUNS = 2,   // more runs than atoms: the pairs of a source are not contiguous
 };
-static_assert(SS_FLAGS == SP_FLAGS, "the store's scans raise their stall flag in SP_FLAGS");
+static_assert((int)SS_FLAGS == (int)SP_FLAGS,
+              "the store's scans raise their stall flag in SP_FLAGS");
 
 // ------------------------------------------------------------ helpers
 
