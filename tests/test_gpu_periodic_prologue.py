@@ -2,14 +2,18 @@
 
 A repeated count of one fully periodic structure chooses its bin grid from
 the cell and the cutoff before any atom is reduced (``k_periodic_atoms``),
-ranks the atoms while the plan is finished (``k_periodic_rank``) and scans
-the bin counts per workgroup (``k_periodic_scatter``).  Every case here drives
-the hint through the C ABI and compares the emitted (i, j, S) multiset with
-the CPU oracle bit for bit and D with the float64 formula; the cases cover
-cubic and triclinic cells, both dtypes, all four pair modes, wrapped atoms,
-atoms far enough from the cell that the stencil reach has to grow, atoms so
-far that the margin outgrows the cutoff (planned as brute force), and the
-hint failing (slab, cluster, small structure under auto) with TNR_RETRY.
+then in one more launch (``k_periodic_place``) finishes the plan in one
+workgroup while the others rank the atoms in their bins, meet at a grid
+barrier, scan the bin counts (whole in every workgroup up to 8,192 bins, in
+slices between two more barriers beyond) and place the atoms.  Every case
+here drives the hint through the C ABI and compares the emitted (i, j, S)
+multiset with the CPU oracle bit for bit and D with the float64 formula; the
+cases cover cubic and triclinic cells, both dtypes, all four pair modes,
+wrapped atoms, more bins than one workgroup scans, atoms far enough from the
+cell that the stencil reach has to grow, atoms so far that the margin
+outgrows the cutoff (planned as brute force), the hint failing (slab,
+cluster, small structure under auto) with TNR_RETRY, and barrier waits
+forced to expire (TNR_PLACE_WAIT_US=0).
 """
 
 from __future__ import annotations
@@ -36,8 +40,9 @@ MODES = [(False, False), (False, True), (True, False), (True, True)]
 
 
 def search(cfg, hint, *, algorithm="cell_list", half_list=False, include_self=False,
-           sorted=False):
-    """Count with `hint`, then emit P, S, D; returns (code, message, plan, P, S, D)."""
+           sorted=False, info=None):
+    """Count with `hint`, then emit P, S, D; returns (code, message, plan, P, S, D).
+    `info`, when given, receives the count's bin total ("bins")."""
     lib = load_torch_hip()
     t = {k: torch.as_tensor(cfg[k]).to(DEV) for k in ("positions", "cell", "pbc", "batch_ptr")}
     pos = t["positions"]
@@ -62,6 +67,8 @@ def search(cfg, hint, *, algorithm="cell_list", half_list=False, include_self=Fa
     n = ctypes.c_int64(-1)
     code = lib.tnr_count_finish(host.data_ptr(), ctypes.byref(n), err, len(err))
     plan = int(host[3])
+    if info is not None:
+        info["bins"] = int(host[4])
     if code != TNR_OK:
         return code, err.value.decode(), plan, None, None, None
     E = int(n.value)
@@ -123,6 +130,46 @@ def test_wrapped_atoms(dtype):
         cfg = box(2500, (26.0, 24.0, 27.0), angles, dtype, 5.0, seed, shift=3)
         for half_list, include_self in MODES:
             check(cfg, half_list=half_list, include_self=include_self)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+def test_many_bins_take_the_sliced_scan(dtype):
+    # a sparse 90 A box at rc 3: more bins than one workgroup scans whole
+    # (8,192), so the bin counts are summed and scanned in slices
+    print(f"[periodic] sliced bin scan {np.dtype(dtype).name}", flush=True)
+    cfg = box(10000, (90.0, 90.0, 90.0), (90, 90, 90), dtype, 3.0, 44)
+    for half_list, include_self in ((False, False), (True, True)):
+        info = {}
+        check(cfg, half_list=half_list, include_self=include_self, info=info)
+        assert info["bins"] > 8192, info
+    check(box(9000, (80.0, 85.0, 90.0), (80, 100, 95), dtype, 3.0, 45, shift=1))
+
+
+def test_expired_barrier_waits_count_again(monkeypatch):
+    # a wait bound of zero: workgroups that have to wait at a barrier give up
+    # and the count reports that the hint does not hold (the caller counts
+    # again without it); a count whose workgroups never wait succeeds.  Either
+    # way the frontend's result is the oracle's.
+    monkeypatch.setenv("TNR_PLACE_WAIT_US", "0")
+    for cfg in (box(40000, (70.0, 70.0, 70.0), (90, 90, 90), np.float32, 6.0, 46),
+                box(10000, (90.0, 90.0, 90.0), (90, 90, 90), np.float32, 3.0, 47)):
+        print(f"[periodic] wait bound 0, {len(cfg['positions'])} atoms", flush=True)
+        full = dict(cfg, half_list=False, include_self=False)
+        expected = keys_of(*oracle_call(full, algorithm="cell_list"))
+        code, msg, plan, P, S, D = search(full, HINT)
+        assert code in (TNR_OK, TNR_RETRY), (code, msg)
+        if code == TNR_RETRY:
+            assert "plan hint" in msg, msg
+        else:
+            assert_same_keys(keys_of(P, S), expected)
+        t = {k: torch.as_tensor(cfg[k]).to(DEV) for k in ("positions", "cell", "pbc", "batch_ptr")}
+        _speculation().clear()
+        for call in range(3):
+            P, S, D = neighbor_list("PSD", t["positions"], t["cell"], t["pbc"], cfg["cutoff"],
+                                    t["batch_ptr"], algorithm="cell_list")
+            torch.cuda.synchronize()
+            assert_same_keys(keys_of(P, S), expected)
+            assert_geometry_close(P, S, None, D, cfg)
 
 
 def test_c1_auto_and_c4_sizes():

@@ -169,7 +169,8 @@ struct Layout {
     size_t status, structs, struct_bins, struct_bin_off, struct_units, struct_unit_off,
         atom_struct, atom_wrap, atom_q, binned_w, binned_p,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets,
-        block_partials, masks, tiles_bins, tiles_pairs, struct_meta, total;
+        block_partials, masks, tiles_bins, tiles_pairs, struct_meta, place, place_flags,
+        place_cnt, total;
     int64_t cap_bins, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
 };
 
@@ -228,6 +229,24 @@ constexpr int64_t kMolLocalMax = 64 * 64;  // 64 workgroups of 64 structures: on
 // slice pair counts fill the first words of its hit-mask slot).
 constexpr int kMaxSlices = 32;
 
+// Placing kernel of the periodic fast prologue (k_periodic_place): grid
+// barrier counters, one per group of workgroups (blockIdx % 8) and one for
+// the groups, each alone in a 128-byte line, followed by one slice sum per
+// workgroup (place); one flag per k_periodic_atoms workgroup, set when one
+// of its atoms is wrapped (place_flags); and the bin counters of the
+// ranking atomics, kPlaceStride ints apart (place_cnt: returning atomics on
+// adjacent 4-byte counters took about three times as long on gfx950 as on
+// counters 8 bytes apart, 100,000 atomics on 4,096 bins; wider spacing
+// gained nothing more).  The barrier and bin counters are zeroed by
+// k_periodic_atoms.  Up to kPlaceScanMax bins every workgroup scans the bin
+// counts whole (one barrier); beyond, slices of the bins are summed and
+// scanned (three).
+constexpr int kPlaceLine = 16;
+constexpr int kPlaceCounters = 9;
+constexpr int kPlaceStride = 2;
+constexpr unsigned kPlaceFirst = 8;  // workgroups of k_periodic_place before the placing ones
+constexpr int64_t kPlaceScanMax = 8192;
+
 constexpr int64_t kScanItems = 8;
 constexpr int64_t kScanChunk = kBlock * kScanItems;
 // Items per thread of the single-pass scan.
@@ -271,6 +290,10 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize, int mask_words) {
     L.tiles_bins = take(sizeof(unsigned long long) * (size_t)L.n_tiles_bins);
     L.tiles_pairs = take(sizeof(unsigned long long) * (size_t)L.n_tiles_pairs);
     L.struct_meta = take(sizeof(PlanSummary) * (size_t)(b + 1));
+    L.place = take(sizeof(unsigned long long) *
+                   (size_t)(kPlaceCounters * kPlaceLine + L.n_atom_blocks + 1));
+    L.place_flags = take(sizeof(int32_t) * (size_t)(L.n_atom_blocks + 1));
+    L.place_cnt = take(sizeof(int32_t) * kPlaceStride * (size_t)(L.cap_bins + 1));
     L.total = o;
     return L;
 }

@@ -1418,18 +1418,18 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
 // structure depends on the cell, the cutoff and the margin pad only, so it is
 // chosen from a margin estimate before any atom is reduced (periodic_grid)
 // and every atom is binned in the first kernel.  The margins are finished
-// from the atom reductions beside the bin scan, where the stencil reach is
-// refitted to the true margin (periodic_finish).
-//   k_periodic_atoms     set-up and grid per block; per atom: wraps, wrapped
-//                        position, block reductions, bin;
-//   k_periodic_rank      one returning atomic per atom on its bin counter;
-//   k_periodic_bin_scan  the bin scan (look-back), and in one more workgroup
-//                        the finished plan and the status words;
-//   k_scatter            as for every cell-list request.
-// Four launches, as the general single-structure prologue (k_atoms,
-// k_single_bin, the bin scan, k_scatter), but the reductions and the
-// planning no longer sit between the atom pass and the atomics (every
-// k_single_bin block re-reduces all partials and plans before it bins).
+// from the atom reductions beside the placing of the atoms, where the
+// stencil reach is refitted to the true margin (periodic_finish).
+//   k_periodic_atoms  set-up and grid per block; per atom: wraps, wrapped
+//                     position, block reductions, bin;
+//   k_periodic_place  in one workgroup the finished plan and the status
+//                     words; in the others the ranking atomics, a grid
+//                     barrier, the bin scan and the binned atoms.
+// Two launches against four for the general single-structure prologue
+// (k_atoms, k_single_bin, the bin scan, k_scatter): the reductions and the
+// planning do not sit between the atom pass and the atomics (every
+// k_single_bin block re-reduces all partials and plans before it bins), and
+// the bin scan and the scatter wait on a barrier instead of a launch.
 
 // First kernel of the periodic fast prologue (one thread per atom).  As
 // k_atoms<T, true> (every block derives the record in LDS, thread 0; per
@@ -1439,8 +1439,10 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
 // 0 stores the record and the status words: all zero but the bin total, or
 // ST_PLAN_HINT when the fast prologue does not apply (every later kernel then
 // skips its work and the caller counts again without the hint).  The grid
-// also zeroes the bin counters, the pair scan's tile states and the
-// per-source pair counts.
+// also zeroes the bin counters (k_periodic_place's, kPlaceStride ints
+// apart) and its barrier counters, the pair scan's tile states and the
+// per-source pair counts, and each block flags whether one of its atoms is
+// wrapped (place_flags).
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
     const T* pos, const int64_t* bp, const T* cells, const uint8_t* pbc, double cutoff, int mw,
@@ -1448,7 +1450,7 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
     int* atom_struct, int4* atom_wrap, Vec4<T>* atom_q, int* atom_bin,
     unsigned long long* status, int* bin_count, int64_t n_bin_count, unsigned long long* tiles,
     int64_t n_tiles, long long* counts, long long* struct_bins, long long* bin_off,
-    long long* struct_units, long long* unit_off) {
+    long long* struct_units, long long* unit_off, unsigned long long* place, int* place_flags) {
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
     __shared__ unsigned long long s_atom_flags;
     __shared__ int s_fast;
@@ -1458,6 +1460,7 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
         const int64_t stride = (int64_t)gridDim.x * kBlock;
         const int64_t k0 = (int64_t)blockIdx.x * kBlock + tid;
         if (k0 < n_atoms) counts[k0] = 0;
+        if (k0 < kPlaceCounters) place[k0 * kPlaceLine] = 0;
         for (int64_t k = k0; k < n_bin_count; k += stride) bin_count[k] = 0;
         for (int64_t k = k0; k < n_tiles; k += stride) tiles[k] = 0;
     }
@@ -1586,9 +1589,16 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
         partials[blockIdx.x].red[e] = x;
     }
     if (tid == kRedCount) partials[blockIdx.x].flags = s_atom_flags;
+    if (tid == kRedCount + 1) {
+        unsigned long long w = 0;
+#pragma unroll
+        for (int k = 0; k < kWavesPerBlock; ++k)
+            w |= s_red[k][kRedW] | s_red[k][kRedW + 1] | s_red[k][kRedW + 2];
+        place_flags[blockIdx.x] = w != 0ull ? 1 : 0;
+    }
 }
 
-// Last workgroup of k_periodic_bin_scan: the reductions of every k_periodic_atoms
+// Workgroup 0 of k_periodic_place: the reductions of every k_periodic_atoms
 // block, the margins (plan_margins), the reference's layout rule for an
 // explicit cell_list, and the stencil reach refitted to the true margin
 // (bins of the chosen grid, a padded cutoff of rc + 2 pad); a structure whose
@@ -1706,34 +1716,212 @@ __device__ __forceinline__ void periodic_finish(const T* cells, int64_t n_atoms,
     if (st) atomicOr(status + SS_FLAGS, st);
 }
 
-// Second kernel of the periodic fast prologue: one returning atomic per
-// binned atom on its bin's counter (the atom's rank in the bin).
-__global__ __launch_bounds__(kBlock) void k_periodic_rank(int64_t n_atoms, const int* atom_bin,
-                                                           int* atom_rank, int* bin_count) {
-    const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    if (i >= n_atoms) return;
-    const int g = atom_bin[i];
-    if (g >= 0) atom_rank[i] = atomicAdd(bin_count + g, 1);
+// Grid barrier of k_periodic_place, for its nblk workgroups blk = 0 ..
+// nblk - 1 (all resident at once): every wave first waits for its own
+// memory operations (its atomics have been performed, its stores written),
+// then thread 0 adds the workgroup to its group's counter (blk % 8), the
+// group's last arrival adds the group to the groups' counter, and thread 0
+// waits for that counter to reach round x groups (the counters only grow:
+// round is the barrier's number, from 1).  Everything that crosses
+// workgroups inside the kernel is read with device-scope atomic loads
+// (place_load), so no fence writes back or invalidates the XCD's L2 (an
+// agent-scope fence does both, and one per wave on each side cost tens of
+// microseconds on C4).  The wait is bounded by `ticks` of the constant-rate
+// clock (s_memrealtime); false when it expired.
+__device__ __forceinline__ bool place_barrier(unsigned long long* ctr, unsigned nblk, unsigned blk,
+                                              unsigned round, long long ticks) {
+    __shared__ int s_ok;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned x = blk & 7u;
+        const unsigned long long members = (nblk - x + 7u) / 8u;
+        const unsigned long long groups = nblk < 8u ? nblk : 8u;
+        const unsigned long long old = atomicAdd(ctr + x * kPlaceLine, 1ull);
+        if (old + 1ull == round * members) atomicAdd(ctr + 8 * kPlaceLine, 1ull);
+        const unsigned long long want = round * groups;
+        const long long t0 = (long long)wall_clock64();
+        int ok = 1;
+        while (__hip_atomic_load(ctr + 8 * kPlaceLine, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) < want) {
+            if ((long long)wall_clock64() - t0 > ticks) {
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        s_ok = ok;
+    }
+    __syncthreads();
+    return s_ok != 0;
 }
 
-// Third kernel of the periodic fast prologue: the look-back scan of the bin
-// counts (bin starts), and in its last workgroup, which takes no scan tile,
-// the finished plan (periodic_finish), which leaves the bin total the scan
-// reads alone.  Per-block timestamps on C4: run beside the ranking atomics,
-// the finishing workgroup waited 7.8 us for its loads of the block partials.
+template <typename V>
+__device__ __forceinline__ V place_load(const V* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ void place_store(V* p, V v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Atom i (record q) to binned position `at`, with its wraps and original
+// position when some atom of the request is wrapped.
 template <typename T>
-__global__ __launch_bounds__(kBlock) void k_periodic_bin_scan(
+__device__ __forceinline__ void place_atom(int64_t i, int at, Vec4<T> q, bool wrapped,
+                                           const T* pos, const int4* atom_wrap, Vec4<T>* binned,
+                                           int4* binned_w, Vec4<T>* binned_p) {
+    binned[at] = q;
+    if (wrapped) {
+        binned_w[at] = atom_wrap[i];
+        binned_p[at] = Vec4<T>{pos[3 * i], pos[3 * i + 1], pos[3 * i + 2], q.w};
+    }
+}
+
+// Second and last kernel of the periodic fast prologue: ranks, bin starts
+// and the binned atoms in one launch.  Workgroup 0 finishes the plan
+// (periodic_finish: it leaves the bin total alone), workgroups 1 .. 7 leave
+// at once, and workgroups 8 + blk, blk = 0 .. G - 1 (G no more than the
+// device holds at once beside them), take the atoms i = (blk + k G) 256 +
+// thread: for k = 0 the atoms k_periodic_atoms block blk wrote, on the
+// same XCD (workgroup b runs on XCD b % 8), so their records are read from
+// that XCD's L2 (read from another XCD's writes, the loads took a median
+// 8 us on C4 against under 1 us):
+//   1. one returning atomic per binned atom on its bin's counter (its rank
+//      in the bin), and whether any atom is wrapped (the flags of the
+//      k_periodic_atoms workgroups);
+//   2. grid barrier; up to kPlaceScanMax bins every workgroup scans the bin
+//      counts whole into LDS and writes its share of bin_start; beyond,
+//      each workgroup sums a slice of the bins, and after a second barrier
+//      scans its slice behind the sums of the slices before it (bin_start
+//      from memory after a third);
+//   3. each atom to binned[bin start + rank] (with its wraps and original
+//      position when some atom is wrapped).
+// A wait that expires (`ticks`; the workgroups could not all be resident)
+// raises ST_PLAN_HINT, so the caller counts again without the hint, and the
+// workgroup leaves: every wave exits.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_periodic_place(
     const T* cells, int64_t n_atoms, double cutoff, int requested, StructRec* recs,
     const BlockPartial* partials, int64_t n_partials, long long* struct_bins, long long* bin_off,
     long long* struct_units, long long* unit_off, int64_t cap_bins, unsigned long long* status,
-    const int* bin_count, int* bin_start, unsigned long long* tiles) {
-    if (blockIdx.x + 1 == gridDim.x) {
-        periodic_finish<T>(cells, n_atoms, cutoff, requested, recs, partials, n_partials,
-                           struct_bins, bin_off, struct_units, unit_off, cap_bins, status);
+    const int* atom_bin, int* atom_rank, int* place_cnt, int* bin_start, const Vec4<T>* atom_q,
+    Vec4<T>* binned, const T* pos, const int4* atom_wrap, int4* binned_w, Vec4<T>* binned_p,
+    unsigned long long* place, const int* place_flags, long long ticks) {
+    if (blockIdx.x < kPlaceFirst) {
+        if (blockIdx.x == 0)
+            periodic_finish<T>(cells, n_atoms, cutoff, requested, recs, partials, n_partials,
+                               struct_bins, bin_off, struct_units, unit_off, cap_bins, status);
         return;
     }
-    scan_lookback_block<int, int>(bin_count, cap_bins, status + SS_TOTAL_BINS, bin_start, tiles,
-                                  status + SS_TICKET_BINS, status, nullptr, nullptr);
+    // bin starts of the whole scan, entry k at k + k / 32 (each thread's 32
+    // consecutive bins fall in 32 different banks)
+    __shared__ int s_start[kPlaceScanMax + kPlaceScanMax / 32 + 1];
+    const int tid = threadIdx.x;
+    const unsigned G = gridDim.x - kPlaceFirst, blk = blockIdx.x - kPlaceFirst;
+    // ST_PLAN_HINT here comes from k_periodic_atoms (the same for every
+    // workgroup) or from an expired wait; the finishing workgroup's error
+    // bits are left to the later kernels
+    if (load_status(status + SS_FLAGS) & ST_PLAN_HINT) return;
+    const int64_t stride = (int64_t)G * kBlock;
+    const int64_t i0 = (int64_t)blk * kBlock + tid;
+    int g0 = -1, r0 = 0;
+    Vec4<T> q0{T(0), T(0), T(0), T(0)};
+    if (i0 < n_atoms) {
+        g0 = atom_bin[i0];
+        q0 = atom_q[i0];
+    }
+    if (g0 >= 0) r0 = atomicAdd(place_cnt + (int64_t)g0 * kPlaceStride, 1);
+    for (int64_t i = i0 + stride; i < n_atoms; i += stride) {
+        const int g = atom_bin[i];
+        if (g >= 0) atom_rank[i] = atomicAdd(place_cnt + (int64_t)g * kPlaceStride, 1);
+    }
+    int wf = 0;
+    for (int64_t k = tid; k < n_partials; k += kBlock) wf |= place_flags[k];
+    const bool wrapped = __syncthreads_or(wf) != 0;
+    unsigned long long* ctr = place;
+    if (!place_barrier(ctr, G, blk, 1u, ticks)) {
+        if (tid == 0) atomicOr(status + SS_FLAGS, ST_PLAN_HINT);
+        return;
+    }
+    const int64_t nbins = (int64_t)load_status(status + SS_TOTAL_BINS);
+    const bool whole = nbins <= kPlaceScanMax;
+    auto lds = [](int64_t k) { return (int)(k + (k >> 5)); };
+    if (whole) {
+        // the counts into LDS, 256 consecutive bins per load (all loads
+        // issued before the first is stored); then each thread scans 32
+        // consecutive bins
+        constexpr int kPer = (int)(kPlaceScanMax / kBlock);
+        int c[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int64_t g = (int64_t)k * kBlock + tid;
+            c[k] = g < nbins ? place_load(place_cnt + g * kPlaceStride) : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) s_start[lds((int64_t)k * kBlock + tid)] = c[k];
+        __syncthreads();
+        const int64_t base = (int64_t)tid * kPer;
+        long long sum = 0;
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            c[k] = s_start[lds(base + k)];
+            sum += c[k];
+        }
+        long long total;
+        long long run = block_exclusive_scan(sum, &total);
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            s_start[lds(base + k)] = (int)run;
+            run += c[k];
+        }
+        if (tid == 0) s_start[lds(nbins)] = (int)total;
+        __syncthreads();
+        for (int64_t k = (int64_t)blk * kBlock + tid; k <= nbins; k += stride)
+            bin_start[k] = s_start[lds(k)];
+    } else {
+        long long* slice = reinterpret_cast<long long*>(place + kPlaceCounters * kPlaceLine);
+        const int64_t S = (nbins + G - 1) / G;
+        const int64_t b0 = min((int64_t)blk * S, nbins), b1 = min(nbins, b0 + S);
+        long long sum = 0, total;
+        for (int64_t k = b0 + tid; k < b1; k += kBlock) sum += place_load(place_cnt + k * kPlaceStride);
+        (void)block_exclusive_scan(sum, &total);
+        if (tid == 0) place_store(slice + blk, total);
+        if (!place_barrier(ctr, G, blk, 2u, ticks)) {
+            if (tid == 0) atomicOr(status + SS_FLAGS, ST_PLAN_HINT);
+            return;
+        }
+        long long before = 0;
+        for (int64_t k = tid; k < (int64_t)blk; k += kBlock) before += place_load(slice + k);
+        (void)block_exclusive_scan(before, &total);
+        long long run = total;
+        for (int64_t k0 = b0; k0 < b1; k0 += kBlock) {
+            const int64_t k = k0 + tid;
+            const long long x = k < b1 ? place_load(place_cnt + k * kPlaceStride) : 0;
+            const long long ex = block_exclusive_scan(x, &total);
+            if (k < b1) place_store(bin_start + k, (int)(run + ex));
+            run += total;
+        }
+        if (blk == G - 1 && tid == 0) place_store(bin_start + nbins, (int)run);
+        if (!place_barrier(ctr, G, blk, 3u, ticks)) {
+            if (tid == 0) atomicOr(status + SS_FLAGS, ST_PLAN_HINT);
+            return;
+        }
+    }
+    // the records stay in registers (place_atom takes them by value): an
+    // atom record whose address was taken (a by-reference lambda, or a
+    // select between it and a load) was kept in LDS at a 12-byte stride,
+    // whose misaligned 8-byte writes held the loads up by about 7 us per
+    // workgroup on C4, or in scratch memory
+    if (g0 >= 0)
+        place_atom<T>(i0, (whole ? s_start[lds(g0)] : place_load(bin_start + g0)) + r0, q0,
+                      wrapped, pos, atom_wrap, binned, binned_w, binned_p);
+    for (int64_t i = i0 + stride; i < n_atoms; i += stride) {
+        const int g = atom_bin[i];
+        if (g < 0) continue;
+        place_atom<T>(i, (whole ? s_start[lds(g)] : place_load(bin_start + g)) + atom_rank[i],
+                      atom_q[i], wrapped, pos, atom_wrap, binned, binned_w, binned_p);
+    }
 }
 
 }  // namespace tnr

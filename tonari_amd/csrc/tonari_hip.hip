@@ -12,9 +12,9 @@
 //              status words; then binning);
 //   tnr_count, one fully periodic structure with the plan hint of an
 //              earlier count: k_periodic_atoms (grid from the cell and
-//              cutoff; per atom also its bin) -> k_periodic_rank (bin
-//              atomics) -> k_periodic_bin_scan (bin starts, and the plan
-//              finished from the atom reductions) -> k_scatter;
+//              cutoff; per atom also its bin) -> k_periodic_place (the
+//              plan finished from the atom reductions; beside it the bin
+//              atomics, a grid barrier, bin starts and binned atoms);
 //   tnr_count, a batch: k_setup (zeroes the status words; per structure:
 //              batch_ptr checks, active pseudo-inverse, image repeats, grid
 //              frame) -> k_atoms<T, false> -> k_plan (one workgroup per
@@ -54,6 +54,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <mutex>
@@ -89,6 +90,9 @@ struct Views {
     unsigned long long* tiles_bins;
     unsigned long long* tiles_pairs;
     PlanSummary* struct_meta;
+    unsigned long long* place;
+    int* place_flags;
+    int* place_cnt;
 };
 
 static Views views(void* ws, const Layout& L) {
@@ -117,6 +121,9 @@ static Views views(void* ws, const Layout& L) {
     v.tiles_bins = (unsigned long long*)(base + L.tiles_bins);
     v.tiles_pairs = (unsigned long long*)(base + L.tiles_pairs);
     v.struct_meta = (PlanSummary*)(base + L.struct_meta);
+    v.place = (unsigned long long*)(base + L.place);
+    v.place_flags = (int*)(base + L.place_flags);
+    v.place_cnt = (int*)(base + L.place_cnt);
     return v;
 }
 
@@ -146,6 +153,32 @@ static int64_t resident_blocks() {
     v = per_cu * cus;
     cache[dev].store(v, std::memory_order_relaxed);
     return v;
+}
+
+// Bound of k_periodic_place's barrier waits, in ticks of the device's
+// constant-rate clock: TNR_PLACE_WAIT_US microseconds (read on every call;
+// default 20,000).  The wait only runs out when the placing workgroups cannot
+// all be resident (other kernels holding the device), and then the request
+// is counted again without the periodic plan hint; the variable lets a test
+// force that path.
+static long long barrier_ticks() {
+    static std::atomic<int> rate_khz[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int r = rate_khz[dev].load(std::memory_order_relaxed);
+    if (r <= 0) {
+        if (hipDeviceGetAttribute(&r, hipDeviceAttributeWallClockRate, dev) != hipSuccess ||
+            r <= 0)
+            r = 100000;
+        rate_khz[dev].store(r, std::memory_order_relaxed);
+    }
+    long long us = 20000;
+    if (const char* e = std::getenv("TNR_PLACE_WAIT_US")) {
+        char* end = nullptr;
+        const long long x = std::strtoll(e, &end, 10);
+        if (end != e && x >= 0 && x <= 60000000) us = x;
+    }
+    return us * (long long)r / 1000;
 }
 
 // Blocks of the persistent counting kernel: as many as the device holds at
@@ -295,8 +328,9 @@ static void dispatch_queries(const tnr_request* req, const Layout& L, const Quer
 //                   summaries);
 //   HINT_PERIODIC   one fully periodic structure planned as a cell list
 //                   whose grid periodic_grid chooses: the periodic fast
-//                   prologue (k_periodic_atoms, k_periodic_rank,
-//                   k_periodic_bin_scan; ST_PLAN_HINT if it does not apply).
+//                   prologue (k_periodic_atoms, k_periodic_place;
+//                   ST_PLAN_HINT if it does not apply, or if the placing
+//                   kernel's workgroups could not all be resident).
 enum CountHint : int { HINT_NONE = 0, HINT_BRUTE = 1, HINT_MOLECULES = 2, HINT_PERIODIC = 3 };
 
 template <typename T>
@@ -326,20 +360,27 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                                                     v.struct_unit_off, v.recs, v.status,
                                                     L.cap_bins, 0);
     } else if (periodic) {
-        // one fully periodic structure: set-up, grid, atoms and bins; ranks;
-        // the bin scan beside the finished plan (k_scatter follows below)
+        // one fully periodic structure: set-up, grid, atoms and bins; then
+        // the finished plan beside ranks, bin starts and binned atoms
         const unsigned nblk = blocks_for(n);
         k_periodic_atoms<T><<<nblk, kBlock, 0, stream>>>(
             (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc, req->cutoff,
             mw, n, req->algorithm, reach, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
-            (Vec4<T>*)v.atom_q, v.atom_bin, v.status, v.bin_count, L.cap_bins + 1, v.tiles_bins,
-            n_tiles, v.counts, v.struct_bins, v.struct_bin_off, v.struct_units,
-            v.struct_unit_off);
-        k_periodic_rank<<<nblk, kBlock, 0, stream>>>(n, v.atom_bin, v.atom_rank, v.bin_count);
-        k_periodic_bin_scan<T><<<(unsigned)(L.n_tiles_bins + 1), kBlock, 0, stream>>>(
+            (Vec4<T>*)v.atom_q, v.atom_bin, v.status, v.place_cnt,
+            kPlaceStride * (L.cap_bins + 1), v.tiles_bins, n_tiles, v.counts, v.struct_bins,
+            v.struct_bin_off, v.struct_units, v.struct_unit_off, v.place, v.place_flags);
+        // the placing workgroups (behind the finishing one and seven that
+        // leave at once) are no more than the device holds at once, so that
+        // every one reaches the barrier
+        const int64_t cap = resident_blocks<k_periodic_place<T>>() - (int64_t)kPlaceFirst;
+        const int64_t place_blocks = (int64_t)nblk < cap ? (int64_t)nblk : (cap > 1 ? cap : 1);
+        k_periodic_place<T><<<(unsigned)(place_blocks + kPlaceFirst), kBlock, 0, stream>>>(
             (const T*)req->cell, n, req->cutoff, req->algorithm, v.recs, v.block_partials,
             (int64_t)nblk, v.struct_bins, v.struct_bin_off, v.struct_units, v.struct_unit_off,
-            L.cap_bins, v.status, v.bin_count, v.bin_start, v.tiles_bins);
+            L.cap_bins, v.status, v.atom_bin, v.atom_rank, v.place_cnt, v.bin_start,
+            (const Vec4<T>*)v.atom_q, (Vec4<T>*)v.binned, (const T*)req->positions,
+            v.atom_wrap, v.binned_w, (Vec4<T>*)v.binned_p, v.place, v.place_flags,
+            barrier_ticks());
     } else if (nb == 1 && n > 0) {
         // one structure: set-up and atoms, then plan and binning, in two
         // launches; k_single_bin writes the status words
@@ -379,11 +420,10 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
                                                            (const Vec4<T>*)v.atom_q, v.atom_bin,
                                                            v.atom_rank, v.bin_count, v.status);
     }
-    if (n > 0 && cell_kernels) {
-        if (!periodic)
-            k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
-                v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
-                v.status + SS_TICKET_BINS, v.status, nullptr);
+    if (n > 0 && cell_kernels && !periodic) {
+        k_scan_lookback<int, int><<<(unsigned)(L.n_tiles_bins), kBlock, 0, stream>>>(
+            v.bin_count, L.cap_bins, v.status + SS_TOTAL_BINS, v.bin_start, v.tiles_bins,
+            v.status + SS_TICKET_BINS, v.status, nullptr);
         k_scatter<T><<<blocks_for(n), kBlock, 0, stream>>>(n, (const Vec4<T>*)v.atom_q,
                                                            v.atom_bin, v.atom_rank,
                                                            v.bin_start, (Vec4<T>*)v.binned,
