@@ -145,6 +145,25 @@ struct alignas(16) StructRec {
     int32_t mneed;       // brute force: hit-mask words per atom the structure wants
 };
 
+// Memo of the periodic fast prologue's set-up: the record k_periodic_atoms
+// derives before its atom pass (setup_structure, then the grid of
+// periodic_grid), with every input it depends on as the key (batch_ptr, the
+// cell, pbc, atoms, cutoff, mask words, algorithm, reach, dtype) and a
+// checksum over key, flag and record.  k_periodic_place's finishing
+// workgroup writes it (after k_periodic_atoms has finished, before the next
+// request's starts); the next request's k_periodic_atoms takes the record
+// from it when every key word and the checksum match, and otherwise derives
+// it.
+constexpr int kMemoKey = 20;
+struct alignas(16) PeriodicMemo {
+    unsigned long long key[kMemoKey];
+    unsigned long long check;
+    unsigned long long fast;
+    StructRec rec;
+};
+constexpr int kMemoRecWords = (int)(sizeof(StructRec) / sizeof(unsigned long long));
+constexpr int kMemoWords = kMemoKey + 1 + kMemoRecWords;  // words the checksum covers
+
 // Per-block reduction record written by k_atoms for blocks whose atoms all
 // lie in one structure (k_plan combines them without atomics); for a
 // single-structure request also the block's atom error bits.
@@ -170,7 +189,7 @@ struct Layout {
         atom_struct, atom_wrap, atom_q, binned_w, binned_p,
         atom_bin, atom_rank, bin_count, bin_start, binned, counts, offsets,
         block_partials, masks, tiles_bins, tiles_pairs, struct_meta, place, place_flags,
-        place_cnt, total;
+        place_cnt, memo, total;
     int64_t cap_bins, n_atom_blocks, n_tiles_bins, n_tiles_pairs;
 };
 
@@ -294,6 +313,7 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize, int mask_words) {
                    (size_t)(kPlaceCounters * kPlaceLine + L.n_atom_blocks + 1));
     L.place_flags = take(sizeof(int32_t) * (size_t)(L.n_atom_blocks + 1));
     L.place_cnt = take(sizeof(int32_t) * kPlaceStride * (size_t)(L.cap_bins + 1));
+    L.memo = take(sizeof(PeriodicMemo));
     L.total = o;
     return L;
 }

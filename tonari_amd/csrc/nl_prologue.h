@@ -1431,6 +1431,100 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
 // k_single_bin block re-reduces all partials and plans before it bins), and
 // the bin scan and the scatter wait on a barrier instead of a launch.
 
+// Key word e < kMemoKey of a periodic fast prologue request (one lane per
+// word).
+template <typename T>
+__device__ __forceinline__ unsigned long long memo_key_word(int e, const int64_t* bp,
+                                                            const T* cells, const uint8_t* pbc,
+                                                            int64_t n_atoms, double cutoff, int mw,
+                                                            int requested, int reach_target) {
+    if (e < 2) return (unsigned long long)bp[e];
+    if (e < 11) return (unsigned long long)__double_as_longlong((double)cells[e - 2]);
+    switch (e) {
+        case 11:
+            return (unsigned long long)(pbc[0] != 0) | (unsigned long long)(pbc[1] != 0) << 8 |
+                   (unsigned long long)(pbc[2] != 0) << 16;
+        case 12: return (unsigned long long)n_atoms;
+        case 13: return (unsigned long long)__double_as_longlong(cutoff);
+        case 14: return (unsigned long long)(unsigned)mw;
+        case 15: return (unsigned long long)(unsigned)requested;
+        case 16: return (unsigned long long)(unsigned)reach_target;
+        case 17: return (unsigned long long)sizeof(T);
+        case 18: return (unsigned long long)sizeof(StructRec);
+        default: return 0x544e524d454d4f31ull;  // format tag
+    }
+}
+
+// Word i < kMemoWords of the memo's checksum cover (key, flag, record).
+__device__ __forceinline__ unsigned long long memo_word(const PeriodicMemo* m, int i) {
+    if (i < kMemoKey) return m->key[i];
+    if (i == kMemoKey) return m->fast;
+    return reinterpret_cast<const unsigned long long*>(&m->rec)[i - kMemoKey - 1];
+}
+
+// splitmix64 finaliser of a word and its index; the checksum is the XOR of
+// these over the covered words.
+__device__ __forceinline__ unsigned long long memo_mix(unsigned long long x, int i) {
+    x ^= (unsigned long long)(i + 1) * 0x9e3779b97f4a7c15ull;
+    x ^= x >> 30;
+    x *= 0xbf58476d1ce4e5b9ull;
+    x ^= x >> 27;
+    x *= 0x94d049bb133111ebull;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ unsigned long long wave_xor(unsigned long long x) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) x ^= __shfl_xor(x, d);
+    return x;
+}
+
+// One whole wave: whether the memo holds the set-up of this request (every
+// key word equal to the request's, the flag set and the checksum right).
+template <typename T>
+__device__ __forceinline__ bool memo_hit(const PeriodicMemo* m, const int64_t* bp,
+                                         const T* cells, const uint8_t* pbc, int64_t n_atoms,
+                                         double cutoff, int mw, int requested, int reach_target) {
+    const int lane = lane_id();
+    bool differs = false;
+    if (lane < kMemoKey)
+        differs = m->key[lane] != memo_key_word<T>(lane, bp, cells, pbc, n_atoms, cutoff, mw,
+                                                   requested, reach_target);
+    unsigned long long h = 0;
+    for (int i = lane; i < kMemoWords; i += kWave) h ^= memo_mix(memo_word(m, i), i);
+    h = wave_xor(h);
+    return !__builtin_amdgcn_ballot_w64(differs) && m->fast == 1ull && h == m->check;
+}
+
+// One whole wave: stores record r (the set-up of this request, in LDS) into
+// the memo with the request's key and the checksum.
+template <typename T>
+__device__ __forceinline__ void memo_store(PeriodicMemo* m, const StructRec& r, const int64_t* bp,
+                                           const T* cells, const uint8_t* pbc, int64_t n_atoms,
+                                           double cutoff, int mw, int requested,
+                                           int reach_target) {
+    const int lane = lane_id();
+    const unsigned long long* rw = reinterpret_cast<const unsigned long long*>(&r);
+    unsigned long long h = 0;
+    if (lane < kMemoKey) {
+        const unsigned long long k =
+            memo_key_word<T>(lane, bp, cells, pbc, n_atoms, cutoff, mw, requested, reach_target);
+        m->key[lane] = k;
+        h ^= memo_mix(k, lane);
+    }
+    if (lane == 0) {
+        m->fast = 1ull;
+        h ^= memo_mix(1ull, kMemoKey);
+    }
+    unsigned long long* mr = reinterpret_cast<unsigned long long*>(&m->rec);
+    for (int j = lane; j < kMemoRecWords; j += kWave) {
+        mr[j] = rw[j];
+        h ^= memo_mix(rw[j], kMemoKey + 1 + j);
+    }
+    h = wave_xor(h);
+    if (lane == 0) m->check = h;
+}
+
 // First kernel of the periodic fast prologue (one thread per atom).  As
 // k_atoms<T, true> (every block derives the record in LDS, thread 0; per
 // atom the wraps, the wrapped position and the block reductions, written as
@@ -1450,10 +1544,11 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
     int* atom_struct, int4* atom_wrap, Vec4<T>* atom_q, int* atom_bin,
     unsigned long long* status, int* bin_count, int64_t n_bin_count, unsigned long long* tiles,
     int64_t n_tiles, long long* counts, long long* struct_bins, long long* bin_off,
-    long long* struct_units, long long* unit_off, unsigned long long* place, int* place_flags) {
+    long long* struct_units, long long* unit_off, unsigned long long* place, int* place_flags,
+    const PeriodicMemo* memo) {
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount];
     __shared__ unsigned long long s_atom_flags;
-    __shared__ int s_fast;
+    __shared__ int s_fast, s_hit;
     __shared__ StructRec s_rec;
     const int tid = threadIdx.x, lane = lane_id(), wv = tid / kWave;
     {
@@ -1469,34 +1564,55 @@ __global__ __launch_bounds__(kBlock) void k_periodic_atoms(
     T p_pre[3];
 #pragma unroll
     for (int c = 0; c < 3; ++c) p_pre[c] = pos[3 * ic + c];
-    if (tid == 0) {
-        setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, mw, 0, s_rec);
-        s_atom_flags = 0;
+    // the set-up of an earlier request with the same inputs, when the memo
+    // holds it (the record loads beside the key check)
+    constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(int4));
+    if (tid < kRecWords)
+        reinterpret_cast<int4*>(&s_rec)[tid] = reinterpret_cast<const int4*>(&memo->rec)[tid];
+    if (wv == 0) {
+        const bool hit = memo_hit<T>(memo, bp, cells, pbc, n_atoms, cutoff, mw, requested,
+                                     reach_target);
+        if (lane == 0) {
+            s_hit = hit ? 1 : 0;
+            s_fast = hit ? 1 : 0;
+            s_atom_flags = 0;
+        }
     }
     __syncthreads();
-    if (wv == 0) {
-        GridPlan gp;
-        const bool fast = periodic_grid<T>(s_rec, cells, cutoff, requested, reach_target, gp);
-        if (lane == 0) {
-            StructRec& r = s_rec;
-            r.bin0 = 0;
-            r.unit0 = 0;
-            r.algo = fast ? ALGO_CELL : ALGO_NONE;
-            r.nbins = fast ? gp.nbins : 0;
-            if (fast) {
+    if (!s_hit) {
+        if (tid == 0) setup_structure<T>(bp, cells, pbc, 1, n_atoms, cutoff, mw, 0, s_rec);
+        __syncthreads();
+        if (wv == 0) {
+            GridPlan gp;
+            const bool fast = periodic_grid<T>(s_rec, cells, cutoff, requested, reach_target, gp);
+            if (lane == 0) {
+                StructRec& r = s_rec;
+                r.bin0 = 0;
+                r.unit0 = 0;
+                r.algo = fast ? ALGO_CELL : ALGO_NONE;
+                r.nbins = fast ? gp.nbins : 0;
+                if (fast) {
 #pragma unroll
-                for (int a = 0; a < 3; ++a) {
-                    r.nb[a] = (int32_t)gp.nb[a];
-                    r.inv_w[a] = gp.inv_w[a];
-                    r.lo[a] = gp.lo[a];
-                    r.reach[a] = gp.reach[a];
+                    for (int a = 0; a < 3; ++a) {
+                        r.nb[a] = (int32_t)gp.nb[a];
+                        r.inv_w[a] = gp.inv_w[a];
+                        r.lo[a] = gp.lo[a];
+                        r.reach[a] = gp.reach[a];
+                    }
+                    r.zseg = gp.zs;
                 }
-                r.zseg = gp.zs;
+                s_fast = fast ? 1 : 0;
             }
-            s_fast = fast ? 1 : 0;
+        }
+        __syncthreads();
+    }
+    if (wv == 0) {
+        if (lane == 0) {
+            const StructRec& r = s_rec;
+            const bool fast = s_fast != 0;
             if (blockIdx.x == 0) {
                 recs[0] = r;
-                const long long nbins = fast ? (long long)gp.nbins : 0;
+                const long long nbins = fast ? (long long)r.nbins : 0;
                 struct_bins[0] = nbins;
                 bin_off[0] = 0;
                 bin_off[1] = nbins;
@@ -1610,7 +1726,9 @@ __device__ __forceinline__ void periodic_finish(const T* cells, int64_t n_atoms,
                                                 const BlockPartial* partials, int64_t n_partials,
                                                 long long* struct_bins, long long* bin_off,
                                                 long long* struct_units, long long* unit_off,
-                                                int64_t cap_bins, unsigned long long* status) {
+                                                int64_t cap_bins, unsigned long long* status,
+                                                const int64_t* bp, const uint8_t* pbc, int mw,
+                                                int reach_target, PeriodicMemo* memo) {
     using K = RedKeys<T>;
     __shared__ StructRec s_rec;
     __shared__ unsigned long long s_red[kWavesPerBlock][kRedCount + 1];
@@ -1645,6 +1763,10 @@ __device__ __forceinline__ void periodic_finish(const T* cells, int64_t n_atoms,
         for (int e = 0; e <= kRedCount; ++e) s_red[wv][e] = v[e];
     __syncthreads();
     if (wv != 0) return;
+    // the record as k_periodic_atoms derived it, for the next request with
+    // the same inputs (read here before this wave changes it)
+    memo_store<T>(memo, s_rec, bp, cells, pbc, n_atoms, cutoff, mw,
+                  requested, reach_target);
 #pragma unroll
     for (int e = 0; e <= kRedCount; ++e) v[e] = s_red[0][e];
 #pragma unroll
@@ -1807,11 +1929,13 @@ __global__ __launch_bounds__(kBlock) void k_periodic_place(
     long long* struct_units, long long* unit_off, int64_t cap_bins, unsigned long long* status,
     const int* atom_bin, int* atom_rank, int* place_cnt, int* bin_start, const Vec4<T>* atom_q,
     Vec4<T>* binned, const T* pos, const int4* atom_wrap, int4* binned_w, Vec4<T>* binned_p,
-    unsigned long long* place, const int* place_flags, long long ticks) {
+    unsigned long long* place, const int* place_flags, long long ticks, const int64_t* bp,
+    const uint8_t* pbc, int mw, int reach_target, PeriodicMemo* memo) {
     if (blockIdx.x < kPlaceFirst) {
         if (blockIdx.x == 0)
             periodic_finish<T>(cells, n_atoms, cutoff, requested, recs, partials, n_partials,
-                               struct_bins, bin_off, struct_units, unit_off, cap_bins, status);
+                               struct_bins, bin_off, struct_units, unit_off, cap_bins, status,
+                               bp, pbc, mw, reach_target, memo);
         return;
     }
     // bin starts of the whole scan, entry k at k + k / 32 (each thread's 32

@@ -93,6 +93,7 @@ struct Views {
     unsigned long long* place;
     int* place_flags;
     int* place_cnt;
+    PeriodicMemo* memo;
 };
 
 static Views views(void* ws, const Layout& L) {
@@ -124,6 +125,7 @@ static Views views(void* ws, const Layout& L) {
     v.place = (unsigned long long*)(base + L.place);
     v.place_flags = (int*)(base + L.place_flags);
     v.place_cnt = (int*)(base + L.place_cnt);
+    v.memo = (PeriodicMemo*)(base + L.memo);
     return v;
 }
 
@@ -368,7 +370,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
             mw, n, req->algorithm, reach, v.recs, v.block_partials, v.atom_struct, v.atom_wrap,
             (Vec4<T>*)v.atom_q, v.atom_bin, v.status, v.place_cnt,
             kPlaceStride * (L.cap_bins + 1), v.tiles_bins, n_tiles, v.counts, v.struct_bins,
-            v.struct_bin_off, v.struct_units, v.struct_unit_off, v.place, v.place_flags);
+            v.struct_bin_off, v.struct_units, v.struct_unit_off, v.place, v.place_flags, v.memo);
         // the placing workgroups (behind the finishing one and seven that
         // leave at once) are no more than the device holds at once, so that
         // every one reaches the barrier
@@ -380,7 +382,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
             L.cap_bins, v.status, v.atom_bin, v.atom_rank, v.place_cnt, v.bin_start,
             (const Vec4<T>*)v.atom_q, (Vec4<T>*)v.binned, (const T*)req->positions,
             v.atom_wrap, v.binned_w, (Vec4<T>*)v.binned_p, v.place, v.place_flags,
-            barrier_ticks());
+            barrier_ticks(), req->batch_ptr, req->pbc, mw, reach, v.memo);
     } else if (nb == 1 && n > 0) {
         // one structure: set-up and atoms, then plan and binning, in two
         // launches; k_single_bin writes the status words
