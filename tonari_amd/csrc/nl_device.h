@@ -145,16 +145,21 @@ struct alignas(16) StructRec {
     int32_t mneed;       // brute force: hit-mask words per atom the structure wants
 };
 
-// Memo of the periodic fast prologue's set-up: the record k_periodic_atoms
-// derives before its atom pass (setup_structure, then the grid of
-// periodic_grid), with every input it depends on as the key (batch_ptr, the
-// cell, pbc, atoms, cutoff, mask words, algorithm, reach, dtype) and a
-// checksum over key, flag and record.  k_periodic_place's finishing
-// workgroup writes it (after k_periodic_atoms has finished, before the next
-// request's starts); the next request's k_periodic_atoms takes the record
-// from it when every key word and the checksum match, and otherwise derives
-// it.
-constexpr int kMemoKey = 20;
+// Memo of a structure's set-up: a record with every input it depends on as
+// the key (batch_ptr, the cell, pbc, atoms, cutoff, mask words, algorithm,
+// reach, dtype, the structure's index and the batch size, and a tag for
+// the kind of record) and a checksum over key, flag and record.  Two kinds:
+//   the periodic fast prologue's record (setup_structure, then the grid of
+//   periodic_grid), in entry 0: written by k_periodic_place's finishing
+//   workgroup (after k_periodic_atoms has finished, before the next
+//   request's starts) and read by the next request's k_periodic_atoms;
+//   a batch's records (setup_structure), one entry per structure: read and
+//   written by the k_setup thread of that structure.
+// A record is taken from the memo when every key word and the checksum
+// match, and derived otherwise.
+constexpr int kMemoKey = 22;
+constexpr unsigned long long kMemoPeriodic = 0x544e52504552494full;  // tags of the two kinds
+constexpr unsigned long long kMemoSetup = 0x544e525345545550ull;
 struct alignas(16) PeriodicMemo {
     unsigned long long key[kMemoKey];
     unsigned long long check;
@@ -313,7 +318,7 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize, int mask_words) {
                    (size_t)(kPlaceCounters * kPlaceLine + L.n_atom_blocks + 1));
     L.place_flags = take(sizeof(int32_t) * (size_t)(L.n_atom_blocks + 1));
     L.place_cnt = take(sizeof(int32_t) * kPlaceStride * (size_t)(L.cap_bins + 1));
-    L.memo = take(sizeof(PeriodicMemo));
+    L.memo = take(sizeof(PeriodicMemo) * (size_t)(b > 1 ? b : 1));
     L.total = o;
     return L;
 }

@@ -338,12 +338,136 @@ __device__ __forceinline__ void store_records(const StructRec* s_recs, StructRec
 // (store_records).  Block 0 first zeroes the status block of the request
 // (every later kernel reads it).  Per-structure errors go to the record
 // (k_plan folds them into the status words), so no thread races the zeroing.
+// Key word e < kMemoKey of structure b of a request, for a memo entry of
+// kind `tag` (kMemoPeriodic with the request's algorithm and reach, or
+// kMemoSetup).
+template <typename T>
+__device__ __forceinline__ unsigned long long memo_key_word(int e, const int64_t* bp,
+                                                            const T* cells, const uint8_t* pbc,
+                                                            int64_t nb, int64_t b,
+                                                            int64_t n_atoms, double cutoff, int mw,
+                                                            int requested, int reach_target,
+                                                            unsigned long long tag) {
+    if (e < 2) return (unsigned long long)bp[b + e];
+    if (e < 11) return (unsigned long long)__double_as_longlong((double)cells[9 * b + e - 2]);
+    switch (e) {
+        case 11:
+            return (unsigned long long)(pbc[3 * b] != 0) |
+                   (unsigned long long)(pbc[3 * b + 1] != 0) << 8 |
+                   (unsigned long long)(pbc[3 * b + 2] != 0) << 16;
+        case 12: return (unsigned long long)n_atoms;
+        case 13: return (unsigned long long)__double_as_longlong(cutoff);
+        case 14: return (unsigned long long)(unsigned)mw;
+        case 15: return (unsigned long long)(unsigned)requested;
+        case 16: return (unsigned long long)(unsigned)reach_target;
+        case 17: return (unsigned long long)sizeof(T);
+        case 18: return (unsigned long long)sizeof(StructRec);
+        case 19: return (unsigned long long)b;
+        case 20: return (unsigned long long)nb;
+        default: return tag;
+    }
+}
+
+// Word i < kMemoWords of the memo's checksum cover (key, flag, record).
+__device__ __forceinline__ unsigned long long memo_word(const PeriodicMemo* m, int i) {
+    if (i < kMemoKey) return m->key[i];
+    if (i == kMemoKey) return m->fast;
+    return reinterpret_cast<const unsigned long long*>(&m->rec)[i - kMemoKey - 1];
+}
+
+// Word i of the checksum cover, made position-dependent: plus a constant of
+// i, rotated by an amount of i (a bijection of the word, so a single changed
+// word always changes the checksum); the checksum is the XOR of these.
+__device__ __forceinline__ unsigned long long memo_mix(unsigned long long x, int i) {
+    x += (unsigned long long)(i + 1) * 0x9e3779b97f4a7c15ull;
+    const int r = (i * 7 + 1) & 63;
+    return (x << r) | (x >> ((64 - r) & 63));
+}
+
+__device__ __forceinline__ unsigned long long wave_xor(unsigned long long x) {
+#pragma unroll
+    for (int d = kWave / 2; d > 0; d >>= 1) x ^= __shfl_xor(x, d);
+    return x;
+}
+
+// One thread: whether memo entry m holds the set-up of structure b (every
+// key word equal, the flag set and the checksum right); copies the record
+// into r when it does.  The key, checksum and flag load together (twelve
+// 16-byte loads), the record only when the key matches, eleven 16-byte
+// loads at a time.
+template <typename T>
+__device__ __forceinline__ bool memo_take_setup(const PeriodicMemo* m, const int64_t* bp,
+                                                const T* cells, const uint8_t* pbc, int64_t nb,
+                                                int64_t b, int64_t n_atoms, double cutoff, int mw,
+                                                StructRec& r) {
+    static_assert(kMemoKey == 22 && offsetof(PeriodicMemo, check) == 22 * 8 &&
+                      offsetof(PeriodicMemo, fast) == 23 * 8 &&
+                      offsetof(PeriodicMemo, rec) == 24 * 8,
+                  "key, checksum and flag fill the first twelve 16-byte words");
+    const ulonglong2* head = reinterpret_cast<const ulonglong2*>(m);
+    ulonglong2 kw[12];
+#pragma unroll
+    for (int q = 0; q < 12; ++q) kw[q] = head[q];
+    bool same = kw[11].y == 1ull;
+    unsigned long long h = memo_mix(1ull, kMemoKey);
+#pragma unroll
+    for (int i = 0; i < kMemoKey; ++i) {
+        const unsigned long long w = (i & 1) ? kw[i / 2].y : kw[i / 2].x;
+        same = same && w == memo_key_word<T>(i, bp, cells, pbc, nb, b, n_atoms, cutoff, mw, 0, 0,
+                                              kMemoSetup);
+        h ^= memo_mix(w, i);
+    }
+    if (!same) return false;
+    constexpr int kRecWords = (int)(sizeof(StructRec) / sizeof(ulonglong2));
+    static_assert(kRecWords == 33, "the record loads in three batches of eleven");
+    const ulonglong2* src = reinterpret_cast<const ulonglong2*>(&m->rec);
+    ulonglong2* dst = reinterpret_cast<ulonglong2*>(&r);
+#pragma unroll
+    for (int q0 = 0; q0 < kRecWords; q0 += 11) {
+        ulonglong2 x[11];
+#pragma unroll
+        for (int q = 0; q < 11; ++q) x[q] = src[q0 + q];
+#pragma unroll
+        for (int q = 0; q < 11; ++q) {
+            h ^= memo_mix(x[q].x, kMemoKey + 1 + 2 * (q0 + q));
+            h ^= memo_mix(x[q].y, kMemoKey + 2 + 2 * (q0 + q));
+            dst[q0 + q] = x[q];
+        }
+    }
+    return h == kw[11].x;
+}
+
+// One thread: stores record r (the set-up of structure b) into memo entry m.
+template <typename T>
+__device__ __forceinline__ void memo_put_setup(PeriodicMemo* m, const StructRec& r,
+                                               const int64_t* bp, const T* cells,
+                                               const uint8_t* pbc, int64_t nb, int64_t b,
+                                               int64_t n_atoms, double cutoff, int mw) {
+    unsigned long long h = 0;
+    for (int i = 0; i < kMemoKey; ++i) {
+        const unsigned long long k =
+            memo_key_word<T>(i, bp, cells, pbc, nb, b, n_atoms, cutoff, mw, 0, 0, kMemoSetup);
+        m->key[i] = k;
+        h ^= memo_mix(k, i);
+    }
+    m->fast = 1ull;
+    h ^= memo_mix(1ull, kMemoKey);
+    const unsigned long long* rw = reinterpret_cast<const unsigned long long*>(&r);
+    unsigned long long* mr = reinterpret_cast<unsigned long long*>(&m->rec);
+    for (int j = 0; j < kMemoRecWords; ++j) {
+        mr[j] = rw[j];
+        h ^= memo_mix(rw[j], kMemoKey + 1 + j);
+    }
+    m->check = h;
+}
+
 template <typename T>
 __global__ __launch_bounds__(kSetupBlock) void k_setup(const int64_t* bp, const T* cells,
                                                        const uint8_t* pbc, int64_t nb,
                                                        int64_t n_atoms, double cutoff, int mw,
                                                        StructRec* recs,
-                                                       unsigned long long* status) {
+                                                       unsigned long long* status,
+                                                       PeriodicMemo* memo) {
     __shared__ StructRec s_recs[kSetupBlock];
     const int64_t b0 = (int64_t)blockIdx.x * kSetupBlock;
     const int64_t b = b0 + threadIdx.x;
@@ -357,8 +481,14 @@ __global__ __launch_bounds__(kSetupBlock) void k_setup(const int64_t* bp, const 
             status[SS_FLAGS] = st;
         }
     }
-    if (b < nb)
+    // the set-up of an earlier request with the same inputs, when the memo
+    // holds it; otherwise derived and stored there for the next request
+    if (b < nb && !memo_take_setup<T>(memo + b, bp, cells, pbc, nb, b, n_atoms, cutoff, mw,
+                                       s_recs[threadIdx.x])) {
         setup_structure<T>(bp, cells, pbc, nb, n_atoms, cutoff, mw, b, s_recs[threadIdx.x]);
+        memo_put_setup<T>(memo + b, s_recs[threadIdx.x], bp, cells, pbc, nb, b, n_atoms, cutoff,
+                          mw);
+    }
     if (b0 < nb) store_records(s_recs, recs, b0, min((int64_t)kSetupBlock, nb - b0));
 }
 
@@ -1431,54 +1561,6 @@ __global__ __launch_bounds__(kBlock) void k_scatter(int64_t n_atoms, const Vec4<
 // k_single_bin block re-reduces all partials and plans before it bins), and
 // the bin scan and the scatter wait on a barrier instead of a launch.
 
-// Key word e < kMemoKey of a periodic fast prologue request (one lane per
-// word).
-template <typename T>
-__device__ __forceinline__ unsigned long long memo_key_word(int e, const int64_t* bp,
-                                                            const T* cells, const uint8_t* pbc,
-                                                            int64_t n_atoms, double cutoff, int mw,
-                                                            int requested, int reach_target) {
-    if (e < 2) return (unsigned long long)bp[e];
-    if (e < 11) return (unsigned long long)__double_as_longlong((double)cells[e - 2]);
-    switch (e) {
-        case 11:
-            return (unsigned long long)(pbc[0] != 0) | (unsigned long long)(pbc[1] != 0) << 8 |
-                   (unsigned long long)(pbc[2] != 0) << 16;
-        case 12: return (unsigned long long)n_atoms;
-        case 13: return (unsigned long long)__double_as_longlong(cutoff);
-        case 14: return (unsigned long long)(unsigned)mw;
-        case 15: return (unsigned long long)(unsigned)requested;
-        case 16: return (unsigned long long)(unsigned)reach_target;
-        case 17: return (unsigned long long)sizeof(T);
-        case 18: return (unsigned long long)sizeof(StructRec);
-        default: return 0x544e524d454d4f31ull;  // format tag
-    }
-}
-
-// Word i < kMemoWords of the memo's checksum cover (key, flag, record).
-__device__ __forceinline__ unsigned long long memo_word(const PeriodicMemo* m, int i) {
-    if (i < kMemoKey) return m->key[i];
-    if (i == kMemoKey) return m->fast;
-    return reinterpret_cast<const unsigned long long*>(&m->rec)[i - kMemoKey - 1];
-}
-
-// splitmix64 finaliser of a word and its index; the checksum is the XOR of
-// these over the covered words.
-__device__ __forceinline__ unsigned long long memo_mix(unsigned long long x, int i) {
-    x ^= (unsigned long long)(i + 1) * 0x9e3779b97f4a7c15ull;
-    x ^= x >> 30;
-    x *= 0xbf58476d1ce4e5b9ull;
-    x ^= x >> 27;
-    x *= 0x94d049bb133111ebull;
-    return x ^ (x >> 31);
-}
-
-__device__ __forceinline__ unsigned long long wave_xor(unsigned long long x) {
-#pragma unroll
-    for (int d = kWave / 2; d > 0; d >>= 1) x ^= __shfl_xor(x, d);
-    return x;
-}
-
 // One whole wave: whether the memo holds the set-up of this request (every
 // key word equal to the request's, the flag set and the checksum right).
 template <typename T>
@@ -1488,8 +1570,8 @@ __device__ __forceinline__ bool memo_hit(const PeriodicMemo* m, const int64_t* b
     const int lane = lane_id();
     bool differs = false;
     if (lane < kMemoKey)
-        differs = m->key[lane] != memo_key_word<T>(lane, bp, cells, pbc, n_atoms, cutoff, mw,
-                                                   requested, reach_target);
+        differs = m->key[lane] != memo_key_word<T>(lane, bp, cells, pbc, 1, 0, n_atoms, cutoff,
+                                                   mw, requested, reach_target, kMemoPeriodic);
     unsigned long long h = 0;
     for (int i = lane; i < kMemoWords; i += kWave) h ^= memo_mix(memo_word(m, i), i);
     h = wave_xor(h);
@@ -1507,8 +1589,8 @@ __device__ __forceinline__ void memo_store(PeriodicMemo* m, const StructRec& r, 
     const unsigned long long* rw = reinterpret_cast<const unsigned long long*>(&r);
     unsigned long long h = 0;
     if (lane < kMemoKey) {
-        const unsigned long long k =
-            memo_key_word<T>(lane, bp, cells, pbc, n_atoms, cutoff, mw, requested, reach_target);
+        const unsigned long long k = memo_key_word<T>(lane, bp, cells, pbc, 1, 0, n_atoms, cutoff,
+                                                      mw, requested, reach_target, kMemoPeriodic);
         m->key[lane] = k;
         h ^= memo_mix(k, lane);
     }

@@ -400,7 +400,7 @@ static hipError_t run_count(const tnr_request* req, void* ws, const Layout& L,
         // the tile states of both single-pass scans.
         k_setup<T><<<blocks_for(nb > 0 ? nb : 1, kSetupBlock), kSetupBlock, 0, stream>>>(
             req->batch_ptr, (const T*)req->cell, req->pbc, nb, n, req->cutoff, mw, v.recs,
-            v.status);
+            v.status, v.memo);
         if (n > 0)
             k_atoms<T, false><<<blocks_for(n), kBlock, 0, stream>>>(
                 (const T*)req->positions, req->batch_ptr, (const T*)req->cell, req->pbc,
