@@ -314,10 +314,12 @@ inline Layout make_layout(int64_t n, int64_t b, size_t tsize, int mask_words) {
     L.tiles_bins = take(sizeof(unsigned long long) * (size_t)L.n_tiles_bins);
     L.tiles_pairs = take(sizeof(unsigned long long) * (size_t)L.n_tiles_pairs);
     L.struct_meta = take(sizeof(PlanSummary) * (size_t)(b + 1));
-    L.place = take(sizeof(unsigned long long) *
+    // the periodic fast prologue's regions (one structure only)
+    const size_t one = b == 1 ? 1 : 0;
+    L.place = take(one * sizeof(unsigned long long) *
                    (size_t)(kPlaceCounters * kPlaceLine + L.n_atom_blocks + 1));
-    L.place_flags = take(sizeof(int32_t) * (size_t)(L.n_atom_blocks + 1));
-    L.place_cnt = take(sizeof(int32_t) * kPlaceStride * (size_t)(L.cap_bins + 1));
+    L.place_flags = take(one * sizeof(int32_t) * (size_t)(L.n_atom_blocks + 1));
+    L.place_cnt = take(one * sizeof(int32_t) * kPlaceStride * (size_t)(L.cap_bins + 1));
     L.memo = take(sizeof(PeriodicMemo) * (size_t)(b > 1 ? b : 1));
     L.total = o;
     return L;
