@@ -156,9 +156,12 @@ int tnr_count_async(const tnr_request* req, void* workspace, size_t workspace_by
  * TNR_BRUTE_FORCE: one kernel plans the whole batch in place of the set-up,
  * atom and planning kernels.  Hint 10 (one periodic cell-list structure)
  * with TNR_AUTO or TNR_CELL_LIST: the bin grid is chosen before the atoms
- * are reduced and the prologue takes three launches instead of four, none
- * of them a device-wide scan.  The device checks the hint: if a structure
- * does not fit it,
+ * are reduced and the prologue takes two launches instead of four, the
+ * second ranking, scanning and placing the atoms behind a grid barrier
+ * whose waits are bounded by the environment variable TNR_PLACE_WAIT_US
+ * (microseconds of the device clock, default 20,000; a wait that expires
+ * makes the hint fail).  The device checks the hint: if a structure does
+ * not fit it,
  * nothing of this count is valid and tnr_count_finish returns TNR_RETRY;
  * the caller counts again without the hint.  Other hints launch the full
  * count.
