@@ -8,8 +8,9 @@ atoms stay within the skin and rebuilt after), for the pair policies and
 ``sorted``, with float32 coordinates far from the origin (the rounding
 margin), with a skin below that margin, for the rebuild triggers (a large
 move, a changed cell, pbc or batch_ptr, a new size), with no pairs at all, and
-against the CPU oracle directly.  Gradients of d and D equal the public
-call's.
+against the CPU oracle directly, all with the filter forced (``mode="filter"``);
+the ``"auto"`` and ``"search"`` modes along trajectories too.  Gradients of
+d and D equal the public call's.
 """
 
 from __future__ import annotations
@@ -85,7 +86,7 @@ def test_trajectory_equals_fresh_searches(name):
     cfg, dtype = CASES[name]()
     t = _t(cfg, dtype)
     skin = 1.0
-    vl = VerletList("PSdD", cfg["cutoff"], skin, algorithm="auto")
+    vl = VerletList("PSdD", cfg["cutoff"], skin, mode="filter", algorithm="auto")
     rng = np.random.default_rng(7)
     for step in range(8):
         print(f"[verlet] {name} step {step}", flush=True)
@@ -103,10 +104,38 @@ def test_trajectory_equals_fresh_searches(name):
     assert vl.builds == builds + 1
 
 
+@pytest.mark.parametrize("mode", ["auto", "search"])
+@pytest.mark.parametrize("name", ["C2_f32", "C4_f32"])
+def test_modes_equal_fresh_searches(name, mode):
+    # "search" searches afresh at every call; "auto" times one filtered call
+    # against a fresh search of the shape and keeps the faster path.  Every
+    # call returns the fresh search's pairs, d and D.
+    cfg, dtype = CASES[name]()
+    t = _t(cfg, dtype)
+    vl = VerletList("PSdD", cfg["cutoff"], 1.0, mode=mode)
+    rng = np.random.default_rng(8)
+    for step in range(6):
+        print(f"[verlet] {name} mode={mode} step {step}", flush=True)
+        _assert_equal_to_fresh(vl, t, cfg["cutoff"])
+        t = _walk(t, rng, 0.05)  # at most 0.25 after five steps: no rebuild
+    assert vl.calls == 6
+    if mode == "search":
+        assert vl.builds == 0 and vl.choice == {}
+    else:
+        (choice,) = vl.choice.values()
+        assert choice in ("filter", "search")
+        assert vl.builds == 1
+
+
+def test_mode_is_checked():
+    with pytest.raises(ValueError, match="mode"):
+        VerletList("PS", 3.0, 0.5, mode="fast")
+
+
 def test_small_moves_never_rebuild():
     cfg = W.c4(seed=52, n_atoms=8000)
     t = _t(cfg)
-    vl = VerletList("PSdD", cfg["cutoff"], 0.8)
+    vl = VerletList("PSdD", cfg["cutoff"], 0.8, mode="filter")
     rng = np.random.default_rng(8)
     base = t
     _assert_equal_to_fresh(vl, base, cfg["cutoff"])  # the build
@@ -122,7 +151,7 @@ def test_pair_policies_and_order(half_list, include_self, sorted_):
     cfg = W.c2(n_structures=24)
     t = _t(cfg)
     opts = dict(half_list=half_list, include_self=include_self, sorted=sorted_)
-    vl = VerletList("PSdD", cfg["cutoff"], 0.6, **opts)
+    vl = VerletList("PSdD", cfg["cutoff"], 0.6, mode="filter", **opts)
     rng = np.random.default_rng(9)
     for _ in range(3):
         P = _assert_equal_to_fresh(vl, t, cfg["cutoff"], **opts)
@@ -135,7 +164,7 @@ def test_pair_policies_and_order(half_list, include_self, sorted_):
 def test_quantities_follow_the_public_order():
     cfg = W.c2(n_structures=12)
     t = _t(cfg)
-    vl = VerletList("jdiS", cfg["cutoff"], 0.5, sorted=True)
+    vl = VerletList("jdiS", cfg["cutoff"], 0.5, mode="filter", sorted=True)
     for _ in range(2):
         j, d, i, S = vl(t["positions"], t["cell"], t["pbc"], t["batch_ptr"])
         P, Sf, df = neighbor_list("PSd", t["positions"], t["cell"], t["pbc"], cfg["cutoff"],
@@ -149,7 +178,7 @@ def test_quantities_follow_the_public_order():
 def test_rebuild_triggers():
     cfg = W.c2(n_structures=16)
     t = _t(cfg)
-    vl = VerletList("PSdD", cfg["cutoff"], 0.6)
+    vl = VerletList("PSdD", cfg["cutoff"], 0.6, mode="filter")
     _assert_equal_to_fresh(vl, t, cfg["cutoff"])
     assert vl.builds == 1
     # one atom moves by more than skin / 2
@@ -192,14 +221,14 @@ def test_far_float32_coordinates_and_a_skin_below_the_margin():
     # unwrapped coordinates several cells away: larger rounding, larger margin
     t["positions"] = t["positions"] + 4.0 * t["cell"][0, 0]
     rng = np.random.default_rng(10)
-    vl = VerletList("PSdD", cfg["cutoff"], 1.0)
+    vl = VerletList("PSdD", cfg["cutoff"], 1.0, mode="filter")
     for _ in range(3):
         _assert_equal_to_fresh(vl, t, cfg["cutoff"])
         t = _walk(t, rng, 0.1)
     assert vl.builds == 1
     # a skin far below the float32 rounding of these coordinates: every call
     # falls back to a direct search and still equals it
-    tiny = VerletList("PSdD", cfg["cutoff"], 1e-6)
+    tiny = VerletList("PSdD", cfg["cutoff"], 1e-6, mode="filter")
     for _ in range(2):
         _assert_equal_to_fresh(tiny, t, cfg["cutoff"])
         t = _walk(t, rng, 0.1)
@@ -208,7 +237,7 @@ def test_far_float32_coordinates_and_a_skin_below_the_margin():
 def test_no_pairs():
     cfg = W.c4(seed=54, n_atoms=500, density=0.001)
     t = _t(cfg)
-    vl = VerletList("PSdD", 0.05, 0.01)
+    vl = VerletList("PSdD", 0.05, 0.01, mode="filter")
     P, S, d, D = vl(t["positions"], t["cell"], t["pbc"], t["batch_ptr"])
     assert P.shape == (0, 2) and S.shape == (0, 3) and d.shape == (0,) and D.shape == (0, 3)
     t = _walk(t, np.random.default_rng(11), 0.001)
@@ -219,7 +248,7 @@ def test_no_pairs():
 def test_matches_the_oracle():
     cfg = W.c2(n_structures=16)
     t = _t(cfg)
-    vl = VerletList("PS", cfg["cutoff"], 0.7, half_list=True)
+    vl = VerletList("PS", cfg["cutoff"], 0.7, mode="filter", half_list=True)
     rng = np.random.default_rng(12)
     for _ in range(3):
         t = _walk(t, rng, 0.1)
@@ -232,7 +261,7 @@ def test_matches_the_oracle():
 def test_gradients_equal_the_public_call():
     cfg = W.c2(n_structures=8)
     t = _t(cfg, torch.float64)
-    vl = VerletList("dD", cfg["cutoff"], 0.5)
+    vl = VerletList("dD", cfg["cutoff"], 0.5, mode="filter")
     for _ in range(2):
         pos = t["positions"].clone().requires_grad_()
         cell = t["cell"].clone().requires_grad_()
@@ -259,7 +288,7 @@ def test_shifts_beyond_the_compact_records_fall_back_to_searches():
     pbc = torch.tensor([True, False, False], device=DEV)
     bp = torch.tensor([0, 3], device=DEV)
     t = {"positions": pos, "cell": cell[None], "pbc": pbc[None], "batch_ptr": bp}
-    vl = VerletList("PSdD", 30.0, 0.5)
+    vl = VerletList("PSdD", 30.0, 0.5, mode="filter")
     for _ in range(2):
         P = _assert_equal_to_fresh(vl, t, 30.0)
         assert P.shape[0] > 3000
@@ -286,7 +315,7 @@ def test_sources_recovered_across_tiles_and_empty_structures():
     }
     t = _t(cfg)
     for sorted_ in (True, False):
-        vl = VerletList("PSdD", 4.0, 0.8, sorted=sorted_)
+        vl = VerletList("PSdD", 4.0, 0.8, mode="filter", sorted=sorted_)
         for _ in range(3):
             P = _assert_equal_to_fresh(vl, t, 4.0, sorted=sorted_)
             assert P.shape[0] > 2 * 2048

@@ -20,12 +20,22 @@ the order of the stored list (a ``sorted`` list stays sorted; the pairs of a
 source stay contiguous).  Positions that an MD code wraps back into the cell
 move by a cell vector and so force a rebuild; wrap them only at rebuilds, or
 not at all.
+
+Filtering pays where a search is costly per kept pair (batches searched by
+brute force: C2 0.079 against 0.118 ms); where the search stages its
+candidates (a large periodic box under the cell list) it is the faster of
+the two.  So by default (``mode="auto"``) the first call of a request shape
+that filters without a rebuild also times a fresh search of the same inputs
+(wall time, a warm call after a warm-up one) and keeps the faster path for
+that shape; ``mode="filter"`` always filters and ``mode="search"`` always
+searches.  A search returns the same pairs in its own order.
 """
 
 from __future__ import annotations
 
 import contextlib
 import ctypes
+import time
 from math import isfinite
 
 import torch
@@ -73,12 +83,17 @@ class VerletList:
     ``include_self``); calling it with ``(positions, cell, pbc, batch_ptr)``
     returns the requested quantities for those inputs, like
     ``neighbor_list(quantities, positions, cell, pbc, cutoff, batch_ptr, ...)``,
-    with autograd on d and D as there.  ``builds`` counts the searches at
-    ``cutoff + skin``; ``calls`` counts the calls.  ROCm (HIP) tensors only.
+    with autograd on d and D as there.  ``mode`` (``"auto"``, ``"filter"`` or
+    ``"search"``) picks between filtering the stored list and a fresh search:
+    ``"auto"`` times both once per request shape (device, dtype, atoms,
+    structures) and keeps the faster, recorded in ``choice``.  ``builds``
+    counts the searches at ``cutoff + skin``; ``calls`` counts the calls.
+    ROCm (HIP) tensors only.
     """
 
     def __init__(self, quantities: str, cutoff: float, skin: float, *, algorithm: str = "auto",
-                 sorted: bool = False, half_list: bool = False, include_self: bool = False):
+                 sorted: bool = False, half_list: bool = False, include_self: bool = False,
+                 mode: str = "auto"):
         if not isinstance(quantities, str) or not quantities:
             raise ValueError("quantities must be a non-empty string")
         if set(quantities) - _VALID_QUANTITIES:
@@ -92,12 +107,17 @@ class VerletList:
             raise ValueError("algorithm must be 'auto', 'brute_force', or 'cell_list'")
         if not all(isinstance(o, bool) for o in (sorted, half_list, include_self)):
             raise TypeError("sorted, half_list, and include_self must be bool")
+        if mode not in ("auto", "filter", "search"):
+            raise ValueError("mode must be 'auto', 'filter', or 'search'")
         self.quantities = quantities
         self.cutoff, self.skin = cutoff, skin
         self.algorithm, self.sorted = algorithm, sorted
         self.half_list, self.include_self = half_list, include_self
+        self.mode = mode
         self.builds = 0
         self.calls = 0
+        # mode "auto": the faster path per request shape, once timed
+        self.choice: dict = {}
         self._stored: _Stored | None = None
         self._capacity: int | None = None
         self._host = None
@@ -129,22 +149,53 @@ class VerletList:
         key = (device, pos.dtype, pos.shape[0], batch_ptr.numel() - 1)
         switch = device.index is not None and device.index != torch.cuda.current_device()
         with torch.cuda.device(device) if switch else contextlib.nullcontext():
+            path = self.mode if self.mode != "auto" else self.choice.get(key)
+            if path == "search":
+                return self._search(pos, cel, pbc, batch_ptr, grad_positions, grad_cell)
             fresh = self._stored is None or self._stored.key != key
             if fresh:
                 self._build(lib, key, pos, cel, pbc, batch_ptr)
+            timing = self.mode == "auto" and path is None and not fresh
+            if timing:
+                torch.cuda.synchronize(device)
+                t0 = time.perf_counter()
             out = self._filter(lib, pos, cel, pbc, batch_ptr, grad_positions, grad_cell)
+            if timing and out is not None:
+                torch.cuda.synchronize(device)
+                t_filter = time.perf_counter() - t0
+                self.choice[key] = (
+                    "search" if self._time_search(device, pos, cel, pbc, batch_ptr) < t_filter
+                    else "filter"
+                )
             if out is None and not fresh:
                 self._build(lib, key, pos, cel, pbc, batch_ptr)
                 out = self._filter(lib, pos, cel, pbc, batch_ptr, grad_positions, grad_cell)
             if out is None:
                 # a skin below the rounding margin of these inputs: search directly
-                out = neighbor_list_hip(
-                    self.quantities, pos, batch_ptr, cel, pbc, self.cutoff,
-                    half_list=self.half_list, include_self=self.include_self,
-                    algorithm=self.algorithm, sorted=self.sorted,
-                    grad_positions=grad_positions, grad_cell=grad_cell,
-                )
+                out = self._search(pos, cel, pbc, batch_ptr, grad_positions, grad_cell)
         return out
+
+    def _search(self, pos: Tensor, cell: Tensor, pbc: Tensor, batch_ptr: Tensor,
+                grad_positions, grad_cell) -> tuple[Tensor, ...]:
+        """A fresh search of these inputs at the cutoff."""
+        return neighbor_list_hip(
+            self.quantities, pos, batch_ptr, cell, pbc, self.cutoff,
+            half_list=self.half_list, include_self=self.include_self,
+            algorithm=self.algorithm, sorted=self.sorted,
+            grad_positions=grad_positions, grad_cell=grad_cell,
+        )
+
+    def _time_search(self, device, pos: Tensor, cell: Tensor, pbc: Tensor,
+                     batch_ptr: Tensor) -> float:
+        """Wall time of a warm fresh search of these inputs (after one that
+        warms up the search's plan for this shape); its outputs are dropped."""
+        with torch.no_grad():
+            self._search(pos, cell, pbc, batch_ptr, pos, cell)
+            torch.cuda.synchronize(device)
+            t0 = time.perf_counter()
+            self._search(pos, cell, pbc, batch_ptr, pos, cell)
+            torch.cuda.synchronize(device)
+        return time.perf_counter() - t0
 
     def _build(self, lib, key, pos: Tensor, cell: Tensor, pbc: Tensor, batch_ptr: Tensor) -> None:
         build_cutoff = self.cutoff + self.skin
