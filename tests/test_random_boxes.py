@@ -1,4 +1,4 @@
-"""GPU: seeded random single boxes against the CPU oracle, searched repeatedly.
+"""Seeded random single boxes against the CPU oracle, searched repeatedly on the GPU.
 
 Each seed draws one structure large enough for a bin grid: a skewed cell
 of 22 to 50 Angstrom edges at 70 to 110 degrees, periodic along every axis
@@ -10,7 +10,7 @@ plan hint, the periodic fast prologue with its grid barrier and set-up
 memo, the speculative emit) and a repeat with the atoms moved.  Every
 result's (i, j, S) multiset must equal the oracle's bit for bit, with d
 and D within 1e-5 relative (float32) or 1e-12 (float64) of the float64
-formula.
+formula.  Eight of the boxes also go through the host provider (CPU suite).
 """
 
 from __future__ import annotations
@@ -21,7 +21,6 @@ import pytest
 from tests.test_random_batches import check
 from tonari_amd._torch_frontend import _speculation
 
-pytestmark = pytest.mark.gpu
 
 # plan bit of a fully periodic structure searched with a cell list: its
 # repeats take the periodic fast prologue
@@ -62,6 +61,7 @@ def random_box(seed: int) -> dict:
     }
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("seed", range(24))
 def test_random_box_repeats(seed):
     cfg = random_box(seed)
@@ -74,3 +74,8 @@ def test_random_box_repeats(seed):
     (entry,) = _speculation().values()
     if cfg["algorithm"] == "cell_list" and cfg["pbc"].all():
         assert entry[1] & PLAN_PERIODIC_GRID, "the repeats did not take the periodic fast prologue"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_box_host_provider(seed):
+    check(random_box(seed), "cpu")

@@ -1,4 +1,4 @@
-"""GPU: seeded random batches of open molecules, searched repeatedly.
+"""Seeded random batches of open molecules, searched repeatedly on the GPU.
 
 Each seed draws 1 to 400 non-periodic structures (zero cell, no periodic
 axis) of 0 to 200 atoms as Gaussian clouds of random width, now and then
@@ -10,6 +10,7 @@ shape: first, repeated (the molecule plan hint and the molecules-only set-up
 of batches up to 4,096 structures) and repeated with moved atoms.  Every
 result's (i, j, S) multiset must equal the oracle's bit for bit, with d and
 D within 1e-5 relative (float32) or 1e-12 (float64) of the float64 formula.
+Six of the batches also go through the host provider (CPU suite).
 """
 
 from __future__ import annotations
@@ -19,7 +20,6 @@ import pytest
 
 from tests.test_random_batches import check
 
-pytestmark = pytest.mark.gpu
 
 
 def random_molecules(seed: int) -> dict:
@@ -47,6 +47,7 @@ def random_molecules(seed: int) -> dict:
     }
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("block", range(6))
 def test_random_molecule_batches(block):
     for seed in range(10 * block, 10 * block + 10):
@@ -57,3 +58,8 @@ def test_random_molecule_batches(block):
             cfg["positions"].dtype))
         for case in (cfg, cfg, moved):
             check(case, "cuda:0")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_molecule_batches_host_provider(seed):
+    check(random_molecules(seed), "cpu")
