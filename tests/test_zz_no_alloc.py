@@ -5,7 +5,8 @@ scratch array instead of a caller workspace, with outputs of a capacity the
 caller chooses.  Calls in a row share that array: the second, smaller call
 must not see the first one's bins, counts or tickets.  Both entry points are
 called through the C ABI; the (i, j, S) rows must be the same multiset and
-every row's d and D bit-identical.
+every row's d and D bit-identical, on the benchmark configurations and on
+seeded random batches.
 """
 
 from __future__ import annotations
@@ -119,6 +120,24 @@ def test_static_scratch_matches_workspace_entry_points():
     # a batch after them (brute force and half list), then a sorted cell-list batch
     _case(lib, "C2 subset", dict(W.c2(n_structures=48), half_list=True), slack=5)
     _case(lib, "C5 subset", W.c5(n_structures=3, n_min=2000, n_max=4000), slack=0)
+
+
+def test_static_scratch_on_random_batches():
+    # the seeded random batches of tests/test_random_batches.py (explicit
+    # cell_list requests the oracle refuses left out), one after another on
+    # the shared scratch: large and small, periodic and open, both dtypes
+    from tests.test_random_batches import random_batch
+    from tests.test_random_reuse import _usable
+
+    lib = ext.load_torch_hip()
+    done = 0
+    for seed in range(60):
+        cfg = random_batch(seed)
+        if not _usable(cfg):
+            continue
+        _case(lib, f"random batch {seed}", cfg, slack=7)
+        done += 1
+    assert done > 40
 
 
 def test_static_scratch_reports_a_count_beyond_capacity():
