@@ -5,7 +5,7 @@ D / d / S row-aligned to its columns, as the reference's PyTorch Geometric
 example builds it (``README.md:81-99``), for brute-force and cell-list plans,
 first and repeated calls (the repeated call writes into a buffer sized
 before E is known), a pair count that outgrows the previous call's buffer,
-and gradients of the edge vectors.
+gradients of the edge vectors, and seeded random batches with every option.
 """
 
 from __future__ import annotations
@@ -105,3 +105,26 @@ def test_from_batch_follows_the_readme_example():
     torch.cuda.synchronize()
     assert g.edge_index.shape == pairs.T.shape
     _check(dict(cfg, algorithm="auto"), g)
+
+
+@pytest.mark.parametrize("block", range(4))
+def test_graph_on_random_batches(block):
+    # the seeded random batches of tests/test_random_batches.py, each built
+    # twice (first and repeated call of the shape), with every option of
+    # the search, against the oracle
+    from tests.test_random_batches import random_batch
+    from tests.test_random_reuse import _usable
+
+    for seed in range(15 * block, 15 * block + 15):
+        cfg = random_batch(seed)
+        if not _usable(cfg):
+            continue
+        print(f"[graph] random batch {seed}", flush=True)
+        t = _t(cfg)
+        options = {k: cfg[k] for k in ("half_list", "include_self", "sorted")}
+        for _ in range(2):
+            g = neighbor_graph(t["positions"], t["cell"], t["pbc"], cfg["cutoff"],
+                               t["batch_ptr"], lengths=True, shifts=True,
+                               algorithm=cfg["algorithm"], **options)
+            torch.cuda.synchronize()
+            _check(cfg, g)
